@@ -1,0 +1,569 @@
+// Split-K paged attention for gfx950 (GQA, head_dim 128).
+//
+// Three kernels:
+//   plan_kernel   one work-group; turns (cu_seqlens_q, seqlens_kv) into a flat
+//                 list of segments (request, kv head, head block, query
+//                 block) with their key tiles (16 keys each), then cuts the
+//                 concatenated tile list into equal contiguous ranges, one
+//                 per wave (balanced split-K: every wave streams the same
+//                 number of KV bytes whatever the context-length mix).
+//   gqa_attn      one wave per range.  Per 16-key tile: K rows go straight
+//                 from HBM into MFMA A-fragments (S^T = K Q^T on
+//                 v_mfma_f32_16x16x16_bf16, the 16 query rows of a segment
+//                 are the N dimension), online softmax on the S^T fragment
+//                 (row max over the 4 lane groups with two xor shuffles),
+//                 V is transposed through LDS and O^T += V^T P^T runs on the
+//                 same MFMA with P^T taken directly from the S^T registers.
+//                 A wave that covers a whole segment writes bf16 output;
+//                 otherwise it writes an fp32 partial (O, m, l).
+//   gqa_merge     log-sum-exp merge of the partials of each split segment.
+#include <math.h>
+
+#include "common.h"
+
+namespace {
+
+using aia::float4_t;
+using aia::short4_t;
+
+constexpr int kHeadDim = 128;
+constexpr int kTile = 16;         // keys per MFMA tile
+constexpr int kRows = 16;         // query rows per segment (MFMA N)
+constexpr int kVtStride = 20;     // LDS row stride (elements) of the V^T tile
+constexpr int kMaxBatch = 8192;   // planner keeps the request offsets in LDS
+constexpr int kDefaultWaves = 2048;
+constexpr int kMaxWaves = 16384;
+constexpr int kPlanThreads = 1024;
+
+struct Geometry {
+  int32_t hkv, group, hb, nhb, qb;
+};
+
+Geometry geometry(int32_t hq, int32_t hkv) {
+  Geometry g;
+  g.hkv = hkv;
+  g.group = hq / hkv;
+  g.hb = g.group < kRows ? g.group : kRows;            // heads per segment
+  g.nhb = (g.group + g.hb - 1) / g.hb;                 // head blocks per kv head
+  g.qb = kRows / g.hb;                                  // query tokens per segment
+  return g;
+}
+
+// Workspace layout (all offsets 256-byte aligned).
+struct Layout {
+  int64_t hdr, seg, wave, part_ml, part_o, total;
+  int64_t seg_cap, part_cap;
+};
+
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int32_t waves) {
+  Layout L;
+  L.seg_cap = (int64_t)g.hkv * g.nhb * (batch + (tokens + g.qb - 1) / g.qb);
+  L.part_cap = L.seg_cap + waves;
+  int64_t off = 0;
+  L.hdr = off;      off = align256(off + 64 * 4);
+  L.seg = off;      off = align256(off + (L.seg_cap + 1) * 8 * 4);
+  L.wave = off;     off = align256(off + (int64_t)waves * 16);
+  L.part_ml = off;  off = align256(off + L.part_cap * kRows * 8);
+  L.part_o = off;   off = align256(off + L.part_cap * kRows * (int64_t)dv * 4);
+  L.total = off;
+  return L;
+}
+
+int32_t resolve_waves(int32_t w) {
+  if (w <= 0) w = kDefaultWaves;
+  if (w > kMaxWaves) w = kMaxWaves;
+  return (w + 3) & ~3;
+}
+
+// ---------------------------------------------------------------- planner
+
+// Exclusive scan of one value per thread across the 1024-thread block;
+// returns the exclusive prefix and writes the block total to *total.
+__device__ int block_exclusive_scan(int v, int* wave_sums, int* total) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    int y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) wave_sums[wid] = x;
+  __syncthreads();
+  if (wid == 0) {
+    int s = lane < kPlanThreads / 64 ? wave_sums[lane] : 0;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      int y = __shfl_up(s, d);
+      if (lane >= d) s += y;
+    }
+    if (lane < kPlanThreads / 64) wave_sums[lane] = s;  // inclusive
+  }
+  __syncthreads();
+  const int before = wid ? wave_sums[wid - 1] : 0;
+  *total = wave_sums[kPlanThreads / 64 - 1];
+  __syncthreads();
+  return before + x - v;
+}
+
+// Segment record, 8 ints: b, kvh | hb << 16, first query token (global row),
+// query tokens, lim_base = Lk - Lq + q0 (last key of the block's first
+// row), tile_begin, tile_end, part_base.
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ kvlen,
+    int32_t batch, Geometry g, int32_t waves,
+    int32_t* __restrict__ hdr, int32_t* __restrict__ seg, int4* __restrict__ wave_info) {
+  __shared__ int req_off[kMaxBatch + 1];
+  __shared__ int wave_sums[kPlanThreads / 64];
+  const int tid = threadIdx.x;
+  const int per_req = g.hkv * g.nhb;
+
+  // 1) segments per request -> request offsets (LDS)
+  int carry = 0;
+  for (int base = 0; base < batch; base += kPlanThreads) {
+    const int b = base + tid;
+    int cnt = 0;
+    if (b < batch) {
+      const int lq = cu_q[b + 1] - cu_q[b];
+      cnt = lq > 0 ? ((lq + g.qb - 1) / g.qb) * per_req : 0;
+    }
+    int tot;
+    const int ex = block_exclusive_scan(cnt, wave_sums, &tot);
+    if (b < batch) req_off[b] = carry + ex;
+    carry += tot;
+  }
+  if (tid == 0) req_off[batch] = carry;
+  __syncthreads();
+  const int nseg = req_off[batch];
+
+  // 2) segment records and their key tiles
+  carry = 0;
+  for (int base = 0; base < nseg; base += kPlanThreads) {
+    const int s = base + tid;
+    int ntiles = 0;
+    int rec[6];
+    if (s < nseg) {
+      int lo = 0, hi = batch - 1;  // last b with req_off[b] <= s
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (req_off[mid] <= s) lo = mid; else hi = mid - 1;
+      }
+      const int b = lo;
+      const int local = s - req_off[b];
+      const int hb = local % g.nhb;
+      const int kvh = (local / g.nhb) % g.hkv;
+      const int qblk = local / per_req;
+      const int q_begin = cu_q[b];
+      const int lq = cu_q[b + 1] - q_begin;
+      const int lk = kvlen[b];
+      const int q0 = qblk * g.qb;
+      const int nq = min(g.qb, lq - q0);
+      const int lim_base = lk - lq + q0;
+      const int visible = max(0, min(lk, lim_base + nq));
+      ntiles = (visible + kTile - 1) / kTile;
+      rec[0] = b; rec[1] = kvh | (hb << 16); rec[2] = q_begin + q0; rec[3] = nq;
+      rec[4] = lim_base; rec[5] = ntiles;
+    }
+    int tot;
+    const int ex = block_exclusive_scan(ntiles, wave_sums, &tot);
+    if (s < nseg) {
+      int* r = seg + (int64_t)s * 8;
+      r[0] = rec[0]; r[1] = rec[1]; r[2] = rec[2]; r[3] = rec[3]; r[4] = rec[4];
+      r[5] = carry + ex; r[6] = carry + ex + ntiles;
+    }
+    carry += tot;
+  }
+  const int total_tiles = carry;
+  const int tpw = max(1, (total_tiles + waves - 1) / waves);
+  __syncthreads();
+
+  // 3) partial slots: a segment split over k waves owns k consecutive slots
+  carry = 0;
+  for (int base = 0; base < nseg; base += kPlanThreads) {
+    const int s = base + tid;
+    int np = 0;
+    if (s < nseg) {
+      const int tb = seg[(int64_t)s * 8 + 5], te = seg[(int64_t)s * 8 + 6];
+      np = te > tb ? (te - 1) / tpw - tb / tpw + 1 : 0;
+    }
+    int tot;
+    const int ex = block_exclusive_scan(np, wave_sums, &tot);
+    if (s < nseg) seg[(int64_t)s * 8 + 7] = carry + ex;
+    carry += tot;
+  }
+  if (tid == 0) {
+    hdr[0] = nseg; hdr[1] = total_tiles; hdr[2] = tpw; hdr[3] = carry; hdr[4] = waves;
+    // sentinel record so readers may look one past the end
+    int* r = seg + (int64_t)nseg * 8;
+    r[0] = 0; r[1] = 0; r[2] = 0; r[3] = 0; r[4] = 0;
+    r[5] = total_tiles; r[6] = total_tiles; r[7] = carry;
+  }
+  __syncthreads();
+
+  // 4) per-wave start: first segment whose tile range contains w * tpw
+  for (int w = tid; w < waves; w += kPlanThreads) {
+    const int t0 = w * tpw;
+    int4 info = make_int4(-1, 0, 0, 0);
+    if (t0 < total_tiles) {
+      int lo = 0, hi = nseg - 1;  // last s with tile_begin <= t0
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (seg[(int64_t)mid * 8 + 5] <= t0) lo = mid; else hi = mid - 1;
+      }
+      info = make_int4(lo, t0, min(total_tiles, t0 + tpw), 0);
+    }
+    wave_info[w] = info;
+  }
+}
+
+// ---------------------------------------------------------------- attention
+
+struct AttnArgs {
+  const uint16_t* q;
+  int64_t q_ts, q_hs;
+  const uint16_t* kc;
+  const uint16_t* vc;
+  const int32_t* bt;
+  int64_t bt_stride;
+  int32_t hkv, group, hb, bs, nb;
+  float scale_log2;
+  const int32_t* hdr;
+  const int32_t* seg;
+  const int4* wave_info;
+  float* part_o;
+  float2* part_ml;
+  uint16_t* out;
+  int64_t o_ts, o_hs;
+  int32_t waves;
+};
+
+__device__ __forceinline__ short4_t as_s4(uint32_t a, uint32_t b) {
+  short4_t r;
+  r[0] = (short)(a & 0xffff); r[1] = (short)(a >> 16);
+  r[2] = (short)(b & 0xffff); r[3] = (short)(b >> 16);
+  return r;
+}
+
+__device__ __forceinline__ uint16_t half_of(uint4 v, int e) {
+  const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+  return (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffff));
+}
+
+__global__ __launch_bounds__(256) void gqa_attn_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t vt_all[4][kHeadDim * kVtStride];
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int w = blockIdx.x * 4 + wid;
+  if (w >= a.waves) return;
+  const int4 wi = a.wave_info[w];
+  if (wi.x < 0) return;
+  uint16_t* vt = vt_all[wid];
+  const int tpw = a.hdr[2];
+  const int n = lane & 15, g = lane >> 4;
+  const int row_elems = a.hkv * kHeadDim;
+
+  int s = wi.x, t = wi.y;
+  const int t_end = wi.z;
+  while (t < t_end) {
+    const int4 r0 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8);
+    const int4 r1 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8 + 4);
+    const int tile_begin = r1.y, tile_end = r1.z;
+    if (tile_end <= t) { ++s; continue; }
+    const int lt0 = t - tile_begin;
+    const int chunk_end = min(t_end, tile_end);
+    const int lt1 = chunk_end - tile_begin;
+
+    const int b = r0.x, kvh = r0.y & 0xffff, hbi = r0.y >> 16;
+    const int qtok0 = r0.z, nq = r0.w, lim_base = r1.x;
+    const int qi = n / a.hb, hh = n - qi * a.hb;
+    const bool rv = qi < nq && hbi * a.hb + hh < a.group;
+    const int head = kvh * a.group + hbi * a.hb + hh;
+    const int lim = rv ? lim_base + qi : -1;
+    const int visible = max(0, lim_base + nq);
+
+    uint4 qf[4];
+    if (rv) {
+      const uint4* qp = reinterpret_cast<const uint4*>(
+          a.q + (int64_t)(qtok0 + qi) * a.q_ts + (int64_t)head * a.q_hs);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qf[j] = qp[4 * j + g];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qf[j] = make_uint4(0, 0, 0, 0);
+    }
+
+    // Block ids of up to 64 consecutive logical blocks live one per lane.
+    const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
+    const int nblk_vis = (visible + a.bs - 1) / a.bs;
+    int blk_base = (lt0 * kTile) / a.bs;
+    int btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
+
+    float4_t o[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    float m = -1e30f, lsum = 0.f;
+
+    auto load = [&](int lt, uint4 (&kk)[4], uint4 (&vv)[4]) {
+      const int last = min(lt * kTile + kTile - 1, visible - 1);
+      if (last / a.bs - blk_base >= 64) {
+        blk_base = (lt * kTile) / a.bs;
+        btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
+      }
+      const int tok = min(lt * kTile + n, visible - 1);
+      const int bi = tok / a.bs;
+      // block ids outside the pool are clamped so a bad table cannot fault
+      const int blk = min(max(__shfl(btv, bi - blk_base), 0), a.nb - 1);
+      const int off = tok - bi * a.bs;
+      const int64_t base = ((int64_t)blk * a.bs + off) * row_elems + (int64_t)kvh * kHeadDim;
+      const uint4* kp = reinterpret_cast<const uint4*>(a.kc + base);
+      const uint4* vp = reinterpret_cast<const uint4*>(a.vc + base);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) kk[j] = kp[4 * j + g];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vv[j] = vp[4 * j + g];
+    };
+
+    auto compute = [&](int lt, const uint4 (&kk)[4], const uint4 (&vv)[4]) {
+      float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s4(kk[j].x, kk[j].y),
+                                                        as_s4(qf[j].x, qf[j].y), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s4(kk[j].z, kk[j].w),
+                                                        as_s4(qf[j].z, qf[j].w), acc, 0, 0, 0);
+      }
+      // V tile -> LDS, transposed: vt[d][key]
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vt[(32 * j + 8 * g + e) * kVtStride + n] = half_of(vv[j], e);
+      }
+      const int tb = lt * kTile + 4 * g;
+      float sv[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sv[v] = (tb + v <= lim) ? acc[v] * a.scale_log2 : -INFINITY;
+      float tmax = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const float mnew = fmaxf(m, tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+      float p[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) p[v] = __builtin_amdgcn_exp2f(sv[v] - mnew);
+      lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+      m = mnew;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
+      const short4_t pb = as_s4(aia::pack_bf16x2(p[0], p[1]), aia::pack_bf16x2(p[2], p[3]));
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const short4_t va = *reinterpret_cast<const short4_t*>(vt + (16 * dt + n) * kVtStride + 4 * g);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[dt], 0, 0, 0);
+      }
+      __builtin_amdgcn_wave_barrier();
+    };
+
+    uint4 ka[4], va_[4], kb[4], vb[4];
+    int lt = lt0;
+    load(lt, ka, va_);
+    while (true) {
+      bool more = lt + 1 < lt1;
+      if (more) load(lt + 1, kb, vb);
+      compute(lt, ka, va_);
+      if (!more) break;
+      ++lt;
+      more = lt + 1 < lt1;
+      if (more) load(lt + 1, ka, va_);
+      compute(lt, kb, vb);
+      if (!more) break;
+      ++lt;
+    }
+
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    const int first_wave = tile_begin / tpw;
+    const int nparts = (tile_end - 1) / tpw - first_wave + 1;
+    if (nparts == 1) {
+      if (rv) {
+        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+        uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          uint2 wv;
+          wv.x = aia::pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
+          wv.y = aia::pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
+          *reinterpret_cast<uint2*>(op + 16 * dt + 4 * g) = wv;
+        }
+      }
+    } else {
+      const int part = r1.w + (w - first_wave);
+      if (rv) {
+        float* pp = a.part_o + ((int64_t)part * kRows + n) * kHeadDim;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+          *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * g) = o[dt];
+        if (g == 0) a.part_ml[(int64_t)part * kRows + n] = make_float2(m, lsum);
+      }
+    }
+    t = chunk_end;
+    ++s;
+  }
+}
+
+struct MergeArgs {
+  const int32_t* hdr;
+  const int32_t* seg;
+  const float* part_o;
+  const float2* part_ml;
+  uint16_t* out;
+  int64_t o_ts, o_hs;
+  int32_t group, hb;
+};
+
+// One work-group per split segment: thread (row, 8 dims).
+__global__ __launch_bounds__(256) void gqa_merge_kernel(MergeArgs a) {
+  const int nseg = a.hdr[0], tpw = a.hdr[2];
+  const int n = threadIdx.x >> 4;
+  const int c = (threadIdx.x & 15) * 8;
+  for (int s = blockIdx.x; s < nseg; s += gridDim.x) {
+    const int4 r0 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8);
+    const int4 r1 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8 + 4);
+    const int tb = r1.y, te = r1.z;
+    const int np = te > tb ? (te - 1) / tpw - tb / tpw + 1 : 0;
+    if (np == 1) continue;
+    const int kvh = r0.y & 0xffff, hbi = r0.y >> 16, qtok0 = r0.z, nq = r0.w;
+    const int qi = n / a.hb, hh = n - qi * a.hb;
+    if (!(qi < nq && hbi * a.hb + hh < a.group)) continue;
+    const int head = kvh * a.group + hbi * a.hb + hh;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float lsum = 0.f;
+    if (np > 1) {
+      const int pb = r1.w;
+      float mx = -1e30f;
+      for (int k = 0; k < np; ++k) mx = fmaxf(mx, a.part_ml[(int64_t)(pb + k) * kRows + n].x);
+      for (int k = 0; k < np; ++k) {
+        const float2 ml = a.part_ml[(int64_t)(pb + k) * kRows + n];
+        const float wgt = __builtin_amdgcn_exp2f(ml.x - mx);
+        lsum += ml.y * wgt;
+        const float4* src = reinterpret_cast<const float4*>(
+            a.part_o + ((int64_t)(pb + k) * kRows + n) * kHeadDim + c);
+        const float4 x0 = src[0], x1 = src[1];
+        acc[0] += x0.x * wgt; acc[1] += x0.y * wgt; acc[2] += x0.z * wgt; acc[3] += x0.w * wgt;
+        acc[4] += x1.x * wgt; acc[5] += x1.y * wgt; acc[6] += x1.z * wgt; acc[7] += x1.w * wgt;
+      }
+    }
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    uint4 wv;
+    wv.x = aia::pack_bf16x2(acc[0] * inv, acc[1] * inv);
+    wv.y = aia::pack_bf16x2(acc[2] * inv, acc[3] * inv);
+    wv.z = aia::pack_bf16x2(acc[4] * inv, acc[5] * inv);
+    wv.w = aia::pack_bf16x2(acc[6] * inv, acc[7] * inv);
+    *reinterpret_cast<uint4*>(a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs + c) = wv;
+  }
+}
+
+int check_heads(const char* fn, int32_t hq, int32_t hkv) {
+  if (hq <= 0 || hkv <= 0 || hq % hkv != 0)
+    return aia::fail(AIA_ERR_INVALID, "%s: num_q_heads %d must be a positive multiple of num_kv_heads %d",
+                     fn, hq, hkv);
+  const int32_t group = hq / hkv;
+  if (group > kRows && group % kRows != 0)
+    return aia::fail(AIA_ERR_UNSUPPORTED, "%s: query group %d > 16 must be a multiple of 16", fn, group);
+  return AIA_OK;
+}
+
+}  // namespace
+
+extern "C" int aia_attn_workspace_bytes(int32_t batch, int32_t num_tokens, int32_t num_q_heads,
+                                        int32_t num_kv_heads, int32_t head_dim_v, int64_t* bytes) {
+  if (int rc = check_heads("aia_attn_workspace_bytes", num_q_heads, num_kv_heads)) return rc;
+  if (batch < 0 || num_tokens < 0 || head_dim_v <= 0 || !bytes)
+    return aia::fail(AIA_ERR_INVALID, "aia_attn_workspace_bytes: bad arguments");
+  const Geometry g = geometry(num_q_heads, num_kv_heads);
+  *bytes = layout(batch, num_tokens, g, head_dim_v, kMaxWaves).total;
+  return AIA_OK;
+}
+
+extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv, int32_t batch,
+                             int32_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                             int32_t head_dim_v, int32_t num_waves, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
+  using namespace aia;
+  if (int rc = check_heads("aia_attn_plan", num_q_heads, num_kv_heads)) return rc;
+  if (batch < 0 || batch > kMaxBatch)
+    return fail(AIA_ERR_CAPACITY, "aia_attn_plan: batch %d exceeds planner limit %d", batch, kMaxBatch);
+  if (batch > 0 && (!cu_seqlens_q || !seqlens_kv))
+    return fail(AIA_ERR_INVALID, "aia_attn_plan: null metadata");
+  if (!workspace) return fail(AIA_ERR_INVALID, "aia_attn_plan: null workspace");
+  const Geometry g = geometry(num_q_heads, num_kv_heads);
+  const int32_t waves = resolve_waves(num_waves);
+  const Layout L = layout(batch, num_tokens, g, head_dim_v, waves);
+  if (workspace_bytes < L.total)
+    return fail(AIA_ERR_CAPACITY, "aia_attn_plan: workspace %lld bytes < %lld needed",
+                (long long)workspace_bytes, (long long)L.total);
+  char* ws = static_cast<char*>(workspace);
+  plan_kernel<<<1, kPlanThreads, 0, (hipStream_t)stream>>>(
+      cu_seqlens_q, seqlens_kv, batch, g, waves, reinterpret_cast<int32_t*>(ws + L.hdr),
+      reinterpret_cast<int32_t*>(ws + L.seg), reinterpret_cast<int4*>(ws + L.wave));
+  return check_hip(hipGetLastError(), "aia_attn_plan launch");
+}
+
+extern "C" int aia_paged_attention_gqa(
+    const void* query, int64_t q_token_stride, int64_t q_head_stride, const void* key_cache,
+    const void* value_cache, const int32_t* block_table, int32_t block_table_stride,
+    const int32_t* cu_seqlens_q, const int32_t* seqlens_kv, int32_t batch, int32_t num_tokens,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+    int32_t num_blocks, float scale, void* out, int64_t out_token_stride, int64_t out_head_stride,
+    int32_t num_waves, void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace aia;
+  (void)cu_seqlens_q; (void)seqlens_kv;
+  if (int rc = check_heads("aia_paged_attention_gqa", num_q_heads, num_kv_heads)) return rc;
+  if (head_dim != kHeadDim)
+    return fail(AIA_ERR_UNSUPPORTED, "aia_paged_attention_gqa: head_dim %d (only 128)", head_dim);
+  if (block_size <= 0 || num_blocks <= 0)
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: block_size %d / num_blocks %d",
+                block_size, num_blocks);
+  if (!query || !key_cache || !value_cache || !block_table || !out || !workspace)
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: null pointer argument");
+  if (q_token_stride % 8 || q_head_stride % 8 || out_token_stride % 4 || out_head_stride % 8 ||
+      ((uintptr_t)query & 15) || ((uintptr_t)key_cache & 15) || ((uintptr_t)value_cache & 15) ||
+      ((uintptr_t)out & 15))
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: query/out/cache must be 16-byte aligned "
+                "with strides a multiple of 8 elements");
+  if (num_tokens == 0 || batch == 0) return AIA_OK;
+  const Geometry g = geometry(num_q_heads, num_kv_heads);
+  const int32_t waves = resolve_waves(num_waves);
+  const Layout L = layout(batch, num_tokens, g, head_dim, waves);
+  if (workspace_bytes < L.total)
+    return fail(AIA_ERR_CAPACITY, "aia_paged_attention_gqa: workspace %lld bytes < %lld needed",
+                (long long)workspace_bytes, (long long)L.total);
+  char* ws = static_cast<char*>(workspace);
+  AttnArgs a;
+  a.q = static_cast<const uint16_t*>(query);
+  a.q_ts = q_token_stride; a.q_hs = q_head_stride;
+  a.kc = static_cast<const uint16_t*>(key_cache);
+  a.vc = static_cast<const uint16_t*>(value_cache);
+  a.bt = block_table; a.bt_stride = block_table_stride;
+  a.hkv = g.hkv; a.group = g.group; a.hb = g.hb; a.bs = block_size; a.nb = num_blocks;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
+  a.seg = reinterpret_cast<const int32_t*>(ws + L.seg);
+  a.wave_info = reinterpret_cast<const int4*>(ws + L.wave);
+  a.part_o = reinterpret_cast<float*>(ws + L.part_o);
+  a.part_ml = reinterpret_cast<float2*>(ws + L.part_ml);
+  a.out = static_cast<uint16_t*>(out);
+  a.o_ts = out_token_stride; a.o_hs = out_head_stride;
+  a.waves = waves;
+  hipStream_t s = (hipStream_t)stream;
+  gqa_attn_kernel<<<waves / 4, 256, 0, s>>>(a);
+  if (int rc = check_hip(hipGetLastError(), "gqa_attn_kernel launch")) return rc;
+  MergeArgs mg;
+  mg.hdr = a.hdr; mg.seg = a.seg; mg.part_o = a.part_o; mg.part_ml = a.part_ml;
+  mg.out = a.out; mg.o_ts = a.o_ts; mg.o_hs = a.o_hs; mg.group = g.group; mg.hb = g.hb;
+  int64_t mgrid = L.seg_cap < 4096 ? L.seg_cap : 4096;
+  if (mgrid < 1) mgrid = 1;
+  gqa_merge_kernel<<<(unsigned)mgrid, 256, 0, s>>>(mg);
+  return check_hip(hipGetLastError(), "gqa_merge_kernel launch");
+}

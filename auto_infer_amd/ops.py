@@ -1,0 +1,198 @@
+"""Torch-facing wrappers of the gfx950 kernels.
+
+PyTorch owns every buffer (caches, metadata, workspace); these functions
+check shapes/dtypes/devices on the host, then hand raw pointers and the
+current HIP stream to the C ABI.  Nothing here computes on the CPU.
+"""
+import ctypes
+
+import torch
+
+from auto_infer_amd import _native
+
+_BF16 = torch.bfloat16
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _require(cond, msg):
+    if not cond:
+        raise ValueError(msg)
+
+
+def _check_device_tensor(t, name, dtype=None):
+    _require(isinstance(t, torch.Tensor), f"{name} must be a tensor")
+    _require(t.is_cuda, f"{name} must be on the GPU (no CPU fallback)")
+    if dtype is not None:
+        _require(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+
+
+def _row_stride(t, name):
+    """Token stride of a (T, heads, dim) tensor whose (heads, dim) part is
+    one contiguous row."""
+    _require(t.dim() == 3, f"{name} must be (tokens, heads, dim)")
+    _require(t.stride(2) == 1 and t.stride(1) == t.shape[2],
+             f"{name} rows (heads, dim) must be contiguous")
+    return t.stride(0)
+
+
+# ---------------------------------------------------------------- KV write
+
+def write_kv(key, value, key_cache, value_cache, slot_mapping):
+    """Scatter this step's K/V into the paged cache by slot index.
+
+    Same call shape and semantics as the reference's ``write_kv``
+    (auto_infer/layers/attention/base.py:41-45):
+    ``key_cache.view(-1, Hkv, D)[slot_mapping[t]] = key[t]`` and the same for
+    ``value``.  ``value``/``value_cache`` may be None to write a single
+    cache (absorbed MLA).  Slots outside the cache are skipped.
+    """
+    _check_device_tensor(key, "key", _BF16)
+    _check_device_tensor(key_cache, "key_cache", _BF16)
+    _check_device_tensor(slot_mapping, "slot_mapping", torch.int32)
+    _require(key_cache.is_contiguous(), "key_cache must be contiguous")
+    _require(slot_mapping.dim() == 1 and slot_mapping.is_contiguous(),
+             "slot_mapping must be a contiguous 1-D tensor")
+    T = key.shape[0]
+    _require(slot_mapping.shape[0] == T, "slot_mapping length must equal the token count")
+    krow = key.shape[1] * key.shape[2]
+    _require(key_cache.numel() % krow == 0 and key_cache.shape[-1] * key_cache.shape[-2] == krow,
+             "key rows do not match the key cache's (heads, dim)")
+    num_slots = key_cache.numel() // krow
+    kts = _row_stride(key, "key")
+    if value is not None:
+        _check_device_tensor(value, "value", _BF16)
+        _check_device_tensor(value_cache, "value_cache", _BF16)
+        _require(value_cache.is_contiguous(), "value_cache must be contiguous")
+        _require(value.shape[0] == T, "value must have as many tokens as key")
+        vrow = value.shape[1] * value.shape[2]
+        _require(value_cache.numel() // vrow == num_slots and
+                 value_cache.shape[-1] * value_cache.shape[-2] == vrow,
+                 "value rows do not match the value cache")
+        vts = _row_stride(value, "value")
+    else:
+        _require(value_cache is None, "value_cache given without value")
+        vrow, vts = 0, 0
+    _native.call("aia_kv_write", _ptr(key), kts, _ptr(value), vts, _ptr(key_cache),
+                 _ptr(value_cache), _ptr(slot_mapping), T, krow, vrow, num_slots,
+                 _stream(key.device))
+
+
+# ---------------------------------------------------------------- attention
+
+class Workspace:
+    """Grow-only device scratch buffer (one per device), owned by torch."""
+
+    def __init__(self):
+        self._buf = {}
+
+    def get(self, device, nbytes):
+        dev = torch.device(device)
+        buf = self._buf.get(dev)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+            self._buf[dev] = buf
+        return buf
+
+
+DEFAULT_WORKSPACE = Workspace()
+
+
+def workspace_bytes(batch, num_tokens, num_q_heads, num_kv_heads, head_dim_v):
+    out = ctypes.c_int64(0)
+    _native.call("aia_attn_workspace_bytes", batch, num_tokens, num_q_heads, num_kv_heads,
+                 head_dim_v, ctypes.byref(out))
+    return out.value
+
+
+class AttentionPlan:
+    """Device metadata + split-K work plan of one step.
+
+    Built once per step (all layers share it): ``cu_seqlens_q`` is the
+    reference's cumulative query-length list with a leading 0 (B + 1
+    entries), ``seqlens_kv`` the per-request KV lengths
+    (forward_context.py:14-15), both int32 on the device.  The planner runs
+    on the GPU, so device-produced metadata (the packing kernel) needs no
+    host round trip.
+    """
+
+    def __init__(self, block_table, cu_seqlens_q, seqlens_kv, num_tokens, num_q_heads,
+                 num_kv_heads, head_dim_v, num_waves=0, workspace=None):
+        _check_device_tensor(block_table, "block_table", torch.int32)
+        _check_device_tensor(cu_seqlens_q, "cu_seqlens_q", torch.int32)
+        _check_device_tensor(seqlens_kv, "seqlens_kv", torch.int32)
+        _require(block_table.dim() == 2 and block_table.stride(1) == 1,
+                 "block_table must be (batch, max_blocks) with unit column stride")
+        batch = seqlens_kv.shape[0]
+        _require(cu_seqlens_q.shape[0] == batch + 1, "cu_seqlens_q must have batch + 1 entries")
+        _require(block_table.shape[0] >= batch, "block_table has fewer rows than requests")
+        _require(cu_seqlens_q.is_contiguous() and seqlens_kv.is_contiguous(),
+                 "metadata tensors must be contiguous")
+        self.block_table = block_table
+        self.cu_seqlens_q = cu_seqlens_q
+        self.seqlens_kv = seqlens_kv
+        self.batch = batch
+        self.num_tokens = int(num_tokens)
+        self.num_q_heads = num_q_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim_v = head_dim_v
+        self.num_waves = num_waves
+        nbytes = workspace_bytes(batch, self.num_tokens, num_q_heads, num_kv_heads, head_dim_v)
+        if workspace is None:
+            workspace = torch.empty(nbytes, dtype=torch.uint8, device=block_table.device)
+        _require(workspace.numel() >= nbytes, "attention workspace too small")
+        self.workspace = workspace
+        _native.call("aia_attn_plan", _ptr(cu_seqlens_q), _ptr(seqlens_kv), batch,
+                     self.num_tokens, num_q_heads, num_kv_heads, head_dim_v, num_waves,
+                     _ptr(workspace), workspace.numel(), _stream(block_table.device))
+
+    @classmethod
+    def from_lists(cls, block_table, cu_seqlens_q, seqlens_kv, num_q_heads, num_kv_heads,
+                   head_dim_v, **kw):
+        """From the reference's host lists (cumulative ends without the
+        leading 0, per-request KV lengths)."""
+        dev = block_table.device
+        bs = kw.pop("block_size", None)
+        if bs is not None and len(seqlens_kv):
+            _require(block_table.shape[1] * bs >= max(seqlens_kv),
+                     "block_table has fewer columns than the longest context needs")
+        cu = torch.tensor([0, *cu_seqlens_q], dtype=torch.int32).to(dev, non_blocking=True)
+        kv = torch.tensor(list(seqlens_kv), dtype=torch.int32).to(dev, non_blocking=True)
+        total = cu_seqlens_q[-1] if len(cu_seqlens_q) else 0
+        return cls(block_table, cu, kv, total, num_q_heads, num_kv_heads, head_dim_v, **kw)
+
+
+def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None):
+    """Paged GQA attention (reference base.py:48-61 FIA semantics).
+
+    query (T, Hq, 128) bf16; key/value caches (NB, bs, Hkv, 128) bf16
+    contiguous; ``plan`` an ``AttentionPlan`` of this step.  Returns
+    (T, Hq, 128) bf16.
+    """
+    _check_device_tensor(query, "query", _BF16)
+    _check_device_tensor(key_cache, "key_cache", _BF16)
+    _check_device_tensor(value_cache, "value_cache", _BF16)
+    _require(query.dim() == 3 and query.stride(2) == 1, "query must be (T, Hq, D), D contiguous")
+    T, hq, d = query.shape
+    _require(key_cache.dim() == 4 and key_cache.is_contiguous() and value_cache.is_contiguous(),
+             "caches must be contiguous (num_blocks, block_size, Hkv, D)")
+    nb, bs, hkv, dk = key_cache.shape
+    _require(tuple(value_cache.shape) == (nb, bs, hkv, dk), "value cache shape differs from key cache")
+    _require(dk == d, "query head_dim differs from the cache's")
+    _require(hq == plan.num_q_heads and hkv == plan.num_kv_heads and T == plan.num_tokens,
+             "plan was made for other head counts / token count")
+    if out is None:
+        out = torch.empty(T, hq, d, dtype=_BF16, device=query.device)
+    _native.call("aia_paged_attention_gqa", _ptr(query), query.stride(0), query.stride(1),
+                 _ptr(key_cache), _ptr(value_cache), _ptr(plan.block_table),
+                 plan.block_table.stride(0), _ptr(plan.cu_seqlens_q), _ptr(plan.seqlens_kv),
+                 plan.batch, T, hq, hkv, d, bs, nb, float(scale), _ptr(out), out.stride(0),
+                 out.stride(1), plan.num_waves, _ptr(plan.workspace), plan.workspace.numel(),
+                 _stream(query.device))
+    return out

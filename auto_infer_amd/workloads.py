@@ -1,0 +1,116 @@
+"""Seeded synthetic steps for the benchmark configurations.
+
+Each generator returns plain tensors shaped like one layer's inputs for one
+step of the reference's paged path: query rows (T, Hq, D), this step's new
+K/V rows, the paged caches (reference layout (NB, bs, Hkv, D) per cache,
+gqa.py:69-74), block tables, the cumulative query lengths / per-request KV
+lengths lists (ForwardContext, forward_context.py:14-15) and the slot
+mapping of the new rows (token_layout.py:1-4).
+"""
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+
+@dataclass
+class GqaStep:
+    q: torch.Tensor
+    k_new: torch.Tensor
+    v_new: torch.Tensor
+    k_cache: torch.Tensor
+    v_cache: torch.Tensor
+    block_table: torch.Tensor      # (B, max_blocks) int32, zero padded
+    cu_seqlens_q: list             # cumulative ends, no leading 0
+    seqlens_kv: list
+    slot_mapping: torch.Tensor     # (T,) int32
+    scale: float
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def num_tokens(self):
+        return self.q.shape[0]
+
+    def kv_bytes_read(self):
+        """Logical KV bytes one attention pass reads (no dedup of shared blocks)."""
+        _, _, hkv, d = self.k_cache.shape
+        return sum(self.seqlens_kv) * 2 * hkv * d * self.k_cache.element_size()
+
+
+def _block_tables(rng, lks, bs, num_blocks, shared_prefix_blocks=0, share_frac=0.0):
+    """Disjoint random block assignment (a permutation of the pool); a
+    fraction of requests may share their first ``shared_prefix_blocks``."""
+    need = [(lk + bs - 1) // bs for lk in lks]
+    perm = rng.permutation(num_blocks)
+    if sum(need) > num_blocks:
+        raise ValueError(f"pool of {num_blocks} blocks cannot hold {sum(need)}")
+    tables, cur = [], 0
+    shared = None
+    for i, n in enumerate(need):
+        row = perm[cur:cur + n].tolist()
+        cur += n
+        if shared_prefix_blocks and rng.random() < share_frac and n > shared_prefix_blocks:
+            if shared is None:
+                shared = row[:shared_prefix_blocks]
+            else:
+                row[:shared_prefix_blocks] = shared
+        tables.append(row)
+    return tables
+
+
+def make_gqa_step(*, lqs, lks, num_q_heads, num_kv_heads, head_dim=128, block_size=128,
+                  num_blocks=None, seed=0, device="cpu", value_scale=1.0,
+                  dtype=torch.bfloat16, shared_prefix_blocks=0, share_frac=0.0,
+                  extra_blocks=0):
+    """One GQA step: request b has lqs[b] query rows at the end of its
+    lks[b]-long context (new K/V rows are the last lqs[b] positions)."""
+    rng = np.random.default_rng(seed)
+    B = len(lks)
+    need = sum((lk + block_size - 1) // block_size for lk in lks)
+    if num_blocks is None:
+        num_blocks = need + extra_blocks
+    tables = _block_tables(rng, lks, block_size, num_blocks, shared_prefix_blocks, share_frac)
+    width = max((len(t) for t in tables), default=0)
+    bt = np.zeros((B, max(width, 1)), dtype=np.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = t
+    gen = torch.Generator().manual_seed(seed)
+    T = sum(lqs)
+    q = (torch.randn(T, num_q_heads, head_dim, generator=gen) * value_scale).to(dtype)
+    k_new = (torch.randn(T, num_kv_heads, head_dim, generator=gen) * value_scale).to(dtype)
+    v_new = (torch.randn(T, num_kv_heads, head_dim, generator=gen) * value_scale).to(dtype)
+    shape = (num_blocks, block_size, num_kv_heads, head_dim)
+    k_cache = (torch.randn(shape, generator=gen) * value_scale).to(dtype)
+    v_cache = (torch.randn(shape, generator=gen) * value_scale).to(dtype)
+    slots, cu, acc = [], [], 0
+    for b, (lq, lk) in enumerate(zip(lqs, lks)):
+        for p in range(lk - lq, lk):
+            slots.append(bt[b, p // block_size] * block_size + p % block_size)
+        acc += lq
+        cu.append(acc)
+    step = GqaStep(q=q, k_new=k_new, v_new=v_new, k_cache=k_cache, v_cache=v_cache,
+                   block_table=torch.from_numpy(bt), cu_seqlens_q=cu, seqlens_kv=list(lks),
+                   slot_mapping=torch.tensor(slots, dtype=torch.int32),
+                   scale=head_dim ** -0.5)
+    return step.to(device) if device != "cpu" else step
+
+
+def _to(self, device):
+    for name in ("q", "k_new", "v_new", "k_cache", "v_cache", "block_table", "slot_mapping"):
+        setattr(self, name, getattr(self, name).to(device))
+    return self
+
+
+GqaStep.to = _to
+
+
+def config1_decode(seed=0, device="cpu", num_blocks=512):
+    """Qwen3-0.6B heads (16 q / 8 kv / 128), bf16, batch 16,
+    query length 1, contexts U[128, 2048], block 128, pool 512 blocks, values
+    N(0,1)/sqrt(128)."""
+    rng = np.random.default_rng(seed)
+    lks = rng.integers(128, 2048, size=16, endpoint=True).tolist()
+    return make_gqa_step(lqs=[1] * 16, lks=lks, num_q_heads=16, num_kv_heads=8,
+                         block_size=128, num_blocks=num_blocks, seed=seed + 1,
+                         device=device, value_scale=1.0 / math.sqrt(128))

@@ -1,0 +1,103 @@
+/* C ABI of the MI355X (gfx950) ragged paged-attention path.
+ *
+ * Every entry point returns an int status (AIA_OK = 0, negative = error; no
+ * exception crosses the ABI) and records a message readable through
+ * aia_last_error() (thread local).  All tensor arguments are DEVICE pointers
+ * owned by the caller; the library never allocates: scratch space is a
+ * caller-provided workspace.  Work is enqueued on the caller's stream
+ * (a hipStream_t passed as void*, NULL = the default stream) and nothing
+ * synchronises the host.  No global mutable state: calls are reentrant and
+ * may come from several host threads on different streams.
+ *
+ * Element type of query/key/value/output tensors is bf16 (passed as raw
+ * 16-bit words).  Indices are int32.
+ */
+#ifndef AUTO_INFER_AMD_H
+#define AUTO_INFER_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AIA_OK 0
+#define AIA_ERR_INVALID (-1)     /* bad argument (maps to ValueError) */
+#define AIA_ERR_HIP (-2)         /* HIP runtime error (RuntimeError) */
+#define AIA_ERR_CAPACITY (-3)    /* exceeds a gear / workspace (ValueError) */
+#define AIA_ERR_UNSUPPORTED (-4) /* shape not supported (NotImplementedError) */
+
+/* Library ABI version (major * 10000 + minor * 100 + patch). */
+int aia_version(void);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* aia_last_error(void);
+
+/* KV slot write.  Replaces torch_npu._npu_reshape_and_cache
+ * (reference auto_infer/layers/attention/base.py:41-45, called from
+ * gqa.py:76-79 and mla.py:111-113):
+ *   key_cache.view(-1, row)[slot_mapping[t]] = key[t]   (and value).
+ * key:   (num_tokens, key_row_elems) rows, token stride key_token_stride
+ *        elements, each row contiguous (heads * head_dim).
+ * value: same with value_row_elems / value_token_stride; may be NULL (with
+ *        value_cache NULL) to write only one cache (absorbed MLA aliases).
+ * caches: contiguous (num_slots, row) = (num_blocks * block_size, heads, dim).
+ * Slots < 0 or >= num_slots are skipped (padding rows). */
+int aia_kv_write(const void* key, int64_t key_token_stride,
+                 const void* value, int64_t value_token_stride,
+                 void* key_cache, void* value_cache,
+                 const int32_t* slot_mapping, int32_t num_tokens,
+                 int32_t key_row_elems, int32_t value_row_elems,
+                 int64_t num_slots, void* stream);
+
+/* Bytes of workspace the attention planner/kernels need for a step of at
+ * most `batch` requests and `num_tokens` query rows.  No reference
+ * counterpart (the vendor op hides its workspace). */
+int aia_attn_workspace_bytes(int32_t batch, int32_t num_tokens,
+                             int32_t num_q_heads, int32_t num_kv_heads,
+                             int32_t head_dim_v, int64_t* bytes);
+
+/* Split-K work plan for one step: reads the device copies of
+ * cu_seqlens_q (batch + 1 entries, leading 0 -- the reference keeps the
+ * cumulative ends as a host list, model_runner.py:137 / ForwardContext
+ * .cu_seqlens_q) and seqlens_kv (batch entries, forward_context.py:15) and
+ * writes a flat list of (request, kv head, query block, key range) work
+ * items into `workspace`.  The plan depends only on step metadata, so one
+ * plan serves every layer of the step.  num_waves = 0 picks the default
+ * grid (the whole chip once). */
+int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
+                  int32_t batch, int32_t num_tokens,
+                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim_v,
+                  int32_t num_waves, void* workspace, int64_t workspace_bytes,
+                  void* stream);
+
+/* Paged GQA attention over a planned step.  Replaces the FIA call of
+ * GqaFIABackend._attn (reference auto_infer/layers/attention/gqa.py:81-94 ->
+ * base.py:48-61, npu_fused_infer_attention_score, TND layout, sparse_mode 3):
+ * query row i of request b attends keys j <= Lk - Lq + i (bottom-right
+ * causal), query head h reads KV head h / (Hq / Hkv), KV row j at
+ * block_table[b, j / block_size], offset j % block_size.
+ * query:  (num_tokens, Hq, head_dim) with the given token/head strides.
+ * caches: contiguous (num_blocks, block_size, Hkv, head_dim).
+ * out:    (num_tokens, Hq, head_dim) with the given strides.
+ * head_dim must be 128.  The workspace must hold a plan made by
+ * aia_attn_plan with the same metadata, head counts and num_waves. */
+int aia_paged_attention_gqa(const void* query, int64_t q_token_stride,
+                            int64_t q_head_stride,
+                            const void* key_cache, const void* value_cache,
+                            const int32_t* block_table, int32_t block_table_stride,
+                            const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
+                            int32_t batch, int32_t num_tokens,
+                            int32_t num_q_heads, int32_t num_kv_heads,
+                            int32_t head_dim, int32_t block_size,
+                            int32_t num_blocks, float scale,
+                            void* out, int64_t out_token_stride,
+                            int64_t out_head_stride, int32_t num_waves,
+                            void* workspace, int64_t workspace_bytes,
+                            void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AUTO_INFER_AMD_H */

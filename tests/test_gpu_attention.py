@@ -1,0 +1,111 @@
+"""Paged GQA attention on the GPU vs the float32 gather-softmax oracle.
+
+Tolerance (north star): 2e-2 max-abs, bf16 in/out, fp32 accumulation.
+"""
+import numpy as np
+import pytest
+import torch
+
+from auto_infer_amd import ops, workloads
+from oracle.paged_attn import paged_attention
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+TOL = 2e-2
+
+
+def run_gpu(step, num_waves=0):
+    s = step
+    plan = ops.AttentionPlan.from_lists(s.block_table.to(DEV), s.cu_seqlens_q, s.seqlens_kv,
+                                        s.q.shape[1], s.k_cache.shape[2], s.q.shape[2],
+                                        num_waves=num_waves)
+    out = ops.paged_attention_gqa(s.q.to(DEV), s.k_cache.to(DEV), s.v_cache.to(DEV), plan,
+                                  s.scale)
+    torch.cuda.synchronize()
+    return out.float().cpu()
+
+
+def oracle(step):
+    return paged_attention(step.q, step.k_cache, step.v_cache, step.block_table,
+                           step.cu_seqlens_q, step.seqlens_kv, step.scale)
+
+
+def check(step, num_waves=0):
+    got = run_gpu(step, num_waves)
+    exp = oracle(step)
+    err = (got - exp).abs().max().item()
+    print(f"max-abs err {err:.3e}", flush=True)
+    assert err <= TOL, err
+    return got
+
+
+def test_config1_decode_shape():
+    check(workloads.config1_decode(seed=3))
+
+
+@pytest.mark.parametrize("waves", [1, 7, 64, 0])
+def test_split_count_invariance(waves):
+    """The result does not depend on how the key range is split."""
+    step = workloads.make_gqa_step(lqs=[1, 1, 1], lks=[300, 17, 1000], num_q_heads=8,
+                                   num_kv_heads=2, block_size=16, seed=11)
+    check(step, waves)
+
+
+@pytest.mark.parametrize("group", [1, 2, 4, 7, 8, 16])
+def test_gqa_groups_decode(group):
+    hkv = 2
+    step = workloads.make_gqa_step(lqs=[1] * 5, lks=[1, 15, 16, 129, 700],
+                                   num_q_heads=hkv * group, num_kv_heads=hkv,
+                                   block_size=16, seed=group)
+    check(step)
+
+
+def test_mtp_verify_two_token_causal():
+    """Lq = 2 per request, causal inside the pair (config 4 shape, small)."""
+    step = workloads.make_gqa_step(lqs=[2] * 4, lks=[1024, 1500, 2, 4096], num_q_heads=32,
+                                   num_kv_heads=8, block_size=128, seed=4)
+    check(step)
+
+
+def test_chunked_prefill_and_decode_mixed():
+    """Ragged batch: prefill chunks continuing a prefix plus decode rows."""
+    step = workloads.make_gqa_step(lqs=[37, 1, 5, 1, 64], lks=[37 + 100, 300, 5, 77, 64],
+                                   num_q_heads=28, num_kv_heads=4, block_size=16, seed=9)
+    check(step)
+
+
+def test_block_size_not_multiple_of_tile():
+    step = workloads.make_gqa_step(lqs=[1, 3], lks=[45, 90], num_q_heads=4,
+                                   num_kv_heads=2, block_size=4, seed=2)
+    check(step)
+
+
+def test_large_group_split_heads():
+    """Hq/Hkv = 32 > 16 query rows per tile: heads are split over segments."""
+    step = workloads.make_gqa_step(lqs=[1, 2], lks=[200, 513], num_q_heads=64,
+                                   num_kv_heads=2, block_size=128, seed=5)
+    check(step)
+
+
+def test_block_permutation_invariance():
+    """Moving KV blocks in the pool (and the table with them) changes nothing."""
+    step = workloads.make_gqa_step(lqs=[1, 4], lks=[333, 260], num_q_heads=8,
+                                   num_kv_heads=4, block_size=16, seed=21, extra_blocks=13)
+    a = run_gpu(step)
+    nb = step.k_cache.shape[0]
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(1))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(nb)
+    step.k_cache = step.k_cache[perm]
+    step.v_cache = step.v_cache[perm]
+    step.block_table = inv[step.block_table.long()].to(torch.int32)
+    b = run_gpu(step)
+    assert torch.equal(a, b)
+
+
+def test_empty_context_rows_are_zero():
+    step = workloads.make_gqa_step(lqs=[1, 1], lks=[1, 40], num_q_heads=4, num_kv_heads=2,
+                                   block_size=16, seed=3)
+    step.seqlens_kv = [0, 40]        # request 0 sees nothing
+    got = run_gpu(step)
+    assert torch.count_nonzero(got[0]) == 0

@@ -1,0 +1,48 @@
+"""The C-ABI library loads and exports every symbol the header declares (CPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from auto_infer_amd import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if fn.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", fn)).read()
+            names |= set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(aia_\w+)\s*\(", text, re.M))
+    return names
+
+
+def test_header_declares_the_binding_table():
+    assert declared_symbols() == set(_native.SIGNATURES)
+
+
+def test_library_exports_all_declared_symbols():
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.fail(f"library not built: {_native.LIB_PATH}")
+    lib = ctypes.CDLL(_native.LIB_PATH)
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_error_reporting_without_gpu():
+    lib = _native.load()
+    assert lib.aia_version() >= 100
+    # argument validation happens before any device call
+    rc = lib.aia_attn_workspace_bytes(4, 4, 3, 2, 128, ctypes.byref(ctypes.c_int64()))
+    assert rc == _native.AIA_ERR_INVALID
+    assert "multiple" in _native.last_error()
+    with pytest.raises(ValueError, match="multiple"):
+        _native.check(rc, "aia_attn_workspace_bytes")
+
+
+def test_workspace_query():
+    out = ctypes.c_int64(0)
+    _native.call("aia_attn_workspace_bytes", 16, 16, 16, 8, 128, ctypes.byref(out))
+    assert out.value > 0

@@ -32,7 +32,7 @@ SIGNATURES = {
     "aia_attn_plan": [c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp],
     "aia_paged_attention_gqa": [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp,
                                 c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32,
-                                c_vp, c_i64, c_i64, c_i32, c_vp, c_i64, c_vp],
+                                c_vp, c_i64, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp],
 }
 
 

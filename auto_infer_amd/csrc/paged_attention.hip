@@ -64,7 +64,7 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
   int64_t off = 0;
   L.hdr = off;      off = align256(off + 64 * 4);
   L.seg = off;      off = align256(off + (L.seg_cap + 1) * 8 * 4);
-  L.wave = off;     off = align256(off + (int64_t)waves * 16);
+  L.wave = off;     off = align256(off + (int64_t)waves * 64);
   L.part_ml = off;  off = align256(off + L.part_cap * kRows * 8);
   L.part_o = off;   off = align256(off + L.part_cap * kRows * (int64_t)dv * 4);
   L.total = off;
@@ -113,7 +113,7 @@ __device__ int block_exclusive_scan(int v, int* wave_sums, int* total) {
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ kvlen,
     int32_t batch, Geometry g, int32_t waves,
-    int32_t* __restrict__ hdr, int32_t* __restrict__ seg, int4* __restrict__ wave_info) {
+    int32_t* __restrict__ hdr, int32_t* __restrict__ seg, int32_t* __restrict__ wave_rec) {
   __shared__ int req_off[kMaxBatch + 1];
   __shared__ int wave_sums[kPlanThreads / 64];
   const int tid = threadIdx.x;
@@ -201,19 +201,23 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   }
   __syncthreads();
 
-  // 4) per-wave start: first segment whose tile range contains w * tpw
+  // 4) per-wave record: first segment whose tile range holds w * tpw, the
+  //    wave's tile range and a copy of that segment's record, so a wave
+  //    starts with one scalar load.
   for (int w = tid; w < waves; w += kPlanThreads) {
     const int t0 = w * tpw;
-    int4 info = make_int4(-1, 0, 0, 0);
-    if (t0 < total_tiles) {
-      int lo = 0, hi = nseg - 1;  // last s with tile_begin <= t0
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (seg[(int64_t)mid * 8 + 5] <= t0) lo = mid; else hi = mid - 1;
-      }
-      info = make_int4(lo, t0, min(total_tiles, t0 + tpw), 0);
+    int* out = wave_rec + (int64_t)w * 16;
+    if (t0 >= total_tiles) {
+      out[0] = -1; out[1] = 0; out[2] = 0; out[3] = tpw;
+      continue;
     }
-    wave_info[w] = info;
+    int lo = 0, hi = nseg - 1;  // last s with tile_begin <= t0
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (seg[(int64_t)mid * 8 + 5] <= t0) lo = mid; else hi = mid - 1;
+    }
+    out[0] = lo; out[1] = t0; out[2] = min(total_tiles, t0 + tpw); out[3] = tpw;
+    for (int i = 0; i < 8; ++i) out[4 + i] = seg[(int64_t)lo * 8 + i];
   }
 }
 
@@ -228,9 +232,8 @@ struct AttnArgs {
   int64_t bt_stride;
   int32_t hkv, group, hb, bs, nb;
   float scale_log2;
-  const int32_t* hdr;
   const int32_t* seg;
-  const int4* wave_info;
+  const int32_t* wave_rec;
   float* part_o;
   float2* part_ml;
   uint16_t* out;
@@ -250,165 +253,175 @@ __device__ __forceinline__ uint16_t half_of(uint4 v, int e) {
   return (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffff));
 }
 
-__global__ __launch_bounds__(256) void gqa_attn_kernel(AttnArgs a) {
+// Tiles kept in flight per wave (registers: 32 VGPRs per tile).
+constexpr int kPipe = 4;
+
+// Processes key tiles [lt0, lt1) of one segment; rec = the segment record.
+__device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, int lt0, int lt1,
+                                            int w, int tpw, uint16_t* vt, int lane) {
+  const int n = lane & 15, g = lane >> 4;
+  const int b = rec[0], kvh = rec[1] & 0xffff, hbi = rec[1] >> 16;
+  const int qtok0 = rec[2], nq = rec[3], lim_base = rec[4];
+  const int tile_begin = rec[5], tile_end = rec[6], part_base = rec[7];
+  const int qi = n / a.hb, hh = n - qi * a.hb;
+  const bool rv = qi < nq && hbi * a.hb + hh < a.group;
+  const int head = kvh * a.group + hbi * a.hb + hh;
+  const int lim = rv ? lim_base + qi : -1;
+  const int visible = max(0, lim_base + nq);
+  const int row_elems = a.hkv * kHeadDim;
+
+  // Block ids of up to 64 consecutive logical blocks live one per lane.
+  const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
+  const int nblk_vis = (visible + a.bs - 1) / a.bs;
+  int blk_base = (lt0 * kTile) / a.bs;
+  int btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
+
+  uint4 qf[4];
+  if (rv) {
+    const uint4* qp = reinterpret_cast<const uint4*>(
+        a.q + (int64_t)(qtok0 + qi) * a.q_ts + (int64_t)head * a.q_hs);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qf[j] = qp[4 * j + g];
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qf[j] = make_uint4(0, 0, 0, 0);
+  }
+
+  float4_t o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float m = -1e30f, lsum = 0.f;
+
+  auto load = [&](int lt, uint4 (&kk)[4], uint4 (&vv)[4]) {
+    const int last = min(lt * kTile + kTile - 1, visible - 1);
+    if (last / a.bs - blk_base >= 64) {
+      blk_base = (lt * kTile) / a.bs;
+      btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
+    }
+    const int tok = min(lt * kTile + n, visible - 1);
+    const int bi = tok / a.bs;
+    // block ids outside the pool are clamped so a bad table cannot fault
+    const int blk = min(max(__shfl(btv, bi - blk_base), 0), a.nb - 1);
+    const int off = tok - bi * a.bs;
+    const int64_t base = ((int64_t)blk * a.bs + off) * row_elems + (int64_t)kvh * kHeadDim;
+    const uint4* kp = reinterpret_cast<const uint4*>(a.kc + base);
+    const uint4* vp = reinterpret_cast<const uint4*>(a.vc + base);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kk[j] = kp[4 * j + g];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vv[j] = vp[4 * j + g];
+  };
+
+  auto compute = [&](int lt, const uint4 (&kk)[4], const uint4 (&vv)[4]) {
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s4(kk[j].x, kk[j].y),
+                                                      as_s4(qf[j].x, qf[j].y), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s4(kk[j].z, kk[j].w),
+                                                      as_s4(qf[j].z, qf[j].w), acc, 0, 0, 0);
+    }
+    // V tile -> LDS, transposed: vt[d][key]
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vt[(32 * j + 8 * g + e) * kVtStride + n] = half_of(vv[j], e);
+    }
+    const int tb = lt * kTile + 4 * g;
+    float sv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sv[v] = (tb + v <= lim) ? acc[v] * a.scale_log2 : -INFINITY;
+    float tmax = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float mnew = fmaxf(m, tmax);
+    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+    float p[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) p[v] = __builtin_amdgcn_exp2f(sv[v] - mnew);
+    lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    m = mnew;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
+    const short4_t pb = as_s4(aia::pack_bf16x2(p[0], p[1]), aia::pack_bf16x2(p[2], p[3]));
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const short4_t va = *reinterpret_cast<const short4_t*>(vt + (16 * dt + n) * kVtStride + 4 * g);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[dt], 0, 0, 0);
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  uint4 kbuf[kPipe][4], vbuf[kPipe][4];
+#pragma unroll
+  for (int i = 0; i < kPipe; ++i)
+    if (lt0 + i < lt1) load(lt0 + i, kbuf[i], vbuf[i]);
+  for (int base = lt0; base < lt1; base += kPipe) {
+#pragma unroll
+    for (int i = 0; i < kPipe; ++i) {
+      const int lt = base + i;
+      if (lt < lt1) {
+        compute(lt, kbuf[i], vbuf[i]);
+        if (lt + kPipe < lt1) load(lt + kPipe, kbuf[i], vbuf[i]);
+      }
+    }
+  }
+
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+  const int first_wave = tile_begin / tpw;
+  const int nparts = (tile_end - 1) / tpw - first_wave + 1;
+  if (nparts == 1) {
+    if (rv) {
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        uint2 wv;
+        wv.x = aia::pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
+        wv.y = aia::pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
+        *reinterpret_cast<uint2*>(op + 16 * dt + 4 * g) = wv;
+      }
+    }
+  } else {
+    const int part = part_base + (w - first_wave);
+    if (rv) {
+      float* pp = a.part_o + ((int64_t)part * kRows + n) * kHeadDim;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+        *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * g) = o[dt];
+      if (g == 0) a.part_ml[(int64_t)part * kRows + n] = make_float2(m, lsum);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gqa_attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vt_all[4][kHeadDim * kVtStride];
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int w = blockIdx.x * 4 + wid;
   if (w >= a.waves) return;
-  const int4 wi = a.wave_info[w];
-  if (wi.x < 0) return;
+  const int* wr = a.wave_rec + (int64_t)w * 16;
+  int s = wr[0];
+  if (s < 0) return;
+  int t = wr[1];
+  const int t_end = wr[2], tpw = wr[3];
+  int rec[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) rec[i] = wr[4 + i];
   uint16_t* vt = vt_all[wid];
-  const int tpw = a.hdr[2];
-  const int n = lane & 15, g = lane >> 4;
-  const int row_elems = a.hkv * kHeadDim;
-
-  int s = wi.x, t = wi.y;
-  const int t_end = wi.z;
-  while (t < t_end) {
-    const int4 r0 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8);
-    const int4 r1 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8 + 4);
-    const int tile_begin = r1.y, tile_end = r1.z;
-    if (tile_end <= t) { ++s; continue; }
-    const int lt0 = t - tile_begin;
-    const int chunk_end = min(t_end, tile_end);
-    const int lt1 = chunk_end - tile_begin;
-
-    const int b = r0.x, kvh = r0.y & 0xffff, hbi = r0.y >> 16;
-    const int qtok0 = r0.z, nq = r0.w, lim_base = r1.x;
-    const int qi = n / a.hb, hh = n - qi * a.hb;
-    const bool rv = qi < nq && hbi * a.hb + hh < a.group;
-    const int head = kvh * a.group + hbi * a.hb + hh;
-    const int lim = rv ? lim_base + qi : -1;
-    const int visible = max(0, lim_base + nq);
-
-    uint4 qf[4];
-    if (rv) {
-      const uint4* qp = reinterpret_cast<const uint4*>(
-          a.q + (int64_t)(qtok0 + qi) * a.q_ts + (int64_t)head * a.q_hs);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) qf[j] = qp[4 * j + g];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) qf[j] = make_uint4(0, 0, 0, 0);
+  while (true) {
+    if (rec[6] > t) {
+      const int chunk_end = min(t_end, rec[6]);
+      gqa_segment(a, rec, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane);
+      t = chunk_end;
+      if (t >= t_end) break;
     }
-
-    // Block ids of up to 64 consecutive logical blocks live one per lane.
-    const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
-    const int nblk_vis = (visible + a.bs - 1) / a.bs;
-    int blk_base = (lt0 * kTile) / a.bs;
-    int btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
-
-    float4_t o[8];
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
-    float m = -1e30f, lsum = 0.f;
-
-    auto load = [&](int lt, uint4 (&kk)[4], uint4 (&vv)[4]) {
-      const int last = min(lt * kTile + kTile - 1, visible - 1);
-      if (last / a.bs - blk_base >= 64) {
-        blk_base = (lt * kTile) / a.bs;
-        btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
-      }
-      const int tok = min(lt * kTile + n, visible - 1);
-      const int bi = tok / a.bs;
-      // block ids outside the pool are clamped so a bad table cannot fault
-      const int blk = min(max(__shfl(btv, bi - blk_base), 0), a.nb - 1);
-      const int off = tok - bi * a.bs;
-      const int64_t base = ((int64_t)blk * a.bs + off) * row_elems + (int64_t)kvh * kHeadDim;
-      const uint4* kp = reinterpret_cast<const uint4*>(a.kc + base);
-      const uint4* vp = reinterpret_cast<const uint4*>(a.vc + base);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) kk[j] = kp[4 * j + g];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) vv[j] = vp[4 * j + g];
-    };
-
-    auto compute = [&](int lt, const uint4 (&kk)[4], const uint4 (&vv)[4]) {
-      float4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s4(kk[j].x, kk[j].y),
-                                                        as_s4(qf[j].x, qf[j].y), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s4(kk[j].z, kk[j].w),
-                                                        as_s4(qf[j].z, qf[j].w), acc, 0, 0, 0);
-      }
-      // V tile -> LDS, transposed: vt[d][key]
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vt[(32 * j + 8 * g + e) * kVtStride + n] = half_of(vv[j], e);
-      }
-      const int tb = lt * kTile + 4 * g;
-      float sv[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) sv[v] = (tb + v <= lim) ? acc[v] * a.scale_log2 : -INFINITY;
-      float tmax = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const float mnew = fmaxf(m, tmax);
-      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-      float p[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) p[v] = __builtin_amdgcn_exp2f(sv[v] - mnew);
-      lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-      m = mnew;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
-      const short4_t pb = as_s4(aia::pack_bf16x2(p[0], p[1]), aia::pack_bf16x2(p[2], p[3]));
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const short4_t va = *reinterpret_cast<const short4_t*>(vt + (16 * dt + n) * kVtStride + 4 * g);
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[dt], 0, 0, 0);
-      }
-      __builtin_amdgcn_wave_barrier();
-    };
-
-    uint4 ka[4], va_[4], kb[4], vb[4];
-    int lt = lt0;
-    load(lt, ka, va_);
-    while (true) {
-      bool more = lt + 1 < lt1;
-      if (more) load(lt + 1, kb, vb);
-      compute(lt, ka, va_);
-      if (!more) break;
-      ++lt;
-      more = lt + 1 < lt1;
-      if (more) load(lt + 1, ka, va_);
-      compute(lt, kb, vb);
-      if (!more) break;
-      ++lt;
-    }
-
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
-    const int first_wave = tile_begin / tpw;
-    const int nparts = (tile_end - 1) / tpw - first_wave + 1;
-    if (nparts == 1) {
-      if (rv) {
-        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-        uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          uint2 wv;
-          wv.x = aia::pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
-          wv.y = aia::pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
-          *reinterpret_cast<uint2*>(op + 16 * dt + 4 * g) = wv;
-        }
-      }
-    } else {
-      const int part = r1.w + (w - first_wave);
-      if (rv) {
-        float* pp = a.part_o + ((int64_t)part * kRows + n) * kHeadDim;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-          *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * g) = o[dt];
-        if (g == 0) a.part_ml[(int64_t)part * kRows + n] = make_float2(m, lsum);
-      }
-    }
-    t = chunk_end;
     ++s;
+    const int* r = a.seg + (int64_t)s * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rec[i] = r[i];
   }
 }
 
@@ -422,7 +435,8 @@ struct MergeArgs {
   int32_t group, hb;
 };
 
-// One work-group per split segment: thread (row, 8 dims).
+// One work-group per split segment, thread = (row, 8 dims); single pass
+// with running rescale so the loads of successive partials are independent.
 __global__ __launch_bounds__(256) void gqa_merge_kernel(MergeArgs a) {
   const int nseg = a.hdr[0], tpw = a.hdr[2];
   const int n = threadIdx.x >> 4;
@@ -438,21 +452,22 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(MergeArgs a) {
     if (!(qi < nq && hbi * a.hb + hh < a.group)) continue;
     const int head = kvh * a.group + hbi * a.hb + hh;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float lsum = 0.f;
-    if (np > 1) {
-      const int pb = r1.w;
-      float mx = -1e30f;
-      for (int k = 0; k < np; ++k) mx = fmaxf(mx, a.part_ml[(int64_t)(pb + k) * kRows + n].x);
-      for (int k = 0; k < np; ++k) {
-        const float2 ml = a.part_ml[(int64_t)(pb + k) * kRows + n];
-        const float wgt = __builtin_amdgcn_exp2f(ml.x - mx);
-        lsum += ml.y * wgt;
-        const float4* src = reinterpret_cast<const float4*>(
-            a.part_o + ((int64_t)(pb + k) * kRows + n) * kHeadDim + c);
-        const float4 x0 = src[0], x1 = src[1];
-        acc[0] += x0.x * wgt; acc[1] += x0.y * wgt; acc[2] += x0.z * wgt; acc[3] += x0.w * wgt;
-        acc[4] += x1.x * wgt; acc[5] += x1.y * wgt; acc[6] += x1.z * wgt; acc[7] += x1.w * wgt;
-      }
+    float mx = -1e30f, lsum = 0.f;
+    const int pb = r1.w;
+#pragma unroll 4
+    for (int k = 0; k < np; ++k) {
+      const float2 ml = a.part_ml[(int64_t)(pb + k) * kRows + n];
+      const float4* src = reinterpret_cast<const float4*>(
+          a.part_o + ((int64_t)(pb + k) * kRows + n) * kHeadDim + c);
+      const float4 x0 = src[0], x1 = src[1];
+      const float mn = fmaxf(mx, ml.x);
+      const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
+      lsum = lsum * sa + ml.y * sb;
+      acc[0] = acc[0] * sa + x0.x * sb; acc[1] = acc[1] * sa + x0.y * sb;
+      acc[2] = acc[2] * sa + x0.z * sb; acc[3] = acc[3] * sa + x0.w * sb;
+      acc[4] = acc[4] * sa + x1.x * sb; acc[5] = acc[5] * sa + x1.y * sb;
+      acc[6] = acc[6] * sa + x1.z * sb; acc[7] = acc[7] * sa + x1.w * sb;
+      mx = mn;
     }
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
     uint4 wv;
@@ -506,7 +521,7 @@ extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens
   char* ws = static_cast<char*>(workspace);
   plan_kernel<<<1, kPlanThreads, 0, (hipStream_t)stream>>>(
       cu_seqlens_q, seqlens_kv, batch, g, waves, reinterpret_cast<int32_t*>(ws + L.hdr),
-      reinterpret_cast<int32_t*>(ws + L.seg), reinterpret_cast<int4*>(ws + L.wave));
+      reinterpret_cast<int32_t*>(ws + L.seg), reinterpret_cast<int32_t*>(ws + L.wave));
   return check_hip(hipGetLastError(), "aia_attn_plan launch");
 }
 
@@ -516,7 +531,7 @@ extern "C" int aia_paged_attention_gqa(
     const int32_t* cu_seqlens_q, const int32_t* seqlens_kv, int32_t batch, int32_t num_tokens,
     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
     int32_t num_blocks, float scale, void* out, int64_t out_token_stride, int64_t out_head_stride,
-    int32_t num_waves, void* workspace, int64_t workspace_bytes, void* stream) {
+    int32_t num_waves, int32_t flags, void* workspace, int64_t workspace_bytes, void* stream) {
   using namespace aia;
   (void)cu_seqlens_q; (void)seqlens_kv;
   if (int rc = check_heads("aia_paged_attention_gqa", num_q_heads, num_kv_heads)) return rc;
@@ -548,9 +563,8 @@ extern "C" int aia_paged_attention_gqa(
   a.bt = block_table; a.bt_stride = block_table_stride;
   a.hkv = g.hkv; a.group = g.group; a.hb = g.hb; a.bs = block_size; a.nb = num_blocks;
   a.scale_log2 = scale * 1.4426950408889634f;
-  a.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
   a.seg = reinterpret_cast<const int32_t*>(ws + L.seg);
-  a.wave_info = reinterpret_cast<const int4*>(ws + L.wave);
+  a.wave_rec = reinterpret_cast<const int32_t*>(ws + L.wave);
   a.part_o = reinterpret_cast<float*>(ws + L.part_o);
   a.part_ml = reinterpret_cast<float2*>(ws + L.part_ml);
   a.out = static_cast<uint16_t*>(out);
@@ -559,8 +573,9 @@ extern "C" int aia_paged_attention_gqa(
   hipStream_t s = (hipStream_t)stream;
   gqa_attn_kernel<<<waves / 4, 256, 0, s>>>(a);
   if (int rc = check_hip(hipGetLastError(), "gqa_attn_kernel launch")) return rc;
+  if (flags & AIA_ATTN_SKIP_MERGE) return AIA_OK;
   MergeArgs mg;
-  mg.hdr = a.hdr; mg.seg = a.seg; mg.part_o = a.part_o; mg.part_ml = a.part_ml;
+  mg.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr); mg.seg = a.seg; mg.part_o = a.part_o; mg.part_ml = a.part_ml;
   mg.out = a.out; mg.o_ts = a.o_ts; mg.o_hs = a.o_hs; mg.group = g.group; mg.hb = g.hb;
   int64_t mgrid = L.seg_cap < 4096 ? L.seg_cap : 4096;
   if (mgrid < 1) mgrid = 1;

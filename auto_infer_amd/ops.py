@@ -148,9 +148,15 @@ class AttentionPlan:
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=block_table.device)
         _require(workspace.numel() >= nbytes, "attention workspace too small")
         self.workspace = workspace
-        _native.call("aia_attn_plan", _ptr(cu_seqlens_q), _ptr(seqlens_kv), batch,
-                     self.num_tokens, num_q_heads, num_kv_heads, head_dim_v, num_waves,
-                     _ptr(workspace), workspace.numel(), _stream(block_table.device))
+        self.replan()
+
+    def replan(self):
+        """Re-run the device planner on the (possibly updated in place)
+        metadata tensors; graph-capturable."""
+        _native.call("aia_attn_plan", _ptr(self.cu_seqlens_q), _ptr(self.seqlens_kv),
+                     self.batch, self.num_tokens, self.num_q_heads, self.num_kv_heads,
+                     self.head_dim_v, self.num_waves, _ptr(self.workspace),
+                     self.workspace.numel(), _stream(self.block_table.device))
 
     @classmethod
     def from_lists(cls, block_table, cu_seqlens_q, seqlens_kv, num_q_heads, num_kv_heads,
@@ -168,7 +174,10 @@ class AttentionPlan:
         return cls(block_table, cu, kv, total, num_q_heads, num_kv_heads, head_dim_v, **kw)
 
 
-def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None):
+ATTN_SKIP_MERGE = 1   # diagnostic flag: time the split-K kernel alone
+
+
+def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None, flags=0):
     """Paged GQA attention (reference base.py:48-61 FIA semantics).
 
     query (T, Hq, 128) bf16; key/value caches (NB, bs, Hkv, 128) bf16
@@ -193,6 +202,13 @@ def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None):
                  _ptr(key_cache), _ptr(value_cache), _ptr(plan.block_table),
                  plan.block_table.stride(0), _ptr(plan.cu_seqlens_q), _ptr(plan.seqlens_kv),
                  plan.batch, T, hq, hkv, d, bs, nb, float(scale), _ptr(out), out.stride(0),
-                 out.stride(1), plan.num_waves, _ptr(plan.workspace), plan.workspace.numel(),
-                 _stream(query.device))
+                 out.stride(1), plan.num_waves, flags, _ptr(plan.workspace),
+                 plan.workspace.numel(), _stream(query.device))
     return out
+
+
+def paged_attention_kernel_only(query, key_cache, value_cache, plan, scale, out=None):
+    """The split-K attention kernel without the merge pass (timing only:
+    rows split over several waves are left unmerged)."""
+    return paged_attention_gqa(query, key_cache, value_cache, plan, scale, out,
+                               flags=ATTN_SKIP_MERGE)

@@ -1,0 +1,238 @@
+"""Benchmark of the paged decode-attention hot path on one MI355X.
+
+Workload (the configuration the metric is quoted
+on): GQA decode, Qwen3-0.6B heads (Hq 16, Hkv 8, D 128), bf16, batch 16,
+query length 1, contexts U[128, 2048] (seeded), block 128, a 512-block pool
+per layer, values N(0,1)/sqrt(128).
+
+One *step* = one layer's decode attention for the batch: the KV write of the
+16 new rows (slot mapping) + split-K paged attention + partial merge, plus
+1/L of the per-step planner launch (the plan is shared by the L layers of a
+model step).  L = 8 layer caches are rotated (8 x 268 MB > the 256 MB
+Infinity Cache) so KV reads come from HBM.  Steps are replayed from a HIP
+graph captured on the timed stream (the reference replays ACL graphs for
+decode too).
+
+Prints ONE JSON line (see the field notes in DESIGN.md).
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+METRIC = "paged decode attn HBM GB/s (% of 8 TB/s peak), tok/s at bs=16; packing µs/step"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--layers", type=int, default=8)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="budget of the CPU baseline sample")
+    p.add_argument("--no-cpu", action="store_true")
+    return p.parse_args()
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def cpu_baseline(step, budget_s):
+    """The oracle (torch CPU eager restatement of write_kv + paged FIA) on
+    the host cores, timed on a bounded sample of the same workload."""
+    from oracle.paged_attn import kv_write, paged_attention
+    kc, vc = step.k_cache.clone(), step.v_cache.clone()
+    threads = torch.get_num_threads()
+
+    def one():
+        kv_write(step.k_new, step.v_new, kc, vc, step.slot_mapping)
+        paged_attention(step.q, kc, vc, step.block_table, step.cu_seqlens_q,
+                        step.seqlens_kv, step.scale).to(torch.bfloat16)
+
+    for _ in range(2):
+        one()
+    times = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < budget_s or len(times) < 3:
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 200:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": round(len(step.seqlens_kv) / med, 1),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{len(times)} steps of config 1 (one layer: KV write + paged attention, "
+                  f"median {med * 1e3:.1f} ms), torch {torch.__version__} CPU eager, "
+                  f"{threads} threads of {os.cpu_count()} ({cpu_model()})",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    from auto_infer_amd import ops, workloads
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    step = workloads.config1_decode(seed=args.seed)
+    B, T = len(step.seqlens_kv), step.num_tokens
+    hq, hkv, d = step.q.shape[1], step.k_cache.shape[2], step.q.shape[2]
+    L = args.layers
+
+    q = step.q.to(dev)
+    k_new, v_new = step.k_new.to(dev), step.v_new.to(dev)
+    slots = step.slot_mapping.to(dev)
+    bt = step.block_table.to(dev)
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 7)
+    kcs, vcs = [step.k_cache.to(dev)], [step.v_cache.to(dev)]
+    for _ in range(L - 1):
+        kcs.append((torch.randn(step.k_cache.shape, generator=gen, device=dev)
+                    / 128 ** 0.5).to(torch.bfloat16))
+        vcs.append((torch.randn(step.v_cache.shape, generator=gen, device=dev)
+                    / 128 ** 0.5).to(torch.bfloat16))
+    out = torch.empty(T, hq, d, dtype=torch.bfloat16, device=dev)
+    cu = torch.tensor([0, *step.cu_seqlens_q], dtype=torch.int32, device=dev)
+    kvl = torch.tensor(step.seqlens_kv, dtype=torch.int32, device=dev)
+    plan = ops.AttentionPlan(bt, cu, kvl, T, hq, hkv, d)
+
+    def model_step():
+        """Planner once, then L layers of (KV write + attention)."""
+        plan.replan()
+        for layer in range(L):
+            ops.write_kv(k_new, v_new, kcs[layer], vcs[layer], slots)
+            ops.paged_attention_gqa(q, kcs[layer], vcs[layer], plan, step.scale, out=out)
+
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            model_step()
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        model_step()
+    # Graph replays cover L layer-steps each.
+    n_replay = max(1, (args.steps + L - 1) // L)
+    n_warm = max(1, (args.warmup + L - 1) // L)
+    with torch.cuda.stream(stream):
+        for _ in range(n_warm):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(n_replay):
+            graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    steps = n_replay * L
+    ms_per_step = e0.elapsed_time(e1) / steps
+
+    # Dominant kernel alone: back-to-back attention launches on the same
+    # stream, averaged over the timed region (HIP events on that stream).
+    n_k = 50 * L
+    with torch.cuda.stream(stream):
+        for i in range(L):
+            ops.paged_attention_gqa(q, kcs[i], vcs[i], plan, step.scale, out=out)
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        g2 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g2, stream=stream):
+            for i in range(L):
+                ops.paged_attention_kernel_only(q, kcs[i], vcs[i], plan, step.scale, out=out)
+        g2.replay()
+        torch.cuda.synchronize()
+        a0.record(stream)
+        for _ in range(n_k // L):
+            g2.replay()
+        a1.record(stream)
+    torch.cuda.synchronize()
+    attn_us = a0.elapsed_time(a1) * 1e3 / n_k
+
+    # packing: planner launch alone
+    with torch.cuda.stream(stream):
+        g3 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g3, stream=stream):
+            for _ in range(20):
+                plan.replan()
+        g3.replay()
+        torch.cuda.synchronize()
+        p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        p0.record(stream)
+        for _ in range(10):
+            g3.replay()
+        p1.record(stream)
+    torch.cuda.synchronize()
+    plan_us = p0.elapsed_time(p1) * 1e3 / 200
+
+    kv_bytes = step.kv_bytes_read()
+    qo_bytes = 2 * T * hq * d * 2
+    meta_bytes = sum((lk + 127) // 128 for lk in step.seqlens_kv) * 4 + B * 8
+    attn_alg_bytes = kv_bytes + qo_bytes + meta_bytes
+    write_bytes = 2 * T * hkv * d * 2 * 2          # read new rows + write slots
+    step_alg_bytes = attn_alg_bytes + write_bytes
+    achieved = attn_alg_bytes / (attn_us * 1e-6) / 1e9
+    step_s = ms_per_step * 1e-3
+
+    result = {
+        "metric": METRIC,
+        "value": round(B / step_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": n_warm * L,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)/sqrt(128) K/V/Q, random block tables)",
+        "config": {
+            "workload": "configs[0]: GQA paged decode, Qwen3-0.6B heads Hq16/Hkv8/D128, "
+                        "batch 16, Lq 1, Lk~U[128,2048], block 128, 512-block pool/layer",
+            "batch": B, "kv_tokens": int(sum(step.seqlens_kv)),
+            "layers_rotated": L, "timing": "HIP graph replay, HIP events",
+        },
+        "step_hbm_GBps": round(step_alg_bytes / step_s / 1e9, 1),
+        "step_frac_of_peak": round(step_alg_bytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
+        "attention_kernel_us": round(attn_us, 3),
+        "packing_us_per_step": round(plan_us, 3),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(step, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

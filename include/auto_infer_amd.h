@@ -81,7 +81,10 @@ int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
  * caches: contiguous (num_blocks, block_size, Hkv, head_dim).
  * out:    (num_tokens, Hq, head_dim) with the given strides.
  * head_dim must be 128.  The workspace must hold a plan made by
- * aia_attn_plan with the same metadata, head counts and num_waves. */
+ * aia_attn_plan with the same metadata, head counts and num_waves.
+ * flags: 0, or AIA_ATTN_SKIP_MERGE to launch the split-K kernel without the
+ * merge pass (diagnostic timing; split rows are then left unmerged). */
+#define AIA_ATTN_SKIP_MERGE 1
 int aia_paged_attention_gqa(const void* query, int64_t q_token_stride,
                             int64_t q_head_stride,
                             const void* key_cache, const void* value_cache,
@@ -93,7 +96,7 @@ int aia_paged_attention_gqa(const void* query, int64_t q_token_stride,
                             int32_t num_blocks, float scale,
                             void* out, int64_t out_token_stride,
                             int64_t out_head_stride, int32_t num_waves,
-                            void* workspace, int64_t workspace_bytes,
+                            int32_t flags, void* workspace, int64_t workspace_bytes,
                             void* stream);
 
 #ifdef __cplusplus

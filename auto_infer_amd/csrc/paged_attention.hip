@@ -432,15 +432,15 @@ struct MergeArgs {
   const float2* part_ml;
   uint16_t* out;
   int64_t o_ts, o_hs;
-  int32_t group, hb;
+  int32_t group, hb, dv;
 };
 
-// One work-group per split segment, thread = (row, 8 dims); single pass
-// with running rescale so the loads of successive partials are independent.
-__global__ __launch_bounds__(256) void gqa_merge_kernel(MergeArgs a) {
+// One work-group per split segment; thread = (row, 8 dims), looping over the
+// dims when dv > 128.  Single pass with running rescale so the loads of
+// successive partials are independent.
+__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int nseg = a.hdr[0], tpw = a.hdr[2];
   const int n = threadIdx.x >> 4;
-  const int c = (threadIdx.x & 15) * 8;
   for (int s = blockIdx.x; s < nseg; s += gridDim.x) {
     const int4 r0 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8);
     const int4 r1 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8 + 4);
@@ -451,32 +451,253 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(MergeArgs a) {
     const int qi = n / a.hb, hh = n - qi * a.hb;
     if (!(qi < nq && hbi * a.hb + hh < a.group)) continue;
     const int head = kvh * a.group + hbi * a.hb + hh;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float mx = -1e30f, lsum = 0.f;
     const int pb = r1.w;
+    for (int c = (threadIdx.x & 15) * 8; c < a.dv; c += 128) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      float mx = -1e30f, lsum = 0.f;
 #pragma unroll 4
-    for (int k = 0; k < np; ++k) {
-      const float2 ml = a.part_ml[(int64_t)(pb + k) * kRows + n];
-      const float4* src = reinterpret_cast<const float4*>(
-          a.part_o + ((int64_t)(pb + k) * kRows + n) * kHeadDim + c);
-      const float4 x0 = src[0], x1 = src[1];
-      const float mn = fmaxf(mx, ml.x);
-      const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
-      lsum = lsum * sa + ml.y * sb;
-      acc[0] = acc[0] * sa + x0.x * sb; acc[1] = acc[1] * sa + x0.y * sb;
-      acc[2] = acc[2] * sa + x0.z * sb; acc[3] = acc[3] * sa + x0.w * sb;
-      acc[4] = acc[4] * sa + x1.x * sb; acc[5] = acc[5] * sa + x1.y * sb;
-      acc[6] = acc[6] * sa + x1.z * sb; acc[7] = acc[7] * sa + x1.w * sb;
-      mx = mn;
+      for (int k = 0; k < np; ++k) {
+        const float2 ml = a.part_ml[(int64_t)(pb + k) * kRows + n];
+        const float4* src = reinterpret_cast<const float4*>(
+            a.part_o + ((int64_t)(pb + k) * kRows + n) * a.dv + c);
+        const float4 x0 = src[0], x1 = src[1];
+        const float mn = fmaxf(mx, ml.x);
+        const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
+        lsum = lsum * sa + ml.y * sb;
+        acc[0] = acc[0] * sa + x0.x * sb; acc[1] = acc[1] * sa + x0.y * sb;
+        acc[2] = acc[2] * sa + x0.z * sb; acc[3] = acc[3] * sa + x0.w * sb;
+        acc[4] = acc[4] * sa + x1.x * sb; acc[5] = acc[5] * sa + x1.y * sb;
+        acc[6] = acc[6] * sa + x1.z * sb; acc[7] = acc[7] * sa + x1.w * sb;
+        mx = mn;
+      }
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      uint4 wv;
+      wv.x = aia::pack_bf16x2(acc[0] * inv, acc[1] * inv);
+      wv.y = aia::pack_bf16x2(acc[2] * inv, acc[3] * inv);
+      wv.z = aia::pack_bf16x2(acc[4] * inv, acc[5] * inv);
+      wv.w = aia::pack_bf16x2(acc[6] * inv, acc[7] * inv);
+      *reinterpret_cast<uint4*>(a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs + c) = wv;
     }
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    uint4 wv;
-    wv.x = aia::pack_bf16x2(acc[0] * inv, acc[1] * inv);
-    wv.y = aia::pack_bf16x2(acc[2] * inv, acc[3] * inv);
-    wv.z = aia::pack_bf16x2(acc[4] * inv, acc[5] * inv);
-    wv.w = aia::pack_bf16x2(acc[6] * inv, acc[7] * inv);
-    *reinterpret_cast<uint4*>(a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs + c) = wv;
   }
+}
+
+// ---------------------------------------------------------------- absorbed MLA
+//
+// One KV head of 576 bf16 per token (512 latent + 64 rope), V = the first 512
+// values, Hq query heads share it.  A work-group of 4 waves owns one tile
+// range: wave w loads latent dims [128w, 128w + 128) of every key (waves 0/1
+// also one 32-dim rope chunk each), computes its partial S^T on MFMA, the
+// four partials are summed through LDS (one barrier per tile), every wave
+// runs the same softmax, and wave w accumulates output dims
+// [128w, 128w + 128) from the K registers it already holds (V = K).
+constexpr int kMlaK = 576, kMlaV = 512;
+
+struct MlaArgs {
+  const uint16_t* q;
+  int64_t q_ts, q_hs;
+  const uint16_t* cache;
+  const int32_t* bt;
+  int64_t bt_stride;
+  int32_t group, hb, bs, nb;
+  float scale_log2;
+  const int32_t* seg;
+  const int32_t* wave_rec;
+  float* part_o;
+  float2* part_ml;
+  uint16_t* out;
+  int64_t o_ts, o_hs;
+  int32_t waves;
+};
+
+__device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, int lt0, int lt1,
+                                            int w, int tpw, uint16_t* vt, float* sx, int lane,
+                                            int wid) {
+  const int n = lane & 15, g = lane >> 4;
+  const int b = rec[0], hbi = rec[1] >> 16;
+  const int qtok0 = rec[2], nq = rec[3], lim_base = rec[4];
+  const int tile_begin = rec[5], tile_end = rec[6], part_base = rec[7];
+  const int qi = n / a.hb, hh = n - qi * a.hb;
+  const bool rv = qi < nq && hbi * a.hb + hh < a.group;
+  const int head = hbi * a.hb + hh;
+  const int lim = rv ? lim_base + qi : -1;
+  const int visible = max(0, lim_base + nq);
+  const bool has_rope = wid < 2;
+  // 16-byte chunk index (within a 576-element row) of this lane's pieces
+  int cidx[5];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) cidx[j] = 4 * (4 * wid + j) + g;
+  cidx[4] = 4 * (16 + wid) + g;
+
+  const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
+  const int nblk_vis = (visible + a.bs - 1) / a.bs;
+  int blk_base = (lt0 * kTile) / a.bs;
+  int btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
+
+  uint4 qf[5];
+  if (rv) {
+    const uint4* qp = reinterpret_cast<const uint4*>(
+        a.q + (int64_t)(qtok0 + qi) * a.q_ts + (int64_t)head * a.q_hs);
+#pragma unroll
+    for (int j = 0; j < 5; ++j) qf[j] = (j < 4 || has_rope) ? qp[cidx[j]] : make_uint4(0, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 5; ++j) qf[j] = make_uint4(0, 0, 0, 0);
+  }
+
+  float4_t o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float m = -1e30f, lsum = 0.f;
+
+  auto load = [&](int lt, uint4 (&kk)[5]) {
+    const int last = min(lt * kTile + kTile - 1, visible - 1);
+    if (last / a.bs - blk_base >= 64) {
+      blk_base = (lt * kTile) / a.bs;
+      btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
+    }
+    const int tok = min(lt * kTile + n, visible - 1);
+    const int bi = tok / a.bs;
+    const int blk = min(max(__shfl(btv, bi - blk_base), 0), a.nb - 1);
+    const int off = tok - bi * a.bs;
+    const uint4* kp = reinterpret_cast<const uint4*>(a.cache + ((int64_t)blk * a.bs + off) * kMlaK);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kk[j] = kp[cidx[j]];
+    kk[4] = has_rope ? kp[cidx[4]] : make_uint4(0, 0, 0, 0);
+  };
+
+  int parity = 0;
+  auto compute = [&](int lt, const uint4 (&kk)[5]) {
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+      if (j == 4 && !has_rope) break;
+      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s4(kk[j].x, kk[j].y),
+                                                      as_s4(qf[j].x, qf[j].y), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s4(kk[j].z, kk[j].w),
+                                                      as_s4(qf[j].z, qf[j].w), acc, 0, 0, 0);
+    }
+    float* xb = sx + parity * (4 * 256);
+    *reinterpret_cast<float4_t*>(xb + wid * 256 + lane * 4) = acc;
+    // V^T slice of this wave: vt[d][key], d local to [0, 128)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vt[(32 * j + 8 * g + e) * kVtStride + n] = half_of(kk[j], e);
+    }
+    __syncthreads();
+    float4_t tot = *reinterpret_cast<const float4_t*>(xb + lane * 4);
+#pragma unroll
+    for (int ww = 1; ww < 4; ++ww) tot += *reinterpret_cast<const float4_t*>(xb + ww * 256 + lane * 4);
+    parity ^= 1;
+    const int tb = lt * kTile + 4 * g;
+    float sv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sv[v] = (tb + v <= lim) ? tot[v] * a.scale_log2 : -INFINITY;
+    float tmax = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float mnew = fmaxf(m, tmax);
+    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+    float p[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) p[v] = __builtin_amdgcn_exp2f(sv[v] - mnew);
+    lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    m = mnew;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
+    const short4_t pb = as_s4(aia::pack_bf16x2(p[0], p[1]), aia::pack_bf16x2(p[2], p[3]));
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const short4_t va = *reinterpret_cast<const short4_t*>(vt + (16 * dt + n) * kVtStride + 4 * g);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[dt], 0, 0, 0);
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  uint4 kbuf[kPipe][5];
+#pragma unroll
+  for (int i = 0; i < kPipe; ++i)
+    if (lt0 + i < lt1) load(lt0 + i, kbuf[i]);
+  for (int base = lt0; base < lt1; base += kPipe) {
+#pragma unroll
+    for (int i = 0; i < kPipe; ++i) {
+      const int lt = base + i;
+      if (lt < lt1) {
+        compute(lt, kbuf[i]);
+        if (lt + kPipe < lt1) load(lt + kPipe, kbuf[i]);
+      }
+    }
+  }
+
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+  const int first_wave = tile_begin / tpw;
+  const int nparts = (tile_end - 1) / tpw - first_wave + 1;
+  const int d0 = 128 * wid;
+  if (nparts == 1) {
+    if (rv) {
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs + d0;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        uint2 wv;
+        wv.x = aia::pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
+        wv.y = aia::pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
+        *reinterpret_cast<uint2*>(op + 16 * dt + 4 * g) = wv;
+      }
+    }
+  } else {
+    const int part = part_base + (w - first_wave);
+    if (rv) {
+      float* pp = a.part_o + ((int64_t)part * kRows + n) * kMlaV + d0;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+        *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * g) = o[dt];
+      if (g == 0 && wid == 0) a.part_ml[(int64_t)part * kRows + n] = make_float2(m, lsum);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void mla_attn_kernel(MlaArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t vt_all[4][kHeadDim * kVtStride];
+  __shared__ __attribute__((aligned(16))) float sx[2 * 4 * 256];
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int w = blockIdx.x;   // one tile range per work-group
+  if (w >= a.waves) return;
+  const int* wr = a.wave_rec + (int64_t)w * 16;
+  int s = wr[0];
+  if (s < 0) return;
+  int t = wr[1];
+  const int t_end = wr[2], tpw = wr[3];
+  int rec[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) rec[i] = wr[4 + i];
+  while (true) {
+    if (rec[6] > t) {
+      const int chunk_end = min(t_end, rec[6]);
+      mla_segment(a, rec, t - rec[5], chunk_end - rec[5], w, tpw, vt_all[wid], sx, lane, wid);
+      t = chunk_end;
+      if (t >= t_end) break;
+    }
+    ++s;
+    const int* r = a.seg + (int64_t)s * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rec[i] = r[i];
+  }
+}
+
+int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t dv, const float* part_o,
+                 const float2* part_ml, const int32_t* seg, uint16_t* out, int64_t o_ts,
+                 int64_t o_hs, hipStream_t s) {
+  MergeArgs mg;
+  mg.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
+  mg.seg = seg; mg.part_o = part_o; mg.part_ml = part_ml;
+  mg.out = out; mg.o_ts = o_ts; mg.o_hs = o_hs; mg.group = g.group; mg.hb = g.hb; mg.dv = dv;
+  int64_t mgrid = L.seg_cap < 4096 ? L.seg_cap : 4096;
+  if (mgrid < 1) mgrid = 1;
+  merge_kernel<<<(unsigned)mgrid, 256, 0, s>>>(mg);
+  return aia::check_hip(hipGetLastError(), "merge_kernel launch");
 }
 
 int check_heads(const char* fn, int32_t hq, int32_t hkv) {
@@ -574,11 +795,56 @@ extern "C" int aia_paged_attention_gqa(
   gqa_attn_kernel<<<waves / 4, 256, 0, s>>>(a);
   if (int rc = check_hip(hipGetLastError(), "gqa_attn_kernel launch")) return rc;
   if (flags & AIA_ATTN_SKIP_MERGE) return AIA_OK;
-  MergeArgs mg;
-  mg.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr); mg.seg = a.seg; mg.part_o = a.part_o; mg.part_ml = a.part_ml;
-  mg.out = a.out; mg.o_ts = a.o_ts; mg.o_hs = a.o_hs; mg.group = g.group; mg.hb = g.hb;
-  int64_t mgrid = L.seg_cap < 4096 ? L.seg_cap : 4096;
-  if (mgrid < 1) mgrid = 1;
-  gqa_merge_kernel<<<(unsigned)mgrid, 256, 0, s>>>(mg);
-  return check_hip(hipGetLastError(), "gqa_merge_kernel launch");
+  return launch_merge(ws, L, g, head_dim, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs, s);
+}
+
+extern "C" int aia_paged_attention_mla(
+    const void* q_latent, int64_t q_token_stride, int64_t q_head_stride, const void* latent_cache,
+    const int32_t* block_table, int32_t block_table_stride, const int32_t* cu_seqlens_q,
+    const int32_t* seqlens_kv, int32_t batch, int32_t num_tokens, int32_t num_heads,
+    int32_t kv_lora_rank, int32_t rope_dim, int32_t block_size, int32_t num_blocks, float scale,
+    void* out, int64_t out_token_stride, int64_t out_head_stride, int32_t num_waves, int32_t flags,
+    void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace aia;
+  (void)cu_seqlens_q; (void)seqlens_kv;
+  if (kv_lora_rank != kMlaV || rope_dim != kMlaK - kMlaV)
+    return fail(AIA_ERR_UNSUPPORTED, "aia_paged_attention_mla: latent %d + rope %d (only 512 + 64)",
+                kv_lora_rank, rope_dim);
+  if (int rc = check_heads("aia_paged_attention_mla", num_heads, 1)) return rc;
+  if (block_size <= 0 || num_blocks <= 0)
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_mla: block_size %d / num_blocks %d",
+                block_size, num_blocks);
+  if (!q_latent || !latent_cache || !block_table || !out || !workspace)
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_mla: null pointer argument");
+  if (q_token_stride % 8 || q_head_stride % 8 || out_token_stride % 8 || out_head_stride % 8 ||
+      ((uintptr_t)q_latent & 15) || ((uintptr_t)latent_cache & 15) || ((uintptr_t)out & 15))
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_mla: tensors must be 16-byte aligned with "
+                "strides a multiple of 8 elements");
+  if (num_tokens == 0 || batch == 0) return AIA_OK;
+  const Geometry g = geometry(num_heads, 1);
+  const int32_t waves = resolve_waves(num_waves);
+  const Layout L = layout(batch, num_tokens, g, kMlaV, waves);
+  if (workspace_bytes < L.total)
+    return fail(AIA_ERR_CAPACITY, "aia_paged_attention_mla: workspace %lld bytes < %lld needed",
+                (long long)workspace_bytes, (long long)L.total);
+  char* ws = static_cast<char*>(workspace);
+  MlaArgs a;
+  a.q = static_cast<const uint16_t*>(q_latent);
+  a.q_ts = q_token_stride; a.q_hs = q_head_stride;
+  a.cache = static_cast<const uint16_t*>(latent_cache);
+  a.bt = block_table; a.bt_stride = block_table_stride;
+  a.group = g.group; a.hb = g.hb; a.bs = block_size; a.nb = num_blocks;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.seg = reinterpret_cast<const int32_t*>(ws + L.seg);
+  a.wave_rec = reinterpret_cast<const int32_t*>(ws + L.wave);
+  a.part_o = reinterpret_cast<float*>(ws + L.part_o);
+  a.part_ml = reinterpret_cast<float2*>(ws + L.part_ml);
+  a.out = static_cast<uint16_t*>(out);
+  a.o_ts = out_token_stride; a.o_hs = out_head_stride;
+  a.waves = waves;
+  hipStream_t s = (hipStream_t)stream;
+  mla_attn_kernel<<<waves, 256, 0, s>>>(a);
+  if (int rc = check_hip(hipGetLastError(), "mla_attn_kernel launch")) return rc;
+  if (flags & AIA_ATTN_SKIP_MERGE) return AIA_OK;
+  return launch_merge(ws, L, g, kMlaV, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs, s);
 }

@@ -212,3 +212,38 @@ def paged_attention_kernel_only(query, key_cache, value_cache, plan, scale, out=
     rows split over several waves are left unmerged)."""
     return paged_attention_gqa(query, key_cache, value_cache, plan, scale, out,
                                flags=ATTN_SKIP_MERGE)
+
+
+MLA_LATENT, MLA_ROPE = 512, 64
+
+
+def paged_attention_mla(q_latent, latent_cache, plan, scale, out=None, flags=0):
+    """Absorbed-MLA latent attention (reference mla.py:76-122 semantics).
+
+    q_latent (T, H, 576) bf16 = [W_UK-absorbed nope (512), rope (64)];
+    latent_cache (NB, bs, 1, 576) bf16 contiguous; ``plan`` an
+    ``AttentionPlan`` made with (num_q_heads=H, num_kv_heads=1,
+    head_dim_v=512).  Returns the latent output (T, H, 512) bf16, i.e. the
+    first kv_lora_rank values of attention with V = K.
+    """
+    _check_device_tensor(q_latent, "q_latent", _BF16)
+    _check_device_tensor(latent_cache, "latent_cache", _BF16)
+    _require(q_latent.dim() == 3 and q_latent.stride(2) == 1,
+             "q_latent must be (T, H, 576), last dim contiguous")
+    T, h, dk = q_latent.shape
+    _require(dk == MLA_LATENT + MLA_ROPE, "q_latent last dim must be 576")
+    _require(latent_cache.dim() == 4 and latent_cache.is_contiguous() and
+             latent_cache.shape[2] == 1 and latent_cache.shape[3] == dk,
+             "latent_cache must be contiguous (num_blocks, block_size, 1, 576)")
+    nb, bs = latent_cache.shape[0], latent_cache.shape[1]
+    _require(h == plan.num_q_heads and plan.num_kv_heads == 1 and plan.head_dim_v == MLA_LATENT
+             and T == plan.num_tokens, "plan was not made for this MLA shape")
+    if out is None:
+        out = torch.empty(T, h, MLA_LATENT, dtype=_BF16, device=q_latent.device)
+    _native.call("aia_paged_attention_mla", _ptr(q_latent), q_latent.stride(0),
+                 q_latent.stride(1), _ptr(latent_cache), _ptr(plan.block_table),
+                 plan.block_table.stride(0), _ptr(plan.cu_seqlens_q), _ptr(plan.seqlens_kv),
+                 plan.batch, T, h, MLA_LATENT, MLA_ROPE, bs, nb, float(scale), _ptr(out),
+                 out.stride(0), out.stride(1), plan.num_waves, flags, _ptr(plan.workspace),
+                 plan.workspace.numel(), _stream(q_latent.device))
+    return out

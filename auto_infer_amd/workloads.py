@@ -114,3 +114,64 @@ def config1_decode(seed=0, device="cpu", num_blocks=512):
     return make_gqa_step(lqs=[1] * 16, lks=lks, num_q_heads=16, num_kv_heads=8,
                          block_size=128, num_blocks=num_blocks, seed=seed + 1,
                          device=device, value_scale=1.0 / math.sqrt(128))
+
+
+@dataclass
+class MlaStep:
+    q_latent: torch.Tensor        # (T, H, 576) = [absorbed nope (512), rope (64)]
+    latent_new: torch.Tensor      # (T, 1, 576) this step's latent rows
+    cache: torch.Tensor           # (NB, bs, 1, 576)
+    block_table: torch.Tensor
+    cu_seqlens_q: list
+    seqlens_kv: list
+    slot_mapping: torch.Tensor
+    scale: float
+
+    @property
+    def num_tokens(self):
+        return self.q_latent.shape[0]
+
+    def kv_bytes_read(self):
+        return sum(self.seqlens_kv) * self.cache.shape[-1] * self.cache.element_size()
+
+    def to(self, device):
+        for name in ("q_latent", "latent_new", "cache", "block_table", "slot_mapping"):
+            setattr(self, name, getattr(self, name).to(device))
+        return self
+
+
+def make_mla_step(*, lqs, lks, num_heads=16, block_size=128, num_blocks=None, seed=0,
+                  extra_blocks=0, dtype=torch.bfloat16, scale=192 ** -0.5):
+    """Absorbed-MLA step (latent 512 + rope 64 per token, one KV head)."""
+    rng = np.random.default_rng(seed)
+    need = sum((lk + block_size - 1) // block_size for lk in lks)
+    if num_blocks is None:
+        num_blocks = need + extra_blocks
+    tables = _block_tables(rng, lks, block_size, num_blocks)
+    width = max((len(t) for t in tables), default=0)
+    bt = np.zeros((len(lks), max(width, 1)), dtype=np.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = t
+    gen = torch.Generator().manual_seed(seed)
+    T = sum(lqs)
+    q = torch.randn(T, num_heads, 576, generator=gen).to(dtype)
+    lat = torch.randn(T, 1, 576, generator=gen).to(dtype)
+    cache = torch.randn(num_blocks, block_size, 1, 576, generator=gen).to(dtype)
+    slots, cu, acc = [], [], 0
+    for b, (lq, lk) in enumerate(zip(lqs, lks)):
+        for p in range(lk - lq, lk):
+            slots.append(bt[b, p // block_size] * block_size + p % block_size)
+        acc += lq
+        cu.append(acc)
+    return MlaStep(q_latent=q, latent_new=lat, cache=cache, block_table=torch.from_numpy(bt),
+                   cu_seqlens_q=cu, seqlens_kv=list(lks),
+                   slot_mapping=torch.tensor(slots, dtype=torch.int32), scale=scale)
+
+
+def config3_mla(seed=0):
+    """absorbed MLA, 16 heads, latent 512 + rope 64,
+    block 128, batch 64, query length 1, contexts log-uniform [512, 8192],
+    values N(0,1), scale 1/sqrt(192)."""
+    rng = np.random.default_rng(seed)
+    lks = np.exp(rng.uniform(np.log(512), np.log(8192), size=64)).astype(int).tolist()
+    return make_mla_step(lqs=[1] * 64, lks=lks, num_heads=16, block_size=128, seed=seed + 1)

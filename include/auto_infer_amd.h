@@ -99,6 +99,29 @@ int aia_paged_attention_gqa(const void* query, int64_t q_token_stride,
                             int32_t flags, void* workspace, int64_t workspace_bytes,
                             void* stream);
 
+/* Absorbed-MLA paged attention over a planned step.  Replaces the FIA call of
+ * mla_paged_absorbed (reference auto_infer/layers/attention/mla.py:76-122,
+ * from MlaFIABackend.attention :221-241): one KV head holding the 576-wide
+ * latent (kv_lora_rank 512 + rope 64) per token, V = K, output keeps the
+ * first kv_lora_rank values (mla.py:114-120); same causal / paging rules as
+ * the GQA entry.
+ * q_latent:     (num_tokens, num_heads, 576), token/head strides given.
+ * latent_cache: contiguous (num_blocks, block_size, 1, 576).
+ * out:          (num_tokens, num_heads, 512).
+ * The plan must come from aia_attn_plan(num_q_heads = num_heads,
+ * num_kv_heads = 1, head_dim_v = 512, same num_waves). */
+int aia_paged_attention_mla(const void* q_latent, int64_t q_token_stride,
+                            int64_t q_head_stride, const void* latent_cache,
+                            const int32_t* block_table, int32_t block_table_stride,
+                            const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
+                            int32_t batch, int32_t num_tokens, int32_t num_heads,
+                            int32_t kv_lora_rank, int32_t rope_dim,
+                            int32_t block_size, int32_t num_blocks, float scale,
+                            void* out, int64_t out_token_stride,
+                            int64_t out_head_stride, int32_t num_waves,
+                            int32_t flags, void* workspace, int64_t workspace_bytes,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,70 @@
+"""GQA paged attention backend on the gfx950 kernels.
+
+``GqaHipBackend`` is a drop-in for the reference's ``GqaFIABackend``
+(auto_infer/layers/attention/gqa.py:52-94): same constructor arguments,
+same KV-cache layout ``(2, num_blocks, block_size, n_kv, head_dim)`` per
+layer (gqa.py:69-74), same sub-block math around the op pair (packed qkv
+projection, optional Qwen3 QK-RMSNorm, NeoX RoPE, o_proj; gqa.py:27-49) and
+the same op-pair seam ``_write_kv`` / ``_attn``.  Only the op pair differs:
+the KV slot write and the split-K paged attention run as HIP kernels.
+The backend is graph-capturable (no host sync, no allocation in ``_attn``
+once the step's plan exists), so it serves both the "paged" and "graph"
+modes.
+"""
+import torch
+
+from auto_infer_amd import ops
+from auto_infer_amd.attention.base import AttentionBackend
+from auto_infer_amd.attention.layers import lin, rms_norm, rotate_half
+from auto_infer_amd.attention.metadata import step_plan
+
+
+class GqaHipBackend(AttentionBackend):
+
+    def __init__(self, n_q_heads: int, n_kv_heads: int, head_dim: int, scale: float,
+                 num_layers: int, device, dtype, w: dict = None, layer_prefix=None,
+                 rms_eps=None):
+        self.n_q_heads = n_q_heads
+        self.n_kv_heads = n_kv_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_layers = num_layers
+        self.device = device
+        self.dtype = dtype
+        self.w = w
+        self.layer_prefix = layer_prefix or (lambda i: f"model.layers.{i}.")
+        self.rms_eps = rms_eps
+
+    def alloc_kv_caches(self, num_blocks: int, block_size: int) -> list:
+        shape = (2, num_blocks, block_size, self.n_kv_heads, self.head_dim)
+        return [torch.zeros(shape, device=self.device, dtype=self.dtype)
+                for _ in range(self.num_layers)]
+
+    def attention(self, layer_idx: int, x: torch.Tensor, ctx) -> torch.Tensor:
+        T = x.shape[0]
+        n_q, n_kv, hd = self.n_q_heads, self.n_kv_heads, self.head_dim
+        w = self.w
+        p = self.layer_prefix(layer_idx) + "self_attn."
+        qkv = lin(x, w[p + "qkv_proj.weight"], w.get(p + "qkv_proj.bias"))
+        q, k, v = qkv.split((n_q * hd, n_kv * hd, n_kv * hd), dim=-1)
+        q = q.view(T, n_q, hd)
+        k = k.view(T, n_kv, hd)
+        v = v.view(T, n_kv, hd)
+        qn = w.get(p + "q_norm.weight")
+        if qn is not None:
+            q = rms_norm(q, qn, self.rms_eps)
+            k = rms_norm(k, w[p + "k_norm.weight"], self.rms_eps)
+        q = q * ctx.cos + rotate_half(q) * ctx.sin
+        k = k * ctx.cos + rotate_half(k) * ctx.sin
+        self._write_kv(layer_idx, k, v, ctx)
+        o = self._attn(layer_idx, q, k, v, ctx).reshape(T, n_q * hd)
+        return lin(o, w[p + "o_proj.weight"])
+
+    def _write_kv(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor, ctx) -> None:
+        cache = ctx.kv_caches[layer_idx]
+        ops.write_kv(k, v, cache[0], cache[1], ctx.slot_mapping)
+
+    def _attn(self, layer_idx: int, q, k, v, ctx) -> torch.Tensor:
+        cache = ctx.kv_caches[layer_idx]
+        plan = step_plan(ctx, self.n_q_heads, self.n_kv_heads, self.head_dim)
+        return ops.paged_attention_gqa(q, cache[0], cache[1], plan, self.scale)

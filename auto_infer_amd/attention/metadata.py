@@ -1,0 +1,41 @@
+"""Per-step device metadata shared by every layer of a step.
+
+The reference hands the attention op host lists (``ctx.cu_seqlens_q``
+cumulative ends, ``ctx.seqlens_kv`` per request; forward_context.py:14-15)
+and a device block table.  Our kernels read device int32 copies and a
+split-K plan; both depend only on the step, so they are built once per
+``ForwardContext`` (on first use, or by the GPU packer which attaches them
+as ``ctx.aia_cu_seqlens_q`` / ``ctx.aia_seqlens_kv``) and cached on it.
+"""
+import torch
+
+from auto_infer_amd import ops
+
+
+def step_plan(ctx, num_q_heads, num_kv_heads, head_dim_v):
+    plans = getattr(ctx, "_aia_plans", None)
+    if plans is None:
+        plans = {}
+        ctx._aia_plans = plans
+    key = (num_q_heads, num_kv_heads, head_dim_v)
+    plan = plans.get(key)
+    if plan is not None:
+        return plan
+    bt = ctx.block_table
+    cu = getattr(ctx, "aia_cu_seqlens_q", None)
+    kv = getattr(ctx, "aia_seqlens_kv", None)
+    if cu is None or kv is None:
+        dev = bt.device
+        cu = torch.tensor([0, *ctx.cu_seqlens_q], dtype=torch.int32).to(dev)
+        kv = torch.tensor(list(ctx.seqlens_kv), dtype=torch.int32).to(dev)
+        ctx.aia_cu_seqlens_q, ctx.aia_seqlens_kv = cu, kv
+    T = int(ctx.cu_seqlens_q[-1]) if len(ctx.cu_seqlens_q) else 0
+    if bt.dtype != torch.int32:
+        bt = bt.to(torch.int32)
+    plan = ops.AttentionPlan(bt, cu, kv, T, num_q_heads, num_kv_heads, head_dim_v,
+                             workspace=ops.DEFAULT_WORKSPACE.get(
+                                 bt.device, ops.workspace_bytes(kv.shape[0], T, num_q_heads,
+                                                                num_kv_heads, head_dim_v),
+                                 tag=key))
+    plans[key] = plan
+    return plan

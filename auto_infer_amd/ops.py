@@ -87,17 +87,19 @@ def write_kv(key, value, key_cache, value_cache, slot_mapping):
 # ---------------------------------------------------------------- attention
 
 class Workspace:
-    """Grow-only device scratch buffer (one per device), owned by torch."""
+    """Grow-only device scratch buffers owned by torch, one per (device,
+    tag).  Consecutive steps reuse a buffer in stream order; distinct plans
+    that live at the same time must use distinct tags."""
 
     def __init__(self):
         self._buf = {}
 
-    def get(self, device, nbytes):
-        dev = torch.device(device)
-        buf = self._buf.get(dev)
+    def get(self, device, nbytes, tag=None):
+        key = (torch.device(device), tag)
+        buf = self._buf.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
-            self._buf[dev] = buf
+            buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=key[0])
+            self._buf[key] = buf
         return buf
 
 

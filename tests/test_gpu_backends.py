@@ -1,0 +1,164 @@
+"""Backends through the reference's seam on the GPU.
+
+Each backend runs ``attention(layer_idx, x, ctx)`` end to end; a twin
+backend whose op pair (``_write_kv`` / ``_attn``) is the CPU oracle runs the
+identical torch code around it.  KV caches must match bit for bit and the
+attention op outputs within 2e-2 max-abs.
+"""
+import pytest
+import torch
+
+from auto_infer_amd.attention.base import ForwardContext
+from auto_infer_amd.attention.gqa import GqaHipBackend
+from auto_infer_amd.attention.mla import MlaHipBackend
+from oracle.paged_attn import kv_write, mla_absorbed_attention, paged_attention
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+TOL = 2e-2
+
+
+def rope_tables(positions, dim, base=10000.0):
+    inv = 1.0 / (base ** (torch.arange(0, dim, 2, dtype=torch.float32) / dim))
+    f = positions.float()[:, None] * inv[None]
+    emb = torch.cat([f, f], dim=-1)
+    return emb.cos()[:, None].bfloat16(), emb.sin()[:, None].bfloat16()
+
+
+def make_ctx(backend, caches, plan_rows, block_size):
+    """plan_rows: list of (start, n, block_ids) per request."""
+    slots, pos, cu, kv, acc = [], [], [], [], 0
+    width = max(len(r[2]) for r in plan_rows)
+    bt = torch.zeros(len(plan_rows), width, dtype=torch.int32)
+    for i, (start, n, blocks) in enumerate(plan_rows):
+        bt[i, :len(blocks)] = torch.tensor(blocks)
+        for p in range(start, start + n):
+            slots.append(blocks[p // block_size] * block_size + p % block_size)
+            pos.append(p)
+        acc += n
+        cu.append(acc)
+        kv.append(start + n)
+    positions = torch.tensor(pos)
+    return ForwardContext(
+        token_ids=torch.zeros(acc, dtype=torch.long, device=DEV), positions=positions.to(DEV),
+        slot_mapping=torch.tensor(slots, dtype=torch.int32, device=DEV), block_table=bt.to(DEV),
+        cu_seqlens_q=cu, seqlens_kv=kv, attn_mask=None, attn_backend=backend,
+        kv_caches=caches, is_decode=all(n == 1 for _, n, _ in plan_rows)), positions
+
+
+class _Capture:
+    def __init__(self):
+        self.outs = []
+
+
+def oracle_twin(cls):
+    class Twin(cls):
+        captured = None
+
+        def _write_kv(self, layer_idx, k, v, ctx):
+            cache = ctx.kv_caches[layer_idx]
+            if isinstance(cache, tuple):
+                c = cache[0].cpu()
+                kv_write(k.cpu(), None, c, None, ctx.slot_mapping.cpu())
+                cache[0].copy_(c)
+            else:
+                kc, vc = cache[0].cpu(), cache[1].cpu()
+                kv_write(k.cpu(), v.cpu(), kc, vc, ctx.slot_mapping.cpu())
+                cache[0].copy_(kc)
+                cache[1].copy_(vc)
+
+        def _attn(self, layer_idx, q, k, v, ctx):
+            cache = ctx.kv_caches[layer_idx]
+            bt = ctx.block_table.cpu()
+            if isinstance(cache, tuple):
+                o = mla_absorbed_attention(q.cpu(), cache[0].cpu(), bt, ctx.cu_seqlens_q,
+                                           ctx.seqlens_kv, self.softmax_scale, 512)
+            else:
+                o = paged_attention(q.cpu(), cache[0].cpu(), cache[1].cpu(), bt,
+                                    ctx.cu_seqlens_q, ctx.seqlens_kv, self.scale)
+            o = o.to(q.dtype).to(q.device)
+            self.captured.append(o)
+            return o
+    return Twin
+
+
+def run_pair(hip, twin, steps, caches_hip, caches_ref, block_size, hidden, seed):
+    g = torch.Generator().manual_seed(seed)
+    for rows in steps:
+        T = sum(n for _, n, _ in rows)
+        x = (torch.randn(T, hidden, generator=g) * 0.5).bfloat16().to(DEV)
+        ctx_h, positions = make_ctx(hip, caches_hip, rows, block_size)
+        ctx_r, _ = make_ctx(twin, caches_ref, rows, block_size)
+        rope_dim = getattr(hip, "qk_rope", None) or hip.head_dim
+        cos, sin = rope_tables(positions, rope_dim)
+        ctx_h.cos = ctx_r.cos = cos.to(DEV)
+        ctx_h.sin = ctx_r.sin = sin.to(DEV)
+        got_attn = []
+        orig = hip._attn
+
+        def spy(*a, **k):
+            o = orig(*a, **k)
+            got_attn.append(o)
+            return o
+        hip._attn = spy
+        twin.captured = []
+        out_h = hip.attention(0, x, ctx_h)
+        out_r = twin.attention(0, x, ctx_r)
+        hip._attn = orig
+        torch.cuda.synchronize()
+        for a, b in zip(caches_hip[0] if not isinstance(caches_hip[0], tuple) else caches_hip[0][:1],
+                        caches_ref[0] if not isinstance(caches_ref[0], tuple) else caches_ref[0][:1]):
+            assert torch.equal(a.cpu(), b.cpu()), "KV cache differs from the oracle's"
+        err = (got_attn[0].float() - twin.captured[0].float()).abs().max().item()
+        print(f"attention op max-abs err {err:.3e}", flush=True)
+        assert err <= TOL
+        scale = out_r.float().abs().max().item()
+        assert (out_h.float() - out_r.float()).abs().max().item() <= TOL * max(1.0, scale)
+
+
+def test_gqa_backend_prefill_then_decode_qwen3_style():
+    g = torch.Generator().manual_seed(0)
+    hq, hkv, d, hidden, bs = 4, 2, 128, 256, 16
+    p = "model.layers.0.self_attn."
+    w = {
+        p + "qkv_proj.weight": (torch.randn((hq + 2 * hkv) * d, hidden, generator=g) / 16).bfloat16(),
+        p + "q_norm.weight": (1 + 0.1 * torch.randn(d, generator=g)).bfloat16(),
+        p + "k_norm.weight": (1 + 0.1 * torch.randn(d, generator=g)).bfloat16(),
+        p + "o_proj.weight": (torch.randn(hidden, hq * d, generator=g) / 23).bfloat16(),
+    }
+    w = {k: v.to(DEV) for k, v in w.items()}
+    kw = dict(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, scale=d ** -0.5, num_layers=1,
+              device=DEV, dtype=torch.bfloat16, w=w, rms_eps=1e-6)
+    hip = GqaHipBackend(**kw)
+    twin = oracle_twin(GqaHipBackend)(**kw)
+    caches_h = hip.alloc_kv_caches(12, bs)
+    caches_r = twin.alloc_kv_caches(12, bs)
+    steps = [
+        [(0, 5, [3]), (0, 20, [7, 1])],            # prefill two prompts
+        [(5, 1, [3]), (20, 1, [7, 1])],            # decode
+        [(6, 11, [3, 9]), (21, 1, [7, 1])],        # chunked prefill continuation + decode
+    ]
+    run_pair(hip, twin, steps, caches_h, caches_r, bs, hidden, seed=1)
+
+
+def test_mla_backend_absorbed_prefill_then_decode():
+    g = torch.Generator().manual_seed(2)
+    nh, nope, rope, vd, kvl, hidden, bs = 4, 32, 64, 32, 512, 256, 16
+    p = "model.layers.0."
+    w = {
+        p + "self_attn.q_proj.weight": torch.randn(nh * (nope + rope), hidden, generator=g) / 16,
+        p + "self_attn.kv_a_proj_with_mqa.weight": torch.randn(kvl + rope, hidden, generator=g) / 16,
+        p + "self_attn.kv_a_layernorm.weight": 1 + 0.1 * torch.randn(kvl, generator=g),
+        p + "self_attn.kv_b_proj.weight": torch.randn(nh * (nope + vd), kvl, generator=g) / 22,
+        p + "self_attn.o_proj.weight": torch.randn(hidden, nh * vd, generator=g) / 11,
+    }
+    w = {k: v.bfloat16().to(DEV) for k, v in w.items()}
+    kw = dict(num_heads=nh, qk_nope=nope, qk_rope=rope, v_head_dim=vd, kv_lora_rank=kvl,
+              q_lora_rank=None, rms_eps=1e-6, softmax_scale=(nope + rope) ** -0.5,
+              num_layers=1, device=DEV, dtype=torch.bfloat16)
+    hip = MlaHipBackend(w, **kw)
+    twin = oracle_twin(MlaHipBackend)(w, **kw)
+    caches_h = hip.alloc_kv_caches(8, bs)
+    caches_r = twin.alloc_kv_caches(8, bs)
+    steps = [[(0, 7, [2]), (0, 18, [5, 0])], [(7, 1, [2]), (18, 1, [5, 0])]]
+    run_pair(hip, twin, steps, caches_h, caches_r, bs, hidden, seed=3)

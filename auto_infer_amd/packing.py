@@ -1,0 +1,614 @@
+"""Packing of a BatchPlan into device attention metadata, on the GPU.
+
+Host side of the ``aia_pack_rows`` kernel.  The reference packs every step
+on the host (numpy loops + H2D copies of every buffer): the eager runner's
+``_build`` (auto_infer/worker/model_runner.py:111-188) and the fixed-gear
+stagers (worker/decode_input_stager.py:74-123, :304-373,
+worker/prefill_input_stager.py:72-162).  Here the per-request state lives
+on the device in a ``DeviceRequestTable`` (block ids and token ids per
+request slot); a step uploads only what changed since the last step (new
+blocks, new tokens, drafts) plus one 8-int descriptor per row, in ONE
+host-to-device copy, and the kernel writes token_ids, positions,
+slot_mapping, the zero-padded block table, cu_seqlens_q, seqlens_kv and
+the sample rows.
+
+The classes keep the reference's names, constructor arguments, outputs and
+error messages (``DecodeInputStager``, ``SpecDecodeInputStager``,
+``PrefillInputStager`` and ``DeviceBatchPacker.build`` for ``_build``).
+Their ``copied_block_rows`` / ``copied_block_elements`` counters count what
+this design uploads (block ids appended to the device table), not host
+staging rows.
+"""
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from auto_infer_amd import _native
+from auto_infer_amd.attention.base import ForwardContext
+from auto_infer_amd.ops import _check_device_tensor, _ptr, _stream
+
+_ROW_INTS = 8
+
+
+class DeviceRequestTable:
+    """Per-request block ids and token ids, resident on the device.
+
+    ``block_pool`` int32 [slots, max_blocks], ``token_pool`` int64
+    [slots, max_len].  Slots are assigned on first sight of a request id and
+    recycled least-recently-used when the table is full (or on
+    ``release``).  Growth reallocates (amortised, like the reference's
+    ``_ensure_capacity``, model_runner.py:99-109).
+    """
+
+    def __init__(self, device, max_slots=64, max_blocks=64, max_len=4096):
+        self.device = torch.device(device)
+        self.block_pool = torch.zeros(max_slots, max_blocks, dtype=torch.int32, device=self.device)
+        self.token_pool = torch.zeros(max_slots, max_len, dtype=torch.int64, device=self.device)
+        self._slot = {}           # rid -> slot
+        self._blocks = {}         # rid -> tuple of synced block ids
+        self._ntok = {}           # rid -> number of synced leading token ids
+        self._last_use = {}       # rid -> step counter
+        self._free = list(range(max_slots - 1, -1, -1))
+        self._step = 0
+        self.uploaded_block_rows = 0
+        self.uploaded_block_elements = 0
+
+    # -- capacity ---------------------------------------------------------
+    def _grow(self, slots=None, blocks=None, tokens=None):
+        s0, b0 = self.block_pool.shape
+        t0 = self.token_pool.shape[1]
+        s1 = max(s0, slots or 0)
+        b1 = max(b0, blocks or 0)
+        t1 = max(t0, tokens or 0)
+        if (s1, b1) != (s0, b0):
+            bp = torch.zeros(s1, b1, dtype=torch.int32, device=self.device)
+            bp[:s0, :b0] = self.block_pool
+            self.block_pool = bp
+        if (s1, t1) != (s0, t0):
+            tp = torch.zeros(s1, t1, dtype=torch.int64, device=self.device)
+            tp[:s0, :t0] = self.token_pool
+            self.token_pool = tp
+        if s1 > s0:
+            self._free = list(range(s1 - 1, s0 - 1, -1)) + self._free
+
+    def release(self, rid):
+        slot = self._slot.pop(rid, None)
+        if slot is not None:
+            self._free.append(slot)
+        self._blocks.pop(rid, None)
+        self._ntok.pop(rid, None)
+        self._last_use.pop(rid, None)
+
+    def _slot_for(self, rid, live):
+        slot = self._slot.get(rid)
+        if slot is None:
+            if not self._free:
+                idle = [r for r in self._slot if r not in live]
+                if idle:
+                    self.release(min(idle, key=lambda r: self._last_use[r]))
+                else:
+                    n = self.block_pool.shape[0]
+                    self._grow(slots=2 * n)
+            slot = self._free.pop()
+            self._slot[rid] = slot
+        self._last_use[rid] = self._step
+        return slot
+
+    # -- per-step sync ----------------------------------------------------
+    def begin_step(self):
+        self._step += 1
+        return _Updates()
+
+    def sync(self, upd, rid, req, blocks, upto, live, drafts=()):
+        """Make slot rows hold ``blocks`` and token ids [0, upto) of the
+        request (drafts written right after position upto - 1 - len(drafts)
+        + 1, i.e. at the query positions they occupy); returns the slot."""
+        slot = self._slot_for(rid, live)
+        nb = len(blocks)
+        if nb > self.block_pool.shape[1]:
+            self._grow(blocks=max(nb, 2 * self.block_pool.shape[1]))
+        if upto > self.token_pool.shape[1]:
+            self._grow(tokens=max(upto, 2 * self.token_pool.shape[1]))
+        prev = self._blocks.get(rid)
+        if prev is not None and len(prev) <= nb and tuple(blocks[:len(prev)]) == prev:
+            first = len(prev)
+        else:
+            first = 0
+        if first < nb:
+            upd.blk_slot.extend([slot] * (nb - first))
+            upd.blk_idx.extend(range(first, nb))
+            upd.blk_val.extend(blocks[first:nb])
+            self.uploaded_block_rows += 1
+            self.uploaded_block_elements += nb - first
+            self._blocks[rid] = tuple(blocks)
+        elif prev is None:
+            self._blocks[rid] = tuple(blocks)
+        ids = req.all_token_ids
+        have = self._ntok.get(rid, 0)
+        real_hi = min(upto - len(drafts), len(ids))
+        if real_hi > have:
+            upd.tok_slot.extend([slot] * (real_hi - have))
+            upd.tok_idx.extend(range(have, real_hi))
+            upd.tok_val.extend(ids[have:real_hi])
+            self._ntok[rid] = real_hi
+        if drafts:
+            base = upto - len(drafts)
+            upd.tok_slot.extend([slot] * len(drafts))
+            upd.tok_idx.extend(range(base, base + len(drafts)))
+            upd.tok_val.extend(drafts)
+            # drafted positions are not real tokens: resync them later
+            self._ntok[rid] = min(self._ntok.get(rid, 0), upto - len(drafts))
+        return slot
+
+
+class _Updates:
+    """One step's changes: pool entries as (slot, column, value) -- flattened
+    only at upload time, after any pool growth -- and the row descriptors."""
+
+    def __init__(self):
+        self.tok_slot, self.tok_idx, self.tok_val = [], [], []
+        self.blk_slot, self.blk_idx, self.blk_val = [], [], []
+        self.rows = []
+
+    def row(self, slot, start, n, nblocks, base, q_off, zero_tokens, sample_slot):
+        self.rows.append((slot, start, n, nblocks, base, q_off, zero_tokens, sample_slot))
+
+
+class _Uploader:
+    """Pinned host staging -> one device buffer per step.  Two host buffers
+    alternate; before one is rewritten, the copy that last read it is waited
+    for (an event), so a step never overwrites bytes still in flight."""
+
+    def __init__(self, device):
+        self.device = torch.device(device)
+        self._host = [None, None]
+        self._event = [None, None]
+        self._dev = None
+        self._turn = 0
+
+    def upload(self, upd, token_width, block_width):
+        nt, nb, nr = len(upd.tok_idx), len(upd.blk_idx), len(upd.rows)
+        sizes = [nt * 8, nt * 8, nb * 8, nb * 4, nr * _ROW_INTS * 4]
+        offs, total = [], 0
+        for s in sizes:
+            offs.append(total)
+            total += (s + 15) & ~15
+        total = max(total, 16)
+        i = self._turn
+        self._turn ^= 1
+        if self._event[i] is not None:
+            self._event[i].synchronize()
+        host = self._host[i]
+        if host is None or host.numel() < total:
+            cap = max(total * 2, 4096)
+            host = torch.empty(cap, dtype=torch.uint8, pin_memory=self.device.type == "cuda")
+            self._host[i] = host
+        if self._dev is None or self._dev.numel() < total:
+            self._dev = torch.empty(max(total * 2, 4096), dtype=torch.uint8, device=self.device)
+        h = host.numpy()
+        if nt:
+            h[offs[0]:offs[0] + nt * 8].view(np.int64)[:] = (
+                np.asarray(upd.tok_slot, dtype=np.int64) * token_width +
+                np.asarray(upd.tok_idx, dtype=np.int64))
+            h[offs[1]:offs[1] + nt * 8].view(np.int64)[:] = upd.tok_val
+        if nb:
+            h[offs[2]:offs[2] + nb * 8].view(np.int64)[:] = (
+                np.asarray(upd.blk_slot, dtype=np.int64) * block_width +
+                np.asarray(upd.blk_idx, dtype=np.int64))
+            h[offs[3]:offs[3] + nb * 4].view(np.int32)[:] = upd.blk_val
+        if nr:
+            h[offs[4]:offs[4] + nr * _ROW_INTS * 4].view(np.int32)[:] = np.asarray(
+                upd.rows, dtype=np.int32).reshape(-1)
+        self._dev[:total].copy_(host[:total], non_blocking=True)
+        if self.device.type == "cuda":
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(self.device))
+            self._event[i] = ev
+        base = self._dev.data_ptr()
+        return [base + o for o in offs]
+
+
+@dataclass
+class PackedStep:
+    """Device outputs of one pack (views of persistent buffers)."""
+    token_ids: torch.Tensor
+    positions: torch.Tensor
+    slot_mapping: torch.Tensor
+    block_table: torch.Tensor
+    cu_seqlens_q: torch.Tensor     # (rows + 1,) int32 with leading 0
+    seqlens_kv: torch.Tensor       # (rows,) int32
+    last_rows: torch.Tensor        # (rows,) int64
+
+
+def _launch(table, uploader, upd, *, block_size, bt_width, token_ids, positions, slot_mapping,
+            block_table, cu, kv, last_rows, sample_rows=None, sample_count=0):
+    ptrs = uploader.upload(upd, table.token_pool.shape[1], table.block_pool.shape[1])
+    nt, nb, nr = len(upd.tok_idx), len(upd.blk_idx), len(upd.rows)
+    cap = sample_rows.numel() if sample_rows is not None else 0
+    _native.call(
+        "aia_pack_rows", ptrs[0], ptrs[1], nt, ptrs[2], ptrs[3], nb,
+        _ptr(table.token_pool), table.token_pool.shape[1], _ptr(table.block_pool),
+        table.block_pool.shape[1], ptrs[4], nr, block_size, bt_width, _ptr(token_ids),
+        _ptr(positions), _ptr(slot_mapping), _ptr(block_table), _ptr(cu), _ptr(kv),
+        _ptr(last_rows), _ptr(sample_rows), sample_count, cap, _stream(table.device))
+
+
+def _check_blocks(rid, blocks, end, block_size):
+    if end > len(blocks) * block_size:
+        raise ValueError(f"request {rid}: {len(blocks)} blocks cannot hold position {end - 1}")
+
+
+class DeviceBatchPacker:
+    """GPU version of the eager runner's per-step packing (``_build``,
+    model_runner.py:111-188): persistent grow-only device buffers, one
+    upload, one kernel; returns ``(ForwardContext, sample_idx,
+    decode_splice)`` like the reference, with the context's tensors as views
+    of the persistent buffers and the host lists ``cu_seqlens_q`` /
+    ``seqlens_kv`` it carries.  The device copies of those lists (and the
+    leading-0 cumulative form the attention kernels read) are attached as
+    ``ctx.aia_cu_seqlens_q`` / ``ctx.aia_seqlens_kv``."""
+
+    def __init__(self, block_size, device, table=None, max_num_batched_tokens=256,
+                 max_num_seqs=64, max_blocks=64):
+        self.block_size = block_size
+        self.device = torch.device(device)
+        self.table = table or DeviceRequestTable(self.device)
+        self._uploader = _Uploader(self.device)
+        self._tokens = self._seqs = self._blocks = 0
+        self._alloc(max_num_batched_tokens, max_num_seqs, max_blocks)
+
+    def _alloc(self, n_tokens, n_seqs, n_blocks):
+        n_tokens, n_seqs = max(n_tokens, self._tokens), max(n_seqs, self._seqs)
+        n_blocks = max(n_blocks, self._blocks)
+        dev = self.device
+        self.token_ids_buf = torch.zeros(n_tokens, dtype=torch.int64, device=dev)
+        self.positions_buf = torch.zeros(n_tokens, dtype=torch.int64, device=dev)
+        self.slot_mapping_buf = torch.zeros(n_tokens, dtype=torch.int32, device=dev)
+        self.block_table_buf = torch.zeros(n_seqs * n_blocks, dtype=torch.int32, device=dev)
+        self.cu_buf = torch.zeros(n_seqs + 1, dtype=torch.int32, device=dev)
+        self.kv_buf = torch.zeros(n_seqs, dtype=torch.int32, device=dev)
+        self.last_buf = torch.zeros(n_seqs, dtype=torch.int64, device=dev)
+        self._tokens, self._seqs, self._blocks = n_tokens, n_seqs, n_blocks
+
+    def build(self, plan, attn_backend=None, kv_caches=None, attn_mask=None):
+        bs = self.block_size
+        upd = self.table.begin_step()
+        live = {sr.request_id for sr in plan.scheduled}
+        cu, kv = [], []
+        sample_idx, decode_splice = {}, []
+        all_decode = True
+        qacc, width = 0, 0
+        for sr in plan.scheduled:
+            rid = sr.request_id
+            req = plan.get_request(rid)
+            n = sr.num_tokens_to_compute
+            start = req.num_computed_tokens
+            blocks = plan.block_tables[rid]
+            _check_blocks(rid, blocks, start + n, bs)
+            draft = tuple(getattr(req, "spec_draft", ()) or ())
+            drafts = draft if (draft and not sr.is_prefill) else ()
+            slot = self.table.sync(upd, rid, req, blocks, start + n, live, drafts)
+            upd.row(slot, start, n, len(blocks), 0, qacc, 0, -1)
+            npr = req.num_prompt_tokens
+            for li in range(max(npr - start, 0), n):          # positions >= prompt length
+                decode_splice.append((qacc + li, rid))
+            if start < npr:
+                all_decode = False
+            qacc += n
+            cu.append(qacc)
+            kv.append(start + n)
+            sample_idx[rid] = qacc - 1
+            width = max(width, len(blocks))
+        T, B = qacc, len(plan.scheduled)
+        if T > self._tokens or B > self._seqs or width > self._blocks:
+            self._alloc(T * 2 if T > self._tokens else T, B * 2 if B > self._seqs else B,
+                        width * 2 if width > self._blocks else width)
+        bt = self.block_table_buf[:B * width].view(B, width)
+        _launch(self.table, self._uploader, upd, block_size=bs, bt_width=width,
+                token_ids=self.token_ids_buf, positions=self.positions_buf,
+                slot_mapping=self.slot_mapping_buf, block_table=bt, cu=self.cu_buf,
+                kv=self.kv_buf, last_rows=self.last_buf)
+        ctx = ForwardContext(
+            token_ids=self.token_ids_buf[:T], positions=self.positions_buf[:T],
+            slot_mapping=self.slot_mapping_buf[:T], block_table=bt, cu_seqlens_q=cu,
+            seqlens_kv=kv, attn_mask=attn_mask, attn_backend=attn_backend,
+            kv_caches=kv_caches, is_decode=all_decode)
+        ctx.aia_cu_seqlens_q = self.cu_buf[:B + 1]
+        ctx.aia_seqlens_kv = self.kv_buf[:B]
+        return ctx, sample_idx, decode_splice
+
+
+# ---------------------------------------------------------------- stagers
+
+@dataclass(frozen=True)
+class StagedDecodeInput:
+    token_ids: torch.Tensor
+    positions: torch.Tensor
+    slots: torch.Tensor
+    block_table: torch.Tensor
+    kv_lengths: list
+    order: list
+    cu_seqlens_q: torch.Tensor = None
+    seqlens_kv: torch.Tensor = None
+
+    def data_ptrs(self):
+        return (self.token_ids.data_ptr(), self.positions.data_ptr(),
+                self.slots.data_ptr(), self.block_table.data_ptr())
+
+
+def _contig(t, name, dtype):
+    _check_device_tensor(t, name, dtype)
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+class _GearStager:
+    def __init__(self, device, table, rows):
+        self.table = table or DeviceRequestTable(device)
+        self._uploader = _Uploader(device)
+        self._cu = torch.zeros(rows + 1, dtype=torch.int32, device=device)
+        self._kv = torch.zeros(rows, dtype=torch.int32, device=device)
+        self._last = torch.zeros(rows, dtype=torch.int64, device=device)
+        self.copied_block_rows = 0
+        self.copied_block_elements = 0
+
+    def _count(self, before):
+        rows, elems = before
+        self.copied_block_rows += self.table.uploaded_block_rows - rows
+        self.copied_block_elements += self.table.uploaded_block_elements - elems
+
+    def _mark(self):
+        return self.table.uploaded_block_rows, self.table.uploaded_block_elements
+
+
+class DecodeInputStager(_GearStager):
+    """Fixed-address decode gear (reference decode_input_stager.py:35-123):
+    live row = (token at num_computed_tokens, that position, its slot, the
+    request's block row, kv length pos + 1); padding rows use scratch block
+    scratch0 + row, slot block * bs, token 0, position 0, kv length 1."""
+
+    def __init__(self, *, tid, positions, slots, block_table, block_size, scratch0,
+                 active_token_mask=None, table=None):
+        _contig(tid, "tid", torch.int64)
+        _contig(positions, "positions", torch.int64)
+        _contig(slots, "slots", torch.int32)
+        _contig(block_table, "block_table", torch.int32)
+        self.tid, self.positions, self.slots, self.block_table = tid, positions, slots, block_table
+        self.active_token_mask = active_token_mask
+        if active_token_mask is not None and (active_token_mask.dtype is not torch.bool or
+                                              tuple(active_token_mask.shape) != (tid.shape[0],)):
+            raise ValueError("decode active-token mask must be gear-shaped bool")
+        self.block_size = block_size
+        self.scratch0 = scratch0
+        self.gear = tid.shape[0]
+        self.max_blocks = block_table.shape[1]
+        super().__init__(tid.device, table, self.gear)
+
+    def stage(self, plan, scheduled=None):
+        scheduled = plan.scheduled if scheduled is None else scheduled
+        if len(scheduled) > self.gear:
+            raise ValueError(f"decode batch {len(scheduled)} exceeds gear {self.gear}")
+        mark = self._mark()
+        upd = self.table.begin_step()
+        live = {item.request_id for item in scheduled}
+        kv, order = [], []
+        for row, item in enumerate(scheduled):
+            rid = item.request_id
+            req = plan.get_request(rid)
+            pos = req.num_computed_tokens
+            blocks = plan.block_tables[rid]
+            if len(blocks) > self.max_blocks:
+                raise ValueError(f"request {rid} has {len(blocks)} blocks > {self.max_blocks}")
+            _check_blocks(rid, blocks, pos + 1, self.block_size)
+            slot = self.table.sync(upd, rid, req, blocks, pos + 1, live)
+            upd.row(slot, pos, 1, len(blocks), 0, row, 0, -1)
+            kv.append(pos + 1)
+            order.append(rid)
+        for row in range(len(scheduled), self.gear):
+            upd.row(-1, 0, 1, 1, self.scratch0 + row, row, 1, -1)
+            kv.append(1)
+        _launch(self.table, self._uploader, upd, block_size=self.block_size,
+                bt_width=self.max_blocks, token_ids=self.tid, positions=self.positions,
+                slot_mapping=self.slots, block_table=self.block_table, cu=self._cu,
+                kv=self._kv, last_rows=self._last)
+        if self.active_token_mask is not None:
+            self.active_token_mask[:len(scheduled)].fill_(True)
+            self.active_token_mask[len(scheduled):].fill_(False)
+        self._count(mark)
+        return StagedDecodeInput(self.tid, self.positions, self.slots, self.block_table, kv,
+                                 order, self._cu, self._kv)
+
+
+class SpecDecodeInputStager(_GearStager):
+    """MTP-verify gear (reference decode_input_stager.py:257-373): query_width
+    = draft_depth + 1 rows per request with tokens (last, *drafts),
+    positions pos + offset, kv length pos + width; padding request rows on
+    scratch block scratch0 + row with positions 0..width-1."""
+
+    def __init__(self, *, tid, positions, slots, block_table, drafts, block_size, scratch0,
+                 geometry=None, draft_depth=None, active_mask=None, active_token_mask=None,
+                 table=None):
+        if draft_depth is None:
+            draft_depth = geometry.draft_depth
+        self.draft_depth = draft_depth
+        self.query_width = draft_depth + 1
+        _contig(tid, "tid", torch.int64)
+        _contig(positions, "positions", torch.int64)
+        _contig(slots, "slots", torch.int32)
+        _contig(block_table, "block_table", torch.int32)
+        self.tid, self.positions, self.slots, self.block_table = tid, positions, slots, block_table
+        self.drafts = drafts
+        self.active_mask = active_mask
+        self.active_token_mask = active_token_mask
+        self.block_size = block_size
+        self.scratch0 = scratch0
+        self.gear, self.max_blocks = block_table.shape
+        if tid.numel() != self.gear * self.query_width:
+            raise ValueError("spec decode token buffer must match the configured query width")
+        if active_mask is not None and tuple(active_mask.shape) != (self.gear,):
+            raise ValueError("spec active mask must have one row per request")
+        super().__init__(tid.device, table, self.gear)
+        self._draft_host = torch.zeros(tuple(drafts.shape), dtype=torch.int64,
+                                       pin_memory=tid.is_cuda)
+        self._draft_event = None
+
+    def stage(self, plan, scheduled=None):
+        scheduled = plan.scheduled if scheduled is None else scheduled
+        if len(scheduled) > self.gear:
+            raise ValueError(f"spec decode batch {len(scheduled)} exceeds gear {self.gear}")
+        mark = self._mark()
+        upd = self.table.begin_step()
+        live = {item.request_id for item in scheduled}
+        w = self.query_width
+        kv, order = [], []
+        if self._draft_event is not None:
+            self._draft_event.synchronize()
+        dh = self._draft_host.numpy()
+        dh.fill(0)
+        for row, item in enumerate(scheduled):
+            rid = item.request_id
+            req = plan.get_request(rid)
+            pos = req.num_computed_tokens
+            blocks = plan.block_tables[rid]
+            if len(req.spec_draft) != self.draft_depth:
+                raise ValueError(f"request {rid} has {len(req.spec_draft)} drafts; "
+                                 f"expected {self.draft_depth}")
+            _check_blocks(rid, blocks, pos + w, self.block_size)
+            slot = self.table.sync(upd, rid, req, blocks, pos + w, live, tuple(req.spec_draft))
+            upd.row(slot, pos, w, len(blocks), 0, row * w, 0, -1)
+            dh[row] = req.spec_draft
+            kv.append(pos + w)
+            order.append(rid)
+        for row in range(len(scheduled), self.gear):
+            upd.row(-1, 0, w, 1, self.scratch0 + row, row * w, 1, -1)
+            kv.append(w)
+        _launch(self.table, self._uploader, upd, block_size=self.block_size,
+                bt_width=self.max_blocks, token_ids=self.tid, positions=self.positions,
+                slot_mapping=self.slots, block_table=self.block_table, cu=self._cu,
+                kv=self._kv, last_rows=self._last)
+        self.drafts.copy_(self._draft_host, non_blocking=True)
+        if self.drafts.is_cuda:
+            self._draft_event = torch.cuda.Event()
+            self._draft_event.record(torch.cuda.current_stream(self.drafts.device))
+        if self.active_mask is not None:
+            self.active_mask[:len(scheduled)].fill_(1)
+            self.active_mask[len(scheduled):].fill_(0)
+        if self.active_token_mask is not None:
+            self.active_token_mask[:len(scheduled) * w].fill_(True)
+            self.active_token_mask[len(scheduled) * w:].fill_(False)
+        self._count(mark)
+        return StagedDecodeInput(self.tid, self.positions, self.slots, self.block_table, kv,
+                                 order, self._cu, self._kv)
+
+
+@dataclass(frozen=True)
+class StagedPrefillInput:
+    token_ids: torch.Tensor
+    positions: torch.Tensor
+    slots: torch.Tensor
+    block_table: torch.Tensor
+    sample_rows: torch.Tensor
+    cumulative_query_lengths: list
+    kv_lengths: list
+    sample_order: list
+    splice_order: list
+    splice_rows: list
+    query_tokens: int
+    real_query_tokens: int
+    sequence_count: int
+    cu_seqlens_q: torch.Tensor = None
+    seqlens_kv: torch.Tensor = None
+
+    def data_ptrs(self):
+        return (self.token_ids.data_ptr(), self.positions.data_ptr(), self.slots.data_ptr(),
+                self.block_table.data_ptr(), self.sample_rows.data_ptr())
+
+
+class PrefillInputStager(_GearStager):
+    """Flattened-token prefill/mixed gear (reference prefill_input_stager.py:
+    35-162): rows packed request after request, cumulative query lengths,
+    kv length start + n, sample rows for requests whose chunk completes the
+    prefill, and one padding pseudo-sequence on scratch blocks scratch0 + k
+    covering the token-gear slack."""
+
+    def __init__(self, *, token_ids, positions, slots, block_table, sample_rows, block_size,
+                 scratch0, active_token_mask=None, table=None):
+        _contig(token_ids, "token_ids", torch.int64)
+        _contig(positions, "positions", torch.int64)
+        _contig(slots, "slots", torch.int32)
+        _contig(block_table, "block_table", torch.int32)
+        _contig(sample_rows, "sample_rows", torch.int64)
+        self.token_ids, self.positions, self.slots = token_ids, positions, slots
+        self.block_table, self.sample_rows = block_table, sample_rows
+        self.active_token_mask = active_token_mask
+        if active_token_mask is not None and (active_token_mask.dtype is not torch.bool or
+                                              tuple(active_token_mask.shape) !=
+                                              (token_ids.shape[0],)):
+            raise ValueError("prefill active-token mask must be gear-shaped bool")
+        self.block_size = block_size
+        self.scratch0 = scratch0
+        self.query_gear = token_ids.shape[0]
+        self.sequence_gear = sample_rows.shape[0]
+        self.max_blocks = block_table.shape[1]
+        super().__init__(token_ids.device, table, block_table.shape[0])
+
+    def stage(self, plan):
+        scheduled = plan.scheduled
+        real = sum(item.num_tokens_to_compute for item in scheduled)
+        nseq = len(scheduled)
+        if real > self.query_gear or nseq > self.sequence_gear:
+            raise ValueError(
+                f"batch ({real} tokens, {nseq} sequences) "
+                f"exceeds prefill gear ({self.query_gear}, {self.sequence_gear})")
+        if not scheduled:
+            raise ValueError("prefill staging requires at least one sequence")
+        mark = self._mark()
+        upd = self.table.begin_step()
+        live = {item.request_id for item in scheduled}
+        cu, kv, sample_order, splice_order, splice_rows = [], [], [], [], []
+        q = 0
+        for item in scheduled:
+            rid = item.request_id
+            req = plan.get_request(rid)
+            start = req.num_computed_tokens
+            n = item.num_tokens_to_compute
+            blocks = plan.block_tables[rid]
+            _check_blocks(rid, blocks, start + n, self.block_size)
+            slot = self.table.sync(upd, rid, req, blocks, start + n, live)
+            sample = -1
+            if start + n >= req.num_prefill_tokens:
+                sample = len(sample_order)
+                sample_order.append(rid)
+            upd.row(slot, start, n, len(blocks), 0, q, 0, sample)
+            q += n
+            cu.append(q)
+            kv.append(start + n)
+            splice_order.append(rid)
+            splice_rows.append(q - 1)
+        padding = self.query_gear - real
+        if padding:
+            nblk = (padding + self.block_size - 1) // self.block_size
+            upd.row(-1, 0, padding, nblk, self.scratch0, q, 1, -1)
+            cu.append(self.query_gear)
+            kv.append(padding)
+        rows = nseq + int(bool(padding))
+        if rows > self.block_table.shape[0]:
+            raise ValueError(f"batch ({real} tokens, {nseq} sequences) "
+                             f"exceeds prefill gear ({self.query_gear}, {self.sequence_gear})")
+        _launch(self.table, self._uploader, upd, block_size=self.block_size,
+                bt_width=self.max_blocks, token_ids=self.token_ids, positions=self.positions,
+                slot_mapping=self.slots, block_table=self.block_table, cu=self._cu,
+                kv=self._kv, last_rows=self._last, sample_rows=self.sample_rows,
+                sample_count=len(sample_order))
+        # rows past the attention sequences keep zeros (reference fills them)
+        if rows < self.block_table.shape[0]:
+            self.block_table[rows:].zero_()
+        if self.active_token_mask is not None:
+            self.active_token_mask[:real].fill_(True)
+            self.active_token_mask[real:].fill_(False)
+        self._count(mark)
+        return StagedPrefillInput(
+            self.token_ids, self.positions, self.slots, self.block_table[:rows],
+            self.sample_rows, cu, kv, sample_order, splice_order, splice_rows,
+            self.query_gear, real, nseq, self._cu[:rows + 1], self._kv[:rows])

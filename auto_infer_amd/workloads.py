@@ -175,3 +175,21 @@ def config3_mla(seed=0):
     rng = np.random.default_rng(seed)
     lks = np.exp(rng.uniform(np.log(512), np.log(8192), size=64)).astype(int).tolist()
     return make_mla_step(lqs=[1] * 64, lks=lks, num_heads=16, block_size=128, seed=seed + 1)
+
+
+def fragmented_block_tables(lks, *, num_blocks, block_size, ops=10000, seed=0):
+    """Block tables for requests of context lengths ``lks`` drawn from an
+    allocator that first ran a seeded trace of ``ops`` allocate/free
+    operations, so the tables are non-contiguous."""
+    from auto_infer_amd.kv_cache_manager import KVCacheManager
+    rng = np.random.default_rng(seed)
+    kv = KVCacheManager(num_blocks, block_size)
+    live = []
+    for _ in range(ops):
+        if live and (rng.random() < 0.45 or kv.num_free_blocks() < num_blocks // 4):
+            kv.free(live.pop(int(rng.integers(len(live)))))
+        else:
+            n = int(min(32768, max(1, rng.lognormal(np.log(2048), 1.0))))
+            if kv.can_allocate(n):
+                live.append(kv.allocate(n))
+    return [kv.allocate(lk) for lk in lks], kv

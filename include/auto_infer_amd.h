@@ -122,6 +122,37 @@ int aia_paged_attention_mla(const void* q_latent, int64_t q_token_stride,
                             int32_t flags, void* workspace, int64_t workspace_bytes,
                             void* stream);
 
+/* Ragged-batch packing of one step's rows into attention metadata.
+ * Replaces the host packing loops of the reference: NpuModelRunner._build
+ * (auto_infer/worker/model_runner.py:111-188), DecodeInputStager.stage
+ * (worker/decode_input_stager.py:74-123), SpecDecodeInputStager.stage
+ * (:304-373) and PrefillInputStager.stage (worker/prefill_input_stager.py:
+ * 72-162), with slot = block_table[pos / bs] * bs + pos % bs
+ * (engine/token_layout.py:1-4).
+ * Pools (device, caller-owned): token_pool int64 [slots][token_pool_stride],
+ * block_pool int32 [slots][block_pool_stride].  First the given updates are
+ * scattered (flat indices into the pools), then each row is packed.
+ * rows: device int32 [num_rows][8] =
+ *   {slot (-1 = synthetic scratch row), start, n, num_blocks, first scratch
+ *    block (synthetic rows), first query row (cumulative offset),
+ *    zero_tokens, sample slot (-1 = none)}.
+ * Outputs: token_ids/positions int64 [T], slot_mapping int32 [T],
+ * block_table int32 [num_rows][block_table_width] zero padded,
+ * cu_seqlens_q int32 [num_rows + 1] (leading 0), seqlens_kv int32
+ * [num_rows] = start + n, last_rows int64 [num_rows] (may be NULL),
+ * sample_rows int64 [sample_cap]: row q_off + n - 1 at each row's sample
+ * slot, zeros from sample_count on. */
+int aia_pack_rows(const int64_t* token_update_index, const int64_t* token_update_value,
+                  int32_t num_token_updates, const int64_t* block_update_index,
+                  const int32_t* block_update_value, int32_t num_block_updates,
+                  int64_t* token_pool, int64_t token_pool_stride,
+                  int32_t* block_pool, int64_t block_pool_stride,
+                  const int32_t* rows, int32_t num_rows, int32_t block_size,
+                  int32_t block_table_width, int64_t* token_ids, int64_t* positions,
+                  int32_t* slot_mapping, int32_t* block_table, int32_t* cu_seqlens_q,
+                  int32_t* seqlens_kv, int64_t* last_rows, int64_t* sample_rows,
+                  int32_t sample_count, int32_t sample_cap, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

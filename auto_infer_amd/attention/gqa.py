@@ -66,5 +66,5 @@ class GqaHipBackend(AttentionBackend):
 
     def _attn(self, layer_idx: int, q, k, v, ctx) -> torch.Tensor:
         cache = ctx.kv_caches[layer_idx]
-        plan = step_plan(ctx, self.n_q_heads, self.n_kv_heads, self.head_dim)
+        plan = step_plan(ctx, self.n_q_heads, self.n_kv_heads, self.head_dim, cache.shape[2])
         return ops.paged_attention_gqa(q, cache[0], cache[1], plan, self.scale)

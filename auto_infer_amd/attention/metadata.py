@@ -12,12 +12,12 @@ import torch
 from auto_infer_amd import ops
 
 
-def step_plan(ctx, num_q_heads, num_kv_heads, head_dim_v):
+def step_plan(ctx, num_q_heads, num_kv_heads, head_dim_v, block_size):
     plans = getattr(ctx, "_aia_plans", None)
     if plans is None:
         plans = {}
         ctx._aia_plans = plans
-    key = (num_q_heads, num_kv_heads, head_dim_v)
+    key = (num_q_heads, num_kv_heads, head_dim_v, block_size)
     plan = plans.get(key)
     if plan is not None:
         return plan
@@ -32,7 +32,7 @@ def step_plan(ctx, num_q_heads, num_kv_heads, head_dim_v):
     T = int(ctx.cu_seqlens_q[-1]) if len(ctx.cu_seqlens_q) else 0
     if bt.dtype != torch.int32:
         bt = bt.to(torch.int32)
-    plan = ops.AttentionPlan(bt, cu, kv, T, num_q_heads, num_kv_heads, head_dim_v,
+    plan = ops.AttentionPlan(bt, cu, kv, T, num_q_heads, num_kv_heads, head_dim_v, block_size,
                              workspace=ops.DEFAULT_WORKSPACE.get(
                                  bt.device, ops.workspace_bytes(kv.shape[0], T, num_q_heads,
                                                                 num_kv_heads, head_dim_v),

@@ -105,5 +105,5 @@ class MlaHipBackend(AttentionBackend):
 
     def _attn(self, layer_idx, q, k, v, ctx) -> torch.Tensor:
         latent, _ = ctx.kv_caches[layer_idx]
-        plan = step_plan(ctx, self.num_heads, 1, self.kv_lora_rank)
+        plan = step_plan(ctx, self.num_heads, 1, self.kv_lora_rank, latent.shape[1])
         return ops.paged_attention_mla(q, latent, plan, self.softmax_scale)

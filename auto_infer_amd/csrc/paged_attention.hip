@@ -34,24 +34,38 @@ constexpr int kMaxBatch = 8192;   // planner keeps the request offsets in LDS
 constexpr int kDefaultWaves = 2048;
 constexpr int kMaxWaves = 16384;
 constexpr int kPlanThreads = 1024;
+// Per-range work record: {segment, first tile, end tile, tiles per range,
+// the segment's 8-int record, first logical block, 3 pad, the first 16
+// block ids of the range} -- everything a work-group needs to issue its
+// first K/V loads after one load.
+constexpr int kRecInts = 32;
+constexpr int kRecBlocks = 16;
 
+constexpr int kMaxGroupWaves = 8;  // kv heads (waves) per work-group
+
+// A segment is (request, query block, kv-head group, head block): the
+// work-group that owns one of its key ranges runs one wave per kv head of
+// the group over the same keys, so every tile reads whole contiguous
+// (block_size x Hkv x D) cache slots.
 struct Geometry {
-  int32_t hkv, group, hb, nhb, qb;
+  int32_t hkv, group, hb, nhb, qb, nw, nkvg;
 };
 
 Geometry geometry(int32_t hq, int32_t hkv) {
   Geometry g;
   g.hkv = hkv;
   g.group = hq / hkv;
-  g.hb = g.group < kRows ? g.group : kRows;            // heads per segment
+  g.hb = g.group < kRows ? g.group : kRows;            // query heads per segment
   g.nhb = (g.group + g.hb - 1) / g.hb;                 // head blocks per kv head
   g.qb = kRows / g.hb;                                  // query tokens per segment
+  g.nw = hkv < kMaxGroupWaves ? hkv : kMaxGroupWaves;   // waves per work-group
+  g.nkvg = (hkv + g.nw - 1) / g.nw;                     // kv-head groups
   return g;
 }
 
 // Workspace layout (all offsets 256-byte aligned).
 struct Layout {
-  int64_t hdr, seg, wave, part_ml, part_o, total;
+  int64_t hdr, seg, wave, part_ml, part_o, cnt, total;
   int64_t seg_cap, part_cap;
 };
 
@@ -59,22 +73,26 @@ int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int32_t waves) {
   Layout L;
-  L.seg_cap = (int64_t)g.hkv * g.nhb * (batch + (tokens + g.qb - 1) / g.qb);
+  L.seg_cap = (int64_t)g.nkvg * g.nhb * (batch + (tokens + g.qb - 1) / g.qb);
   L.part_cap = L.seg_cap + waves;
   int64_t off = 0;
   L.hdr = off;      off = align256(off + 64 * 4);
   L.seg = off;      off = align256(off + (L.seg_cap + 1) * 8 * 4);
-  L.wave = off;     off = align256(off + (int64_t)waves * 64);
-  L.part_ml = off;  off = align256(off + L.part_cap * kRows * 8);
-  L.part_o = off;   off = align256(off + L.part_cap * kRows * (int64_t)dv * 4);
+  L.wave = off;     off = align256(off + (int64_t)waves * kRecInts * 4);
+  L.part_ml = off;  off = align256(off + L.part_cap * g.nw * kRows * 8);
+  L.part_o = off;   off = align256(off + L.part_cap * g.nw * kRows * (int64_t)dv * 4);
+  L.cnt = off;      off = align256(off + L.seg_cap * g.nw * 4);
   L.total = off;
   return L;
 }
 
-int32_t resolve_waves(int32_t w) {
-  if (w <= 0) w = kDefaultWaves;
+// Number of key ranges (= work-groups).  Default: about kDefaultWaves waves
+// in flight for GQA (one per kv head of a group), 512 four-wave groups for
+// the 576-wide MLA latent.
+int32_t resolve_waves(int32_t w, const Geometry& g, int32_t dv) {
+  if (w <= 0) w = dv == 512 ? 512 : (kDefaultWaves + g.nw - 1) / g.nw;
   if (w > kMaxWaves) w = kMaxWaves;
-  return (w + 3) & ~3;
+  return w;
 }
 
 // ---------------------------------------------------------------- planner
@@ -107,17 +125,19 @@ __device__ int block_exclusive_scan(int v, int* wave_sums, int* total) {
   return before + x - v;
 }
 
-// Segment record, 8 ints: b, kvh | hb << 16, first query token (global row),
+// Segment record, 8 ints: b, kv-head group | head block << 16, first query token (global row),
 // query tokens, lim_base = Lk - Lq + q0 (last key of the block's first
 // row), tile_begin, tile_end, part_base.
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ kvlen,
+    const int32_t* __restrict__ block_table, int64_t bt_stride, int32_t block_size,
     int32_t batch, Geometry g, int32_t waves,
-    int32_t* __restrict__ hdr, int32_t* __restrict__ seg, int32_t* __restrict__ wave_rec) {
+    int32_t* __restrict__ hdr, int32_t* __restrict__ seg, int32_t* __restrict__ wave_rec,
+    int32_t* __restrict__ counters) {
   __shared__ int req_off[kMaxBatch + 1];
   __shared__ int wave_sums[kPlanThreads / 64];
   const int tid = threadIdx.x;
-  const int per_req = g.hkv * g.nhb;
+  const int per_req = g.nkvg * g.nhb;
 
   // 1) segments per request -> request offsets (LDS)
   int carry = 0;
@@ -152,7 +172,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       const int b = lo;
       const int local = s - req_off[b];
       const int hb = local % g.nhb;
-      const int kvh = (local / g.nhb) % g.hkv;
+      const int kvg = (local / g.nhb) % g.nkvg;
       const int qblk = local / per_req;
       const int q_begin = cu_q[b];
       const int lq = cu_q[b + 1] - q_begin;
@@ -161,8 +181,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       const int nq = min(g.qb, lq - q0);
       const int lim_base = lk - lq + q0;
       const int visible = max(0, min(lk, lim_base + nq));
-      ntiles = (visible + kTile - 1) / kTile;
-      rec[0] = b; rec[1] = kvh | (hb << 16); rec[2] = q_begin + q0; rec[3] = nq;
+      // at least one (fully masked) tile, so the work-group that owns it
+      // writes the zero output of rows that see no key
+      ntiles = max(1, (visible + kTile - 1) / kTile);
+      rec[0] = b; rec[1] = kvg | (hb << 16); rec[2] = q_begin + q0; rec[3] = nq;
       rec[4] = lim_base; rec[5] = ntiles;
     }
     int tot;
@@ -189,7 +211,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     }
     int tot;
     const int ex = block_exclusive_scan(np, wave_sums, &tot);
-    if (s < nseg) seg[(int64_t)s * 8 + 7] = carry + ex;
+    if (s < nseg) {
+      seg[(int64_t)s * 8 + 7] = carry + ex;
+      for (int i = 0; i < g.nw; ++i) counters[(int64_t)s * g.nw + i] = 0;
+    }
     carry += tot;
   }
   if (tid == 0) {
@@ -201,12 +226,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   }
   __syncthreads();
 
-  // 4) per-wave record: first segment whose tile range holds w * tpw, the
-  //    wave's tile range and a copy of that segment's record, so a wave
-  //    starts with one scalar load.
+  // 4) per-range record (see kRecInts)
   for (int w = tid; w < waves; w += kPlanThreads) {
     const int t0 = w * tpw;
-    int* out = wave_rec + (int64_t)w * 16;
+    int* out = wave_rec + (int64_t)w * kRecInts;
     if (t0 >= total_tiles) {
       out[0] = -1; out[1] = 0; out[2] = 0; out[3] = tpw;
       continue;
@@ -217,7 +240,16 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       if (seg[(int64_t)mid * 8 + 5] <= t0) lo = mid; else hi = mid - 1;
     }
     out[0] = lo; out[1] = t0; out[2] = min(total_tiles, t0 + tpw); out[3] = tpw;
-    for (int i = 0; i < 8; ++i) out[4 + i] = seg[(int64_t)lo * 8 + i];
+    const int* r = seg + (int64_t)lo * 8;
+    for (int i = 0; i < 8; ++i) out[4 + i] = r[i];
+    const int b = r[0], nq = r[3], lim_base = r[4];
+    const int visible = max(0, lim_base + nq);
+    const int nblk_vis = (visible + block_size - 1) / block_size;
+    const int blk_base = ((t0 - r[5]) * kTile) / block_size;
+    out[12] = blk_base; out[13] = 0; out[14] = 0; out[15] = 0;
+    const int32_t* btrow = block_table + (int64_t)b * bt_stride;
+    for (int i = 0; i < kRecBlocks; ++i)
+      out[16 + i] = blk_base + i < nblk_vis ? btrow[blk_base + i] : 0;
   }
 }
 
@@ -230,16 +262,28 @@ struct AttnArgs {
   const uint16_t* vc;
   const int32_t* bt;
   int64_t bt_stride;
-  int32_t hkv, group, hb, bs, nb;
+  int32_t hkv, group, hb, bs, nb, nw;
   float scale_log2;
   const int32_t* seg;
   const int32_t* wave_rec;
   float* part_o;
   float2* part_ml;
+  int32_t* counters;
+  int32_t fused_merge;
   uint16_t* out;
   int64_t o_ts, o_hs;
   int32_t waves;
 };
+
+// s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima), gfx9 encoding.
+constexpr int kWaitVmcnt0 = 0x0F70;
+
+__device__ __forceinline__ uint64_t pack_f2(float x, float y) {
+  return (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+}
+__device__ __forceinline__ float2 unpack_f2(uint64_t v) {
+  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
 
 __device__ __forceinline__ short4_t as_s4(uint32_t a, uint32_t b) {
   short4_t r;
@@ -254,13 +298,17 @@ __device__ __forceinline__ uint16_t half_of(uint4 v, int e) {
 }
 
 // Tiles kept in flight per wave (registers: 32 VGPRs per tile).
-constexpr int kPipe = 4;
+#ifndef AIA_PIPE
+#define AIA_PIPE 2
+#endif
+constexpr int kPipe = AIA_PIPE;
 
 // Processes key tiles [lt0, lt1) of one segment; rec = the segment record.
-__device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, int lt0, int lt1,
-                                            int w, int tpw, uint16_t* vt, int lane) {
+__device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, int s, int lt0,
+                                            int lt1, int w, int tpw, uint16_t* vt, int lane,
+                                            int wid, bool use_pre, int pre) {
   const int n = lane & 15, g = lane >> 4;
-  const int b = rec[0], kvh = rec[1] & 0xffff, hbi = rec[1] >> 16;
+  const int b = rec[0], kvh = (rec[1] & 0xffff) * a.nw + wid, hbi = rec[1] >> 16;
   const int qtok0 = rec[2], nq = rec[3], lim_base = rec[4];
   const int tile_begin = rec[5], tile_end = rec[6], part_base = rec[7];
   const int qi = n / a.hb, hh = n - qi * a.hb;
@@ -270,11 +318,9 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   const int visible = max(0, lim_base + nq);
   const int row_elems = a.hkv * kHeadDim;
 
-  // Block ids of up to 64 consecutive logical blocks live one per lane.
   const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
   const int nblk_vis = (visible + a.bs - 1) / a.bs;
-  int blk_base = (lt0 * kTile) / a.bs;
-  int btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
+  int blk_base = 0, btv = 0, w1 = 0;
 
   uint4 qf[4];
   if (rv) {
@@ -292,20 +338,22 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   for (int dt = 0; dt < 8; ++dt) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
   float m = -1e30f, lsum = 0.f;
 
+  // Block ids are held one per lane for a window of 64 logical blocks; the
+  // window is (re)loaded only between pipelined runs, so the per-tile address
+  // shuffle never waits on an outstanding global load.
+  // Loads are issued unconditionally (tiles past the window read the first
+  // key row again, an L1 hit) so the load stream is straight-line and the
+  // compiler can wait for each tile with an exact count.
   auto load = [&](int lt, uint4 (&kk)[4], uint4 (&vv)[4]) {
-    const int last = min(lt * kTile + kTile - 1, visible - 1);
-    if (last / a.bs - blk_base >= 64) {
-      blk_base = (lt * kTile) / a.bs;
-      btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
-    }
-    const int tok = min(lt * kTile + n, visible - 1);
+    const bool live = lt < w1;
+    const int tok = live ? min(lt * kTile + n, visible - 1) : blk_base * a.bs;
     const int bi = tok / a.bs;
     // block ids outside the pool are clamped so a bad table cannot fault
     const int blk = min(max(__shfl(btv, bi - blk_base), 0), a.nb - 1);
     const int off = tok - bi * a.bs;
     const int64_t base = ((int64_t)blk * a.bs + off) * row_elems + (int64_t)kvh * kHeadDim;
     const uint4* kp = reinterpret_cast<const uint4*>(a.kc + base);
-    const uint4* vp = reinterpret_cast<const uint4*>(a.vc + base);
+    const uint4* vp = reinterpret_cast<const uint4*>(a.vc + (live ? base : (int64_t)0) );
 #pragma unroll
     for (int j = 0; j < 4; ++j) kk[j] = kp[4 * j + g];
 #pragma unroll
@@ -313,6 +361,15 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   };
 
   auto compute = [&](int lt, const uint4 (&kk)[4], const uint4 (&vv)[4]) {
+#ifdef AIA_NOCOMPUTE
+    {
+      uint32_t x = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x ^= kk[j].x ^ kk[j].y ^ kk[j].z ^ kk[j].w ^ vv[j].x ^ vv[j].y ^ vv[j].z ^ vv[j].w;
+      o[0][0] += __uint_as_float(x & 0x3fffffu);
+      return;
+    }
+#endif
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -354,18 +411,30 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   };
 
   uint4 kbuf[kPipe][4], vbuf[kPipe][4];
-#pragma unroll
-  for (int i = 0; i < kPipe; ++i)
-    if (lt0 + i < lt1) load(lt0 + i, kbuf[i], vbuf[i]);
-  for (int base = lt0; base < lt1; base += kPipe) {
+  for (int w0 = lt0; w0 < lt1;) {
+    blk_base = (w0 * kTile) / a.bs;
+    // tiles whose keys all fall inside blocks [blk_base, blk_base + win);
+    // the first window of a range uses the block ids of its work record
+    const int win = use_pre ? kRecBlocks : 64;
+    w1 = min(lt1, ((blk_base + win) * a.bs - kTile) / kTile + 1);
+    if (use_pre) btv = lane < kRecBlocks ? pre : 0;
+    else btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
+    use_pre = false;
 #pragma unroll
     for (int i = 0; i < kPipe; ++i) {
-      const int lt = base + i;
-      if (lt < lt1) {
-        compute(lt, kbuf[i], vbuf[i]);
-        if (lt + kPipe < lt1) load(lt + kPipe, kbuf[i], vbuf[i]);
+      load(w0 + i, kbuf[i], vbuf[i]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int base = w0; base < w1; base += kPipe) {
+#pragma unroll
+      for (int i = 0; i < kPipe; ++i) {
+        const int lt = base + i;
+        if (lt < w1) compute(lt, kbuf[i], vbuf[i]);
+        load(lt + kPipe, kbuf[i], vbuf[i]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+    w0 = w1;
   }
 
   lsum += __shfl_xor(lsum, 16);
@@ -386,23 +455,120 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
     }
   } else {
     const int part = part_base + (w - first_wave);
-    if (rv) {
-      float* pp = a.part_o + ((int64_t)part * kRows + n) * kHeadDim;
+    if (a.fused_merge) {
+      // In-kernel merge.  Partials go out with agent-coherent stores (sc1,
+      // written through past the per-XCD L2), the wave waits for them to
+      // complete, then bumps the segment's per-head counter; the wave that
+      // sees the last count reads the partials back with agent-coherent
+      // loads, merges, and resets the counter for the next call on this
+      // plan.  No L2 write-back / invalidate is needed.
+      if (rv) {
+        const int64_t prow = ((int64_t)part * a.nw + wid) * kRows + n;
+        uint64_t* pp = reinterpret_cast<uint64_t*>(a.part_o + prow * kHeadDim);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const int e = (16 * dt + 4 * g) / 2;
+          __hip_atomic_store(pp + e, pack_f2(o[dt][0], o[dt][1]), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(pp + e + 1, pack_f2(o[dt][2], o[dt][3]), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (g == 0)
+          __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_ml + prow), pack_f2(m, lsum),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      int* cnt = a.counters + (int64_t)s * a.nw + wid;
+      int old = 0;
+      if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      old = __shfl(old, 0);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      if (old == nparts - 1) {
+        // Merge, one row at a time: lane k holds part k's (m, l) (all parts
+        // requested at once), then every lane accumulates two output dims
+        // over the parts with all partial loads of a batch in flight.
+        const int rows = nq * a.hb;                 // valid rows are a prefix
+        for (int nr = 0; nr < rows; ++nr) {
+          const int qi2 = nr / a.hb, hh2 = nr - qi2 * a.hb;
+          const int head2 = kvh * a.group + hbi * a.hb + hh2;
+          const int64_t row0 = ((int64_t)part_base * a.nw + wid) * kRows + nr;
+          const int64_t pstride = (int64_t)a.nw * kRows;   // rows between parts
+          float mx = -1e30f;
+          for (int k0 = 0; k0 < nparts; k0 += 64) {
+            const int k = k0 + lane;
+            float mk = -1e30f;
+            if (k < nparts)
+              mk = unpack_f2(__hip_atomic_load(reinterpret_cast<const uint64_t*>(
+                                                   a.part_ml + row0 + k * pstride),
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)).x;
+            mx = fmaxf(mx, mk);
+          }
+#pragma unroll
+          for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+          float acc0 = 0.f, acc1 = 0.f, ls = 0.f;
+          for (int k0 = 0; k0 < nparts; k0 += 64) {
+            const int k = k0 + lane;
+            float wk = 0.f, lk = 0.f;
+            if (k < nparts) {
+              const float2 ml = unpack_f2(__hip_atomic_load(
+                  reinterpret_cast<const uint64_t*>(a.part_ml + row0 + k * pstride),
+                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+              wk = __builtin_amdgcn_exp2f(ml.x - mx);
+              lk = ml.y * wk;
+            }
+            ls += lk;
+            const int kn = min(64, nparts - k0);
+            for (int j0 = 0; j0 < kn; j0 += 16) {
+              float2 v[16];
+#pragma unroll
+              for (int j = 0; j < 16; ++j) {
+                const int kk = k0 + min(j0 + j, kn - 1);
+                v[j] = unpack_f2(__hip_atomic_load(
+                    reinterpret_cast<const uint64_t*>(a.part_o + (row0 + kk * pstride) * kHeadDim) +
+                        lane,
+                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+              }
+#pragma unroll
+              for (int j = 0; j < 16; ++j) {
+                const float wj = j0 + j < kn ? __shfl(wk, j0 + j) : 0.f;
+                acc0 += v[j].x * wj;
+                acc1 += v[j].y * wj;
+              }
+            }
+          }
+#pragma unroll
+          for (int d = 32; d >= 1; d >>= 1) ls += __shfl_xor(ls, d);
+          const float inv = ls > 0.f ? 1.f / ls : 0.f;
+          *reinterpret_cast<uint32_t*>(a.out + (int64_t)(qtok0 + qi2) * a.o_ts +
+                                       (int64_t)head2 * a.o_hs + 2 * lane) =
+              aia::pack_bf16x2(acc0 * inv, acc1 * inv);
+        }
+        if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    } else if (rv) {
+      const int64_t prow = ((int64_t)part * a.nw + wid) * kRows + n;
+      float* pp = a.part_o + prow * kHeadDim;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt)
         *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * g) = o[dt];
-      if (g == 0) a.part_ml[(int64_t)part * kRows + n] = make_float2(m, lsum);
+      if (g == 0) a.part_ml[prow] = make_float2(m, lsum);
     }
   }
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gqa_attn_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t vt_all[4][kHeadDim * kVtStride];
+// One work-group per key range, one wave per kv head of the segment's group.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gqa_attn_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t vt_all[NW][kHeadDim * kVtStride];
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int w = blockIdx.x * 4 + wid;
+  const int w = blockIdx.x;
   if (w >= a.waves) return;
-  const int* wr = a.wave_rec + (int64_t)w * 16;
+  const int* wr = a.wave_rec + (int64_t)w * kRecInts;
+  const int pre = wr[16 + (lane & (kRecBlocks - 1))];   // issued with the header
   int s = wr[0];
   if (s < 0) return;
   int t = wr[1];
@@ -411,10 +577,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
   for (int i = 0; i < 8; ++i) rec[i] = wr[4 + i];
   uint16_t* vt = vt_all[wid];
+  bool first = true;
   while (true) {
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
-      gqa_segment(a, rec, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane);
+      if ((rec[1] & 0xffff) * NW + wid < a.hkv)
+        gqa_segment(a, rec, s, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane, wid, first,
+                    pre);
+      first = false;
       t = chunk_end;
       if (t >= t_end) break;
     }
@@ -432,51 +602,46 @@ struct MergeArgs {
   const float2* part_ml;
   uint16_t* out;
   int64_t o_ts, o_hs;
-  int32_t group, hb, dv;
+  int32_t group, hb, dv, nw, hkv;
 };
 
-// One work-group per split segment; thread = (row, 8 dims), looping over the
-// dims when dv > 128.  Single pass with running rescale so the loads of
-// successive partials are independent.
+// One work-group per (split segment, kv head): each half of the group takes
+// every other row, a thread owns one output dim (looping when dv > 128).
+// The max over the partials' m is taken first, then the weighted sum; both
+// loops are unrolled so the loads of many partials are in flight together.
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int nseg = a.hdr[0], tpw = a.hdr[2];
-  const int n = threadIdx.x >> 4;
-  for (int s = blockIdx.x; s < nseg; s += gridDim.x) {
+  const int half = threadIdx.x >> 7, t = threadIdx.x & 127;
+  for (int sw = blockIdx.x; sw < nseg * a.nw; sw += gridDim.x) {
+    const int s = sw / a.nw, wid = sw - s * a.nw;
     const int4 r0 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8);
     const int4 r1 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8 + 4);
     const int tb = r1.y, te = r1.z;
     const int np = te > tb ? (te - 1) / tpw - tb / tpw + 1 : 0;
-    if (np == 1) continue;
-    const int kvh = r0.y & 0xffff, hbi = r0.y >> 16, qtok0 = r0.z, nq = r0.w;
-    const int qi = n / a.hb, hh = n - qi * a.hb;
-    if (!(qi < nq && hbi * a.hb + hh < a.group)) continue;
-    const int head = kvh * a.group + hbi * a.hb + hh;
-    const int pb = r1.w;
-    for (int c = (threadIdx.x & 15) * 8; c < a.dv; c += 128) {
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      float mx = -1e30f, lsum = 0.f;
-#pragma unroll 4
-      for (int k = 0; k < np; ++k) {
-        const float2 ml = a.part_ml[(int64_t)(pb + k) * kRows + n];
-        const float4* src = reinterpret_cast<const float4*>(
-            a.part_o + ((int64_t)(pb + k) * kRows + n) * a.dv + c);
-        const float4 x0 = src[0], x1 = src[1];
-        const float mn = fmaxf(mx, ml.x);
-        const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
-        lsum = lsum * sa + ml.y * sb;
-        acc[0] = acc[0] * sa + x0.x * sb; acc[1] = acc[1] * sa + x0.y * sb;
-        acc[2] = acc[2] * sa + x0.z * sb; acc[3] = acc[3] * sa + x0.w * sb;
-        acc[4] = acc[4] * sa + x1.x * sb; acc[5] = acc[5] * sa + x1.y * sb;
-        acc[6] = acc[6] * sa + x1.z * sb; acc[7] = acc[7] * sa + x1.w * sb;
-        mx = mn;
+    if (np <= 1) continue;
+    const int kvh = (r0.y & 0xffff) * a.nw + wid, hbi = r0.y >> 16, qtok0 = r0.z, nq = r0.w;
+    if (kvh >= a.hkv) continue;
+    const int rows = nq * a.hb;                 // valid rows are a prefix
+    const int64_t pstride = (int64_t)a.nw * kRows;
+    for (int r = half; r < rows; r += 2) {
+      const int qi = r / a.hb, hh = r - qi * a.hb;
+      const int head = kvh * a.group + hbi * a.hb + hh;
+      const int64_t row0 = ((int64_t)r1.w * a.nw + wid) * kRows + r;
+      float mx = -1e30f;
+#pragma unroll 8
+      for (int k = 0; k < np; ++k) mx = fmaxf(mx, a.part_ml[row0 + k * pstride].x);
+      uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs;
+      for (int d = t; d < a.dv; d += 128) {
+        float acc = 0.f, ls = 0.f;
+#pragma unroll 8
+        for (int k = 0; k < np; ++k) {
+          const float2 ml = a.part_ml[row0 + k * pstride];
+          const float wk = __builtin_amdgcn_exp2f(ml.x - mx);
+          ls += ml.y * wk;
+          acc += a.part_o[(row0 + k * pstride) * a.dv + d] * wk;
+        }
+        op[d] = (uint16_t)aia::f32_to_bf16_bits(ls > 0.f ? acc / ls : 0.f);
       }
-      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-      uint4 wv;
-      wv.x = aia::pack_bf16x2(acc[0] * inv, acc[1] * inv);
-      wv.y = aia::pack_bf16x2(acc[2] * inv, acc[3] * inv);
-      wv.z = aia::pack_bf16x2(acc[4] * inv, acc[5] * inv);
-      wv.w = aia::pack_bf16x2(acc[6] * inv, acc[7] * inv);
-      *reinterpret_cast<uint4*>(a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs + c) = wv;
     }
   }
 }
@@ -511,7 +676,7 @@ struct MlaArgs {
 
 __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, int lt0, int lt1,
                                             int w, int tpw, uint16_t* vt, float* sx, int lane,
-                                            int wid) {
+                                            int wid, bool use_pre, int pre) {
   const int n = lane & 15, g = lane >> 4;
   const int b = rec[0], hbi = rec[1] >> 16;
   const int qtok0 = rec[2], nq = rec[3], lim_base = rec[4];
@@ -530,8 +695,7 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
 
   const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
   const int nblk_vis = (visible + a.bs - 1) / a.bs;
-  int blk_base = (lt0 * kTile) / a.bs;
-  int btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
+  int blk_base = 0, btv = 0, w1 = 0;
 
   uint4 qf[5];
   if (rv) {
@@ -550,12 +714,8 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
   float m = -1e30f, lsum = 0.f;
 
   auto load = [&](int lt, uint4 (&kk)[5]) {
-    const int last = min(lt * kTile + kTile - 1, visible - 1);
-    if (last / a.bs - blk_base >= 64) {
-      blk_base = (lt * kTile) / a.bs;
-      btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
-    }
-    const int tok = min(lt * kTile + n, visible - 1);
+    const bool live = lt < w1;
+    const int tok = live ? min(lt * kTile + n, visible - 1) : blk_base * a.bs;
     const int bi = tok / a.bs;
     const int blk = min(max(__shfl(btv, bi - blk_base), 0), a.nb - 1);
     const int off = tok - bi * a.bs;
@@ -615,18 +775,28 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
   };
 
   uint4 kbuf[kPipe][5];
-#pragma unroll
-  for (int i = 0; i < kPipe; ++i)
-    if (lt0 + i < lt1) load(lt0 + i, kbuf[i]);
-  for (int base = lt0; base < lt1; base += kPipe) {
+  for (int w0 = lt0; w0 < lt1;) {
+    blk_base = (w0 * kTile) / a.bs;
+    const int win = use_pre ? kRecBlocks : 64;
+    w1 = min(lt1, ((blk_base + win) * a.bs - kTile) / kTile + 1);
+    if (use_pre) btv = lane < kRecBlocks ? pre : 0;
+    else btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
+    use_pre = false;
 #pragma unroll
     for (int i = 0; i < kPipe; ++i) {
-      const int lt = base + i;
-      if (lt < lt1) {
-        compute(lt, kbuf[i]);
-        if (lt + kPipe < lt1) load(lt + kPipe, kbuf[i]);
+      load(w0 + i, kbuf[i]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int base = w0; base < w1; base += kPipe) {
+#pragma unroll
+      for (int i = 0; i < kPipe; ++i) {
+        const int lt = base + i;
+        if (lt < w1) compute(lt, kbuf[i]);
+        load(lt + kPipe, kbuf[i]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+    w0 = w1;
   }
 
   lsum += __shfl_xor(lsum, 16);
@@ -665,7 +835,8 @@ __global__ __launch_bounds__(256) void mla_attn_kernel(MlaArgs a) {
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int w = blockIdx.x;   // one tile range per work-group
   if (w >= a.waves) return;
-  const int* wr = a.wave_rec + (int64_t)w * 16;
+  const int* wr = a.wave_rec + (int64_t)w * kRecInts;
+  const int pre = wr[16 + (lane & (kRecBlocks - 1))];
   int s = wr[0];
   if (s < 0) return;
   int t = wr[1];
@@ -673,10 +844,13 @@ __global__ __launch_bounds__(256) void mla_attn_kernel(MlaArgs a) {
   int rec[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) rec[i] = wr[4 + i];
+  bool first = true;
   while (true) {
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
-      mla_segment(a, rec, t - rec[5], chunk_end - rec[5], w, tpw, vt_all[wid], sx, lane, wid);
+      mla_segment(a, rec, t - rec[5], chunk_end - rec[5], w, tpw, vt_all[wid], sx, lane, wid,
+                  first, pre);
+      first = false;
       t = chunk_end;
       if (t >= t_end) break;
     }
@@ -687,14 +861,16 @@ __global__ __launch_bounds__(256) void mla_attn_kernel(MlaArgs a) {
   }
 }
 
-int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t dv, const float* part_o,
+int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32_t dv,
+                 const float* part_o,
                  const float2* part_ml, const int32_t* seg, uint16_t* out, int64_t o_ts,
                  int64_t o_hs, hipStream_t s) {
   MergeArgs mg;
   mg.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
   mg.seg = seg; mg.part_o = part_o; mg.part_ml = part_ml;
   mg.out = out; mg.o_ts = o_ts; mg.o_hs = o_hs; mg.group = g.group; mg.hb = g.hb; mg.dv = dv;
-  int64_t mgrid = L.seg_cap < 4096 ? L.seg_cap : 4096;
+  mg.nw = nw; mg.hkv = g.hkv;
+  int64_t mgrid = L.seg_cap * nw < 4096 ? L.seg_cap * nw : 4096;
   if (mgrid < 1) mgrid = 1;
   merge_kernel<<<(unsigned)mgrid, 256, 0, s>>>(mg);
   return aia::check_hip(hipGetLastError(), "merge_kernel launch");
@@ -722,7 +898,9 @@ extern "C" int aia_attn_workspace_bytes(int32_t batch, int32_t num_tokens, int32
   return AIA_OK;
 }
 
-extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv, int32_t batch,
+extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
+                             const int32_t* block_table, int32_t block_table_stride,
+                             int32_t block_size, int32_t batch,
                              int32_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
                              int32_t head_dim_v, int32_t num_waves, void* workspace,
                              int64_t workspace_bytes, void* stream) {
@@ -730,19 +908,21 @@ extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens
   if (int rc = check_heads("aia_attn_plan", num_q_heads, num_kv_heads)) return rc;
   if (batch < 0 || batch > kMaxBatch)
     return fail(AIA_ERR_CAPACITY, "aia_attn_plan: batch %d exceeds planner limit %d", batch, kMaxBatch);
-  if (batch > 0 && (!cu_seqlens_q || !seqlens_kv))
+  if (batch > 0 && (!cu_seqlens_q || !seqlens_kv || !block_table))
     return fail(AIA_ERR_INVALID, "aia_attn_plan: null metadata");
+  if (block_size <= 0) return fail(AIA_ERR_INVALID, "aia_attn_plan: block_size %d", block_size);
   if (!workspace) return fail(AIA_ERR_INVALID, "aia_attn_plan: null workspace");
   const Geometry g = geometry(num_q_heads, num_kv_heads);
-  const int32_t waves = resolve_waves(num_waves);
+  const int32_t waves = resolve_waves(num_waves, g, head_dim_v);
   const Layout L = layout(batch, num_tokens, g, head_dim_v, waves);
   if (workspace_bytes < L.total)
     return fail(AIA_ERR_CAPACITY, "aia_attn_plan: workspace %lld bytes < %lld needed",
                 (long long)workspace_bytes, (long long)L.total);
   char* ws = static_cast<char*>(workspace);
   plan_kernel<<<1, kPlanThreads, 0, (hipStream_t)stream>>>(
-      cu_seqlens_q, seqlens_kv, batch, g, waves, reinterpret_cast<int32_t*>(ws + L.hdr),
-      reinterpret_cast<int32_t*>(ws + L.seg), reinterpret_cast<int32_t*>(ws + L.wave));
+      cu_seqlens_q, seqlens_kv, block_table, block_table_stride, block_size, batch, g, waves, reinterpret_cast<int32_t*>(ws + L.hdr),
+      reinterpret_cast<int32_t*>(ws + L.seg), reinterpret_cast<int32_t*>(ws + L.wave),
+      reinterpret_cast<int32_t*>(ws + L.cnt));
   return check_hip(hipGetLastError(), "aia_attn_plan launch");
 }
 
@@ -770,7 +950,7 @@ extern "C" int aia_paged_attention_gqa(
                 "with strides a multiple of 8 elements");
   if (num_tokens == 0 || batch == 0) return AIA_OK;
   const Geometry g = geometry(num_q_heads, num_kv_heads);
-  const int32_t waves = resolve_waves(num_waves);
+  const int32_t waves = resolve_waves(num_waves, g, head_dim);
   const Layout L = layout(batch, num_tokens, g, head_dim, waves);
   if (workspace_bytes < L.total)
     return fail(AIA_ERR_CAPACITY, "aia_paged_attention_gqa: workspace %lld bytes < %lld needed",
@@ -783,6 +963,7 @@ extern "C" int aia_paged_attention_gqa(
   a.vc = static_cast<const uint16_t*>(value_cache);
   a.bt = block_table; a.bt_stride = block_table_stride;
   a.hkv = g.hkv; a.group = g.group; a.hb = g.hb; a.bs = block_size; a.nb = num_blocks;
+  a.nw = g.nw;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.seg = reinterpret_cast<const int32_t*>(ws + L.seg);
   a.wave_rec = reinterpret_cast<const int32_t*>(ws + L.wave);
@@ -791,11 +972,22 @@ extern "C" int aia_paged_attention_gqa(
   a.out = static_cast<uint16_t*>(out);
   a.o_ts = out_token_stride; a.o_hs = out_head_stride;
   a.waves = waves;
+  a.counters = reinterpret_cast<int32_t*>(ws + L.cnt);
+  a.fused_merge = (flags & AIA_ATTN_FUSED_MERGE) && !(flags & AIA_ATTN_SKIP_MERGE) ? 1 : 0;
   hipStream_t s = (hipStream_t)stream;
-  gqa_attn_kernel<<<waves / 4, 256, 0, s>>>(a);
+  switch (g.nw) {
+    case 1: gqa_attn_kernel<1><<<waves, 64, 0, s>>>(a); break;
+    case 2: gqa_attn_kernel<2><<<waves, 128, 0, s>>>(a); break;
+    case 3: gqa_attn_kernel<3><<<waves, 192, 0, s>>>(a); break;
+    case 4: gqa_attn_kernel<4><<<waves, 256, 0, s>>>(a); break;
+    case 5: gqa_attn_kernel<5><<<waves, 320, 0, s>>>(a); break;
+    case 6: gqa_attn_kernel<6><<<waves, 384, 0, s>>>(a); break;
+    case 7: gqa_attn_kernel<7><<<waves, 448, 0, s>>>(a); break;
+    default: gqa_attn_kernel<8><<<waves, 512, 0, s>>>(a); break;
+  }
   if (int rc = check_hip(hipGetLastError(), "gqa_attn_kernel launch")) return rc;
-  if (flags & AIA_ATTN_SKIP_MERGE) return AIA_OK;
-  return launch_merge(ws, L, g, head_dim, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs, s);
+  if (a.fused_merge || (flags & AIA_ATTN_SKIP_MERGE)) return AIA_OK;
+  return launch_merge(ws, L, g, g.nw, head_dim, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs, s);
 }
 
 extern "C" int aia_paged_attention_mla(
@@ -822,7 +1014,7 @@ extern "C" int aia_paged_attention_mla(
                 "strides a multiple of 8 elements");
   if (num_tokens == 0 || batch == 0) return AIA_OK;
   const Geometry g = geometry(num_heads, 1);
-  const int32_t waves = resolve_waves(num_waves);
+  const int32_t waves = resolve_waves(num_waves, g, kMlaV);
   const Layout L = layout(batch, num_tokens, g, kMlaV, waves);
   if (workspace_bytes < L.total)
     return fail(AIA_ERR_CAPACITY, "aia_paged_attention_mla: workspace %lld bytes < %lld needed",
@@ -846,5 +1038,5 @@ extern "C" int aia_paged_attention_mla(
   mla_attn_kernel<<<waves, 256, 0, s>>>(a);
   if (int rc = check_hip(hipGetLastError(), "mla_attn_kernel launch")) return rc;
   if (flags & AIA_ATTN_SKIP_MERGE) return AIA_OK;
-  return launch_merge(ws, L, g, kMlaV, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs, s);
+  return launch_merge(ws, L, g, 1, kMlaV, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs, s);
 }

@@ -125,7 +125,7 @@ class AttentionPlan:
     """
 
     def __init__(self, block_table, cu_seqlens_q, seqlens_kv, num_tokens, num_q_heads,
-                 num_kv_heads, head_dim_v, num_waves=0, workspace=None):
+                 num_kv_heads, head_dim_v, block_size, num_waves=0, workspace=None):
         _check_device_tensor(block_table, "block_table", torch.int32)
         _check_device_tensor(cu_seqlens_q, "cu_seqlens_q", torch.int32)
         _check_device_tensor(seqlens_kv, "seqlens_kv", torch.int32)
@@ -145,6 +145,7 @@ class AttentionPlan:
         self.num_kv_heads = num_kv_heads
         self.head_dim_v = head_dim_v
         self.num_waves = num_waves
+        self.block_size = int(block_size)
         nbytes = workspace_bytes(batch, self.num_tokens, num_q_heads, num_kv_heads, head_dim_v)
         if workspace is None:
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=block_table.device)
@@ -156,27 +157,30 @@ class AttentionPlan:
         """Re-run the device planner on the (possibly updated in place)
         metadata tensors; graph-capturable."""
         _native.call("aia_attn_plan", _ptr(self.cu_seqlens_q), _ptr(self.seqlens_kv),
+                     _ptr(self.block_table), self.block_table.stride(0), self.block_size,
                      self.batch, self.num_tokens, self.num_q_heads, self.num_kv_heads,
                      self.head_dim_v, self.num_waves, _ptr(self.workspace),
                      self.workspace.numel(), _stream(self.block_table.device))
 
     @classmethod
     def from_lists(cls, block_table, cu_seqlens_q, seqlens_kv, num_q_heads, num_kv_heads,
-                   head_dim_v, **kw):
+                   head_dim_v, block_size, **kw):
         """From the reference's host lists (cumulative ends without the
         leading 0, per-request KV lengths)."""
         dev = block_table.device
-        bs = kw.pop("block_size", None)
-        if bs is not None and len(seqlens_kv):
+        bs = block_size
+        if len(seqlens_kv):
             _require(block_table.shape[1] * bs >= max(seqlens_kv),
                      "block_table has fewer columns than the longest context needs")
         cu = torch.tensor([0, *cu_seqlens_q], dtype=torch.int32).to(dev, non_blocking=True)
         kv = torch.tensor(list(seqlens_kv), dtype=torch.int32).to(dev, non_blocking=True)
         total = cu_seqlens_q[-1] if len(cu_seqlens_q) else 0
-        return cls(block_table, cu, kv, total, num_q_heads, num_kv_heads, head_dim_v, **kw)
+        return cls(block_table, cu, kv, total, num_q_heads, num_kv_heads, head_dim_v, block_size,
+                   **kw)
 
 
-ATTN_SKIP_MERGE = 1   # diagnostic flag: time the split-K kernel alone
+ATTN_SKIP_MERGE = 1         # diagnostic: the split kernel alone, split rows unmerged
+ATTN_FUSED_MERGE = 2        # merge split rows inside the split kernel (default: 2nd kernel)
 
 
 def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None, flags=0):
@@ -196,8 +200,8 @@ def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None, fl
     nb, bs, hkv, dk = key_cache.shape
     _require(tuple(value_cache.shape) == (nb, bs, hkv, dk), "value cache shape differs from key cache")
     _require(dk == d, "query head_dim differs from the cache's")
-    _require(hq == plan.num_q_heads and hkv == plan.num_kv_heads and T == plan.num_tokens,
-             "plan was made for other head counts / token count")
+    _require(hq == plan.num_q_heads and hkv == plan.num_kv_heads and T == plan.num_tokens
+             and bs == plan.block_size, "plan was made for another shape")
     if out is None:
         out = torch.empty(T, hq, d, dtype=_BF16, device=query.device)
     _native.call("aia_paged_attention_gqa", _ptr(query), query.stride(0), query.stride(1),
@@ -239,7 +243,8 @@ def paged_attention_mla(q_latent, latent_cache, plan, scale, out=None, flags=0):
              "latent_cache must be contiguous (num_blocks, block_size, 1, 576)")
     nb, bs = latent_cache.shape[0], latent_cache.shape[1]
     _require(h == plan.num_q_heads and plan.num_kv_heads == 1 and plan.head_dim_v == MLA_LATENT
-             and T == plan.num_tokens, "plan was not made for this MLA shape")
+             and T == plan.num_tokens and bs == plan.block_size,
+             "plan was not made for this MLA shape")
     if out is None:
         out = torch.empty(T, h, MLA_LATENT, dtype=_BF16, device=q_latent.device)
     _native.call("aia_paged_attention_mla", _ptr(q_latent), q_latent.stride(0),

@@ -119,7 +119,7 @@ def main():
     out = torch.empty(T, hq, d, dtype=torch.bfloat16, device=dev)
     cu = torch.tensor([0, *step.cu_seqlens_q], dtype=torch.int32, device=dev)
     kvl = torch.tensor(step.seqlens_kv, dtype=torch.int32, device=dev)
-    plan = ops.AttentionPlan(bt, cu, kvl, T, hq, hkv, d)
+    plan = ops.AttentionPlan(bt, cu, kvl, T, hq, hkv, d, step.k_cache.shape[1])
 
     def model_step():
         """Planner once, then L layers of (KV write + attention)."""
@@ -152,8 +152,9 @@ def main():
     steps = n_replay * L
     ms_per_step = e0.elapsed_time(e1) / steps
 
-    # Dominant kernel alone: back-to-back attention launches on the same
-    # stream, averaged over the timed region (HIP events on that stream).
+    # Dominant kernel alone (the split-K attention kernel, without its merge
+    # pass): back-to-back launches on the same stream, averaged over the
+    # timed region (HIP events on that stream).
     n_k = 50 * L
     with torch.cuda.stream(stream):
         for i in range(L):

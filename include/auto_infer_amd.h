@@ -60,13 +60,16 @@ int aia_attn_workspace_bytes(int32_t batch, int32_t num_tokens,
 /* Split-K work plan for one step: reads the device copies of
  * cu_seqlens_q (batch + 1 entries, leading 0 -- the reference keeps the
  * cumulative ends as a host list, model_runner.py:137 / ForwardContext
- * .cu_seqlens_q) and seqlens_kv (batch entries, forward_context.py:15) and
- * writes a flat list of (request, kv head, query block, key range) work
- * items into `workspace`.  The plan depends only on step metadata, so one
- * plan serves every layer of the step.  num_waves = 0 picks the default
- * grid (the whole chip once). */
+ * .cu_seqlens_q), seqlens_kv (batch entries, forward_context.py:15) and the
+ * block table (batch rows, block_table_stride apart) and writes a flat list
+ * of (request, kv-head group, query block, key range) work items into
+ * `workspace`, each carrying the first block ids it reads.  The plan
+ * depends only on step metadata, so one plan serves every layer of the
+ * step.  num_waves: number of key ranges (work-groups); 0 picks the default
+ * (about 2048 waves in flight for GQA, 512 groups for MLA). */
 int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
-                  int32_t batch, int32_t num_tokens,
+                  const int32_t* block_table, int32_t block_table_stride,
+                  int32_t block_size, int32_t batch, int32_t num_tokens,
                   int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim_v,
                   int32_t num_waves, void* workspace, int64_t workspace_bytes,
                   void* stream);
@@ -82,9 +85,14 @@ int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
  * out:    (num_tokens, Hq, head_dim) with the given strides.
  * head_dim must be 128.  The workspace must hold a plan made by
  * aia_attn_plan with the same metadata, head counts and num_waves.
- * flags: 0, or AIA_ATTN_SKIP_MERGE to launch the split-K kernel without the
- * merge pass (diagnostic timing; split rows are then left unmerged). */
+ * Rows whose keys were split over several work-groups are merged from fp32
+ * (O, max, sum) partials by log-sum-exp, by default in a second kernel.
+ * flags: AIA_ATTN_FUSED_MERGE merges in the split kernel instead (the last
+ * work-group of a split row to finish merges it, via agent-coherent partial
+ * stores and a per-segment counter); AIA_ATTN_SKIP_MERGE launches only the
+ * split kernel (diagnostic: split rows are left unmerged). */
 #define AIA_ATTN_SKIP_MERGE 1
+#define AIA_ATTN_FUSED_MERGE 2
 int aia_paged_attention_gqa(const void* query, int64_t q_token_stride,
                             int64_t q_head_stride,
                             const void* key_cache, const void* value_cache,

@@ -14,13 +14,13 @@ DEV = "cuda:0"
 TOL = 2e-2
 
 
-def run_gpu(step, num_waves=0):
+def run_gpu(step, num_waves=0, flags=0):
     s = step
     plan = ops.AttentionPlan.from_lists(s.block_table.to(DEV), s.cu_seqlens_q, s.seqlens_kv,
                                         s.q.shape[1], s.k_cache.shape[2], s.q.shape[2],
-                                        num_waves=num_waves)
+                                        s.k_cache.shape[1], num_waves=num_waves)
     out = ops.paged_attention_gqa(s.q.to(DEV), s.k_cache.to(DEV), s.v_cache.to(DEV), plan,
-                                  s.scale)
+                                  s.scale, flags=flags)
     torch.cuda.synchronize()
     return out.float().cpu()
 
@@ -30,8 +30,8 @@ def oracle(step):
                            step.cu_seqlens_q, step.seqlens_kv, step.scale)
 
 
-def check(step, num_waves=0):
-    got = run_gpu(step, num_waves)
+def check(step, num_waves=0, flags=0):
+    got = run_gpu(step, num_waves, flags)
     exp = oracle(step)
     err = (got - exp).abs().max().item()
     print(f"max-abs err {err:.3e}", flush=True)
@@ -39,16 +39,35 @@ def check(step, num_waves=0):
     return got
 
 
-def test_config1_decode_shape():
-    check(workloads.config1_decode(seed=3))
+@pytest.mark.parametrize("flags", [0, ops.ATTN_FUSED_MERGE])
+def test_config1_decode_shape(flags):
+    check(workloads.config1_decode(seed=3), flags=flags)
 
 
 @pytest.mark.parametrize("waves", [1, 7, 64, 0])
-def test_split_count_invariance(waves):
-    """The result does not depend on how the key range is split."""
+@pytest.mark.parametrize("flags", [0, ops.ATTN_FUSED_MERGE])
+def test_split_count_invariance(waves, flags):
+    """The result does not depend on how the key range is split, nor on
+    whether split rows are merged in the kernel or by a second pass."""
     step = workloads.make_gqa_step(lqs=[1, 1, 1], lks=[300, 17, 1000], num_q_heads=8,
                                    num_kv_heads=2, block_size=16, seed=11)
-    check(step, waves)
+    check(step, waves, flags)
+
+
+def test_repeated_calls_on_one_plan():
+    """The in-kernel merge resets its counters: many layers on one plan."""
+    step = workloads.make_gqa_step(lqs=[1, 2, 1], lks=[900, 40, 2000], num_q_heads=16,
+                                   num_kv_heads=8, block_size=128, seed=13)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, 16, 8, 128, 128, num_waves=37)
+    q, kc, vc = step.q.to(DEV), step.k_cache.to(DEV), step.v_cache.to(DEV)
+    first = ops.paged_attention_gqa(q, kc, vc, plan, step.scale).clone()
+    for _ in range(5):
+        again = ops.paged_attention_gqa(q, kc, vc, plan, step.scale)
+    torch.cuda.synchronize()
+    assert torch.equal(first.cpu(), again.cpu())
+    exp = oracle(step)
+    assert (first.float().cpu() - exp).abs().max().item() <= TOL
 
 
 @pytest.mark.parametrize("group", [1, 2, 4, 7, 8, 16])

@@ -13,6 +13,7 @@ TOL = 2e-2
 def run(step, num_waves=0):
     plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
                                         step.seqlens_kv, step.q_latent.shape[1], 1, 512,
+                                        step.cache.shape[1],
                                         num_waves=num_waves)
     out = ops.paged_attention_mla(step.q_latent.to(DEV), step.cache.to(DEV), plan, step.scale)
     torch.cuda.synchronize()

@@ -41,7 +41,20 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run a plain 256 MiB device copy 10 times (the reference "
+                        "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
+
+
+def copy_calibration():
+    n = 256 << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "launches": 10}))
 
 
 def cpu_model():
@@ -92,6 +105,9 @@ def cpu_baseline(step, budget_s):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
               f"(--gpus {args.gpus} requested); run with --gpus 1", file=sys.stderr)
@@ -197,6 +213,14 @@ def main():
     step_alg_bytes = attn_alg_bytes + write_bytes
     achieved = attn_alg_bytes / (attn_us * 1e-6) / 1e9
     step_s = ms_per_step * 1e-3
+    # HBM bytes per attention launch, measured with rocprofv3 FETCH_SIZE /
+    # WRITE_SIZE (scaled by a plain-copy calibration) and committed with the
+    # profile summary; null if that measurement is absent.
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gqa_decode_config1_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = int(round(json.load(f)["traffic_bytes"]))
 
     result = {
         "metric": METRIC,
@@ -227,7 +251,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "algorithmic_bytes": attn_alg_bytes,
         },
     }
     if not args.no_cpu:

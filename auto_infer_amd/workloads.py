@@ -62,7 +62,7 @@ def _block_tables(rng, lks, bs, num_blocks, shared_prefix_blocks=0, share_frac=0
 def make_gqa_step(*, lqs, lks, num_q_heads, num_kv_heads, head_dim=128, block_size=128,
                   num_blocks=None, seed=0, device="cpu", value_scale=1.0,
                   dtype=torch.bfloat16, shared_prefix_blocks=0, share_frac=0.0,
-                  extra_blocks=0):
+                  extra_blocks=0, tables=None):
     """One GQA step: request b has lqs[b] query rows at the end of its
     lks[b]-long context (new K/V rows are the last lqs[b] positions)."""
     rng = np.random.default_rng(seed)
@@ -70,30 +70,40 @@ def make_gqa_step(*, lqs, lks, num_q_heads, num_kv_heads, head_dim=128, block_si
     need = sum((lk + block_size - 1) // block_size for lk in lks)
     if num_blocks is None:
         num_blocks = need + extra_blocks
-    tables = _block_tables(rng, lks, block_size, num_blocks, shared_prefix_blocks, share_frac)
+    if tables is None:
+        tables = _block_tables(rng, lks, block_size, num_blocks, shared_prefix_blocks,
+                               share_frac)
     width = max((len(t) for t in tables), default=0)
     bt = np.zeros((B, max(width, 1)), dtype=np.int32)
     for i, t in enumerate(tables):
         bt[i, :len(t)] = t
-    gen = torch.Generator().manual_seed(seed)
+    dev = torch.device(device)
+    gen = torch.Generator(device=dev).manual_seed(seed)
     T = sum(lqs)
-    q = (torch.randn(T, num_q_heads, head_dim, generator=gen) * value_scale).to(dtype)
-    k_new = (torch.randn(T, num_kv_heads, head_dim, generator=gen) * value_scale).to(dtype)
-    v_new = (torch.randn(T, num_kv_heads, head_dim, generator=gen) * value_scale).to(dtype)
+
+    def rnd(*shape):
+        if dev.type == "cpu":
+            return (torch.randn(*shape, generator=gen) * value_scale).to(dtype)
+        # on the GPU: generate in the target dtype (no fp32 temporary of the pool)
+        t = torch.randn(*shape, generator=gen, device=dev, dtype=dtype)
+        return t.mul_(value_scale) if value_scale != 1.0 else t
+    q = rnd(T, num_q_heads, head_dim)
+    k_new = rnd(T, num_kv_heads, head_dim)
+    v_new = rnd(T, num_kv_heads, head_dim)
     shape = (num_blocks, block_size, num_kv_heads, head_dim)
-    k_cache = (torch.randn(shape, generator=gen) * value_scale).to(dtype)
-    v_cache = (torch.randn(shape, generator=gen) * value_scale).to(dtype)
+    k_cache = rnd(*shape)
+    v_cache = rnd(*shape)
     slots, cu, acc = [], [], 0
     for b, (lq, lk) in enumerate(zip(lqs, lks)):
         for p in range(lk - lq, lk):
             slots.append(bt[b, p // block_size] * block_size + p % block_size)
         acc += lq
         cu.append(acc)
-    step = GqaStep(q=q, k_new=k_new, v_new=v_new, k_cache=k_cache, v_cache=v_cache,
-                   block_table=torch.from_numpy(bt), cu_seqlens_q=cu, seqlens_kv=list(lks),
-                   slot_mapping=torch.tensor(slots, dtype=torch.int32),
+    return GqaStep(q=q, k_new=k_new, v_new=v_new, k_cache=k_cache, v_cache=v_cache,
+                   block_table=torch.from_numpy(bt).to(dev), cu_seqlens_q=cu,
+                   seqlens_kv=list(lks),
+                   slot_mapping=torch.tensor(slots, dtype=torch.int32, device=dev),
                    scale=head_dim ** -0.5)
-    return step.to(device) if device != "cpu" else step
 
 
 def _to(self, device):
@@ -103,6 +113,37 @@ def _to(self, device):
 
 
 GqaStep.to = _to
+
+
+def subset(step, requests):
+    """A self-contained CPU copy of the given requests of a GQA step: only
+    their blocks, renumbered, with their query rows (attention rows of a
+    request depend only on that request).  Returns (step, query row index)."""
+    bt = step.block_table.cpu()
+    rows, cu, kv, acc = [], [], [], 0
+    starts = [0] + list(step.cu_seqlens_q[:-1])
+    for r in requests:
+        lq = step.cu_seqlens_q[r] - starts[r]
+        rows.extend(range(starts[r], starts[r] + lq))
+        acc += lq
+        cu.append(acc)
+        kv.append(step.seqlens_kv[r])
+    bs = step.k_cache.shape[1]
+    used = sorted({int(bt[r, c]) for r in requests
+                   for c in range((step.seqlens_kv[r] + bs - 1) // bs)})
+    remap = {b: i for i, b in enumerate(used)}
+    idx = torch.tensor(used, dtype=torch.long, device=step.k_cache.device)
+    width = max((step.seqlens_kv[r] + bs - 1) // bs for r in requests)
+    nbt = torch.zeros(len(requests), max(width, 1), dtype=torch.int32)
+    for i, r in enumerate(requests):
+        for c in range((step.seqlens_kv[r] + bs - 1) // bs):
+            nbt[i, c] = remap[int(bt[r, c])]
+    ridx = torch.tensor(rows, dtype=torch.long, device=step.q.device)
+    sub = GqaStep(q=step.q[ridx].cpu(), k_new=step.k_new[ridx].cpu(),
+                  v_new=step.v_new[ridx].cpu(), k_cache=step.k_cache[idx].cpu(),
+                  v_cache=step.v_cache[idx].cpu(), block_table=nbt, cu_seqlens_q=cu,
+                  seqlens_kv=kv, slot_mapping=None, scale=step.scale)
+    return sub, rows
 
 
 def config1_decode(seed=0, device="cpu", num_blocks=512):
@@ -193,3 +234,34 @@ def fragmented_block_tables(lks, *, num_blocks, block_size, ops=10000, seed=0):
             if kv.can_allocate(n):
                 live.append(kv.allocate(n))
     return [kv.allocate(lk) for lk in lks], kv
+
+
+def config2_mixed(seed=0, device="cpu"):
+    """Qwen2-7B heads (28 q / 4 kv / 128), block 128,
+    token budget 2048 = 3 prefill chunks of 512 continuing a prefix
+    U[0, 1024] (causal inside the chunk) + 512 decode rows with contexts
+    U[256, 4096]; 25% of requests share their first 4 blocks; values N(0,1)."""
+    rng = np.random.default_rng(seed)
+    prefix = rng.integers(0, 1024, size=3, endpoint=True).tolist()
+    dec = rng.integers(256, 4096, size=512, endpoint=True).tolist()
+    lqs = [512] * 3 + [1] * 512
+    lks = [p + 512 for p in prefix] + dec
+    return make_gqa_step(lqs=lqs, lks=lks, num_q_heads=28, num_kv_heads=4, block_size=128,
+                         seed=seed + 1, shared_prefix_blocks=4, share_frac=0.25, device=device)
+
+
+def config4_mtp(seed=0, device="cpu"):
+    """MiMo-7B heads (32 q / 8 kv / 128), block 128, batch
+    16, query length 2 (accepted token + one draft, causal in the pair),
+    contexts U[1024, 4096]; values N(0,1)."""
+    rng = np.random.default_rng(seed)
+    lks = rng.integers(1024, 4096, size=16, endpoint=True).tolist()
+    return make_gqa_step(lqs=[2] * 16, lks=lks, num_q_heads=32, num_kv_heads=8,
+                         block_size=128, seed=seed + 1, device=device)
+
+
+def config5_contexts(seed=0, batch=256):
+    """BASELINE config 5 contexts: lognormal (median 2048, sigma 1), clipped
+    to [64, 32768]."""
+    rng = np.random.default_rng(seed)
+    return np.clip(rng.lognormal(np.log(2048), 1.0, size=batch), 64, 32768).astype(int).tolist()

@@ -273,7 +273,18 @@ struct AttnArgs {
   uint16_t* out;
   int64_t o_ts, o_hs;
   int32_t waves;
+  const int32_t* hdr;
+  int32_t batch, tokens;
 };
+
+// A record is used only if it lies inside the plan (defence against a plan
+// read before its planner finished, e.g. from another stream).
+__device__ __forceinline__ bool rec_ok(const int* r, int nseg_tiles, int batch, int tokens,
+                                       int ngroups, int nhb) {
+  return r[0] >= 0 && r[0] < batch && (r[1] & 0xffff) < ngroups && (r[1] >> 16) < nhb &&
+         r[2] >= 0 && r[3] >= 1 && r[2] + r[3] <= tokens && r[5] >= 0 && r[5] < r[6] &&
+         r[6] <= nseg_tiles;
+}
 
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima), gfx9 encoding.
 constexpr int kWaitVmcnt0 = 0x0F70;
@@ -569,16 +580,19 @@ void gqa_attn_kernel(AttnArgs a) {
   if (w >= a.waves) return;
   const int* wr = a.wave_rec + (int64_t)w * kRecInts;
   const int pre = wr[16 + (lane & (kRecBlocks - 1))];   // issued with the header
+  const int nseg = a.hdr[0], total_tiles = a.hdr[1];
+  const int ngroups = (a.hkv + NW - 1) / NW, nhb = (a.group + a.hb - 1) / a.hb;
   int s = wr[0];
-  if (s < 0) return;
   int t = wr[1];
   const int t_end = wr[2], tpw = wr[3];
+  if (s < 0 || s >= nseg || t < 0 || t >= t_end || t_end > total_tiles || tpw < 1) return;
   int rec[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) rec[i] = wr[4 + i];
   uint16_t* vt = vt_all[wid];
   bool first = true;
   while (true) {
+    if (!rec_ok(rec, total_tiles, a.batch, a.tokens, ngroups, nhb)) return;
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
       if ((rec[1] & 0xffff) * NW + wid < a.hkv)
@@ -588,7 +602,7 @@ void gqa_attn_kernel(AttnArgs a) {
       t = chunk_end;
       if (t >= t_end) break;
     }
-    ++s;
+    if (++s >= nseg) return;
     const int* r = a.seg + (int64_t)s * 8;
 #pragma unroll
     for (int i = 0; i < 8; ++i) rec[i] = r[i];
@@ -605,13 +619,12 @@ struct MergeArgs {
   int32_t group, hb, dv, nw, hkv;
 };
 
-// One work-group per (split segment, kv head): each half of the group takes
-// every other row, a thread owns one output dim (looping when dv > 128).
-// The max over the partials' m is taken first, then the weighted sum; both
-// loops are unrolled so the loads of many partials are in flight together.
+// One work-group per (split segment, kv head); thread = (row, 8 dims),
+// looping over the dims when dv > 128.  Single pass with a running rescale,
+// unrolled so the loads of successive partials are in flight together.
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int nseg = a.hdr[0], tpw = a.hdr[2];
-  const int half = threadIdx.x >> 7, t = threadIdx.x & 127;
+  const int n = threadIdx.x >> 4;
   for (int sw = blockIdx.x; sw < nseg * a.nw; sw += gridDim.x) {
     const int s = sw / a.nw, wid = sw - s * a.nw;
     const int4 r0 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8);
@@ -620,28 +633,37 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     const int np = te > tb ? (te - 1) / tpw - tb / tpw + 1 : 0;
     if (np <= 1) continue;
     const int kvh = (r0.y & 0xffff) * a.nw + wid, hbi = r0.y >> 16, qtok0 = r0.z, nq = r0.w;
-    if (kvh >= a.hkv) continue;
-    const int rows = nq * a.hb;                 // valid rows are a prefix
+    if (kvh >= a.hkv || n >= nq * a.hb) continue;   // valid rows are a prefix
+    const int qi = n / a.hb, hh = n - qi * a.hb;
+    const int head = kvh * a.group + hbi * a.hb + hh;
+    const int64_t row0 = ((int64_t)r1.w * a.nw + wid) * kRows + n;
     const int64_t pstride = (int64_t)a.nw * kRows;
-    for (int r = half; r < rows; r += 2) {
-      const int qi = r / a.hb, hh = r - qi * a.hb;
-      const int head = kvh * a.group + hbi * a.hb + hh;
-      const int64_t row0 = ((int64_t)r1.w * a.nw + wid) * kRows + r;
-      float mx = -1e30f;
-#pragma unroll 8
-      for (int k = 0; k < np; ++k) mx = fmaxf(mx, a.part_ml[row0 + k * pstride].x);
-      uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs;
-      for (int d = t; d < a.dv; d += 128) {
-        float acc = 0.f, ls = 0.f;
-#pragma unroll 8
-        for (int k = 0; k < np; ++k) {
-          const float2 ml = a.part_ml[row0 + k * pstride];
-          const float wk = __builtin_amdgcn_exp2f(ml.x - mx);
-          ls += ml.y * wk;
-          acc += a.part_o[(row0 + k * pstride) * a.dv + d] * wk;
-        }
-        op[d] = (uint16_t)aia::f32_to_bf16_bits(ls > 0.f ? acc / ls : 0.f);
+    uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs;
+    for (int c = (threadIdx.x & 15) * 8; c < a.dv; c += 128) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      float mx = -1e30f, ls = 0.f;
+#pragma unroll 4
+      for (int k = 0; k < np; ++k) {
+        const int64_t pr = row0 + k * pstride;
+        const float2 ml = a.part_ml[pr];
+        const float4* src = reinterpret_cast<const float4*>(a.part_o + pr * a.dv + c);
+        const float4 x0 = src[0], x1 = src[1];
+        const float mn = fmaxf(mx, ml.x);
+        const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
+        ls = ls * sa + ml.y * sb;
+        acc[0] = acc[0] * sa + x0.x * sb; acc[1] = acc[1] * sa + x0.y * sb;
+        acc[2] = acc[2] * sa + x0.z * sb; acc[3] = acc[3] * sa + x0.w * sb;
+        acc[4] = acc[4] * sa + x1.x * sb; acc[5] = acc[5] * sa + x1.y * sb;
+        acc[6] = acc[6] * sa + x1.z * sb; acc[7] = acc[7] * sa + x1.w * sb;
+        mx = mn;
       }
+      const float inv = ls > 0.f ? 1.f / ls : 0.f;
+      uint4 wv;
+      wv.x = aia::pack_bf16x2(acc[0] * inv, acc[1] * inv);
+      wv.y = aia::pack_bf16x2(acc[2] * inv, acc[3] * inv);
+      wv.z = aia::pack_bf16x2(acc[4] * inv, acc[5] * inv);
+      wv.w = aia::pack_bf16x2(acc[6] * inv, acc[7] * inv);
+      *reinterpret_cast<uint4*>(op + c) = wv;
     }
   }
 }
@@ -672,6 +694,8 @@ struct MlaArgs {
   uint16_t* out;
   int64_t o_ts, o_hs;
   int32_t waves;
+  const int32_t* hdr;
+  int32_t batch, tokens;
 };
 
 __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, int lt0, int lt1,
@@ -837,15 +861,18 @@ __global__ __launch_bounds__(256) void mla_attn_kernel(MlaArgs a) {
   if (w >= a.waves) return;
   const int* wr = a.wave_rec + (int64_t)w * kRecInts;
   const int pre = wr[16 + (lane & (kRecBlocks - 1))];
+  const int nseg = a.hdr[0], total_tiles = a.hdr[1];
+  const int nhb = (a.group + a.hb - 1) / a.hb;
   int s = wr[0];
-  if (s < 0) return;
   int t = wr[1];
   const int t_end = wr[2], tpw = wr[3];
+  if (s < 0 || s >= nseg || t < 0 || t >= t_end || t_end > total_tiles || tpw < 1) return;
   int rec[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) rec[i] = wr[4 + i];
   bool first = true;
   while (true) {
+    if (!rec_ok(rec, total_tiles, a.batch, a.tokens, 1, nhb)) return;
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
       mla_segment(a, rec, t - rec[5], chunk_end - rec[5], w, tpw, vt_all[wid], sx, lane, wid,
@@ -854,7 +881,7 @@ __global__ __launch_bounds__(256) void mla_attn_kernel(MlaArgs a) {
       t = chunk_end;
       if (t >= t_end) break;
     }
-    ++s;
+    if (++s >= nseg) return;
     const int* r = a.seg + (int64_t)s * 8;
 #pragma unroll
     for (int i = 0; i < 8; ++i) rec[i] = r[i];
@@ -972,6 +999,8 @@ extern "C" int aia_paged_attention_gqa(
   a.out = static_cast<uint16_t*>(out);
   a.o_ts = out_token_stride; a.o_hs = out_head_stride;
   a.waves = waves;
+  a.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
+  a.batch = batch; a.tokens = num_tokens;
   a.counters = reinterpret_cast<int32_t*>(ws + L.cnt);
   a.fused_merge = (flags & AIA_ATTN_FUSED_MERGE) && !(flags & AIA_ATTN_SKIP_MERGE) ? 1 : 0;
   hipStream_t s = (hipStream_t)stream;
@@ -1034,6 +1063,8 @@ extern "C" int aia_paged_attention_mla(
   a.out = static_cast<uint16_t*>(out);
   a.o_ts = out_token_stride; a.o_hs = out_head_stride;
   a.waves = waves;
+  a.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
+  a.batch = batch; a.tokens = num_tokens;
   hipStream_t s = (hipStream_t)stream;
   mla_attn_kernel<<<waves, 256, 0, s>>>(a);
   if (int rc = check_hip(hipGetLastError(), "mla_attn_kernel launch")) return rc;

@@ -155,7 +155,9 @@ class AttentionPlan:
 
     def replan(self):
         """Re-run the device planner on the (possibly updated in place)
-        metadata tensors; graph-capturable."""
+        metadata tensors; graph-capturable.  The plan is then valid on the
+        current stream (attention calls on another stream wait for it)."""
+        self.stream = torch.cuda.current_stream(self.block_table.device)
         _native.call("aia_attn_plan", _ptr(self.cu_seqlens_q), _ptr(self.seqlens_kv),
                      _ptr(self.block_table), self.block_table.stride(0), self.block_size,
                      self.batch, self.num_tokens, self.num_q_heads, self.num_kv_heads,
@@ -177,6 +179,18 @@ class AttentionPlan:
         total = cu_seqlens_q[-1] if len(cu_seqlens_q) else 0
         return cls(block_table, cu, kv, total, num_q_heads, num_kv_heads, head_dim_v, block_size,
                    **kw)
+
+
+def _ready(plan, device):
+    """Order the attention launch after the planner: on another stream, make
+    the current stream wait for the plan's stream (not allowed while
+    capturing a graph, where the plan must be made on the capturing stream)."""
+    cur = torch.cuda.current_stream(device)
+    if cur != plan.stream:
+        if torch.cuda.is_current_stream_capturing():
+            raise ValueError("attention plan was made on another stream than the one being "
+                             "captured; call plan.replan() on the capturing stream")
+        cur.wait_stream(plan.stream)
 
 
 ATTN_SKIP_MERGE = 1         # diagnostic: the split kernel alone, split rows unmerged
@@ -204,6 +218,7 @@ def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None, fl
              and bs == plan.block_size, "plan was made for another shape")
     if out is None:
         out = torch.empty(T, hq, d, dtype=_BF16, device=query.device)
+    _ready(plan, query.device)
     _native.call("aia_paged_attention_gqa", _ptr(query), query.stride(0), query.stride(1),
                  _ptr(key_cache), _ptr(value_cache), _ptr(plan.block_table),
                  plan.block_table.stride(0), _ptr(plan.cu_seqlens_q), _ptr(plan.seqlens_kv),
@@ -247,6 +262,7 @@ def paged_attention_mla(q_latent, latent_cache, plan, scale, out=None, flags=0):
              "plan was not made for this MLA shape")
     if out is None:
         out = torch.empty(T, h, MLA_LATENT, dtype=_BF16, device=q_latent.device)
+    _ready(plan, q_latent.device)
     _native.call("aia_paged_attention_mla", _ptr(q_latent), q_latent.stride(0),
                  q_latent.stride(1), _ptr(latent_cache), _ptr(plan.block_table),
                  plan.block_table.stride(0), _ptr(plan.cu_seqlens_q), _ptr(plan.seqlens_kv),

@@ -182,7 +182,7 @@ class MlaStep:
 
 
 def make_mla_step(*, lqs, lks, num_heads=16, block_size=128, num_blocks=None, seed=0,
-                  extra_blocks=0, dtype=torch.bfloat16, scale=192 ** -0.5):
+                  extra_blocks=0, dtype=torch.bfloat16, scale=192 ** -0.5, device="cpu"):
     """Absorbed-MLA step (latent 512 + rope 64 per token, one KV head)."""
     rng = np.random.default_rng(seed)
     need = sum((lk + block_size - 1) // block_size for lk in lks)
@@ -193,29 +193,37 @@ def make_mla_step(*, lqs, lks, num_heads=16, block_size=128, num_blocks=None, se
     bt = np.zeros((len(lks), max(width, 1)), dtype=np.int32)
     for i, t in enumerate(tables):
         bt[i, :len(t)] = t
-    gen = torch.Generator().manual_seed(seed)
+    dev = torch.device(device)
+    gen = torch.Generator(device=dev).manual_seed(seed)
     T = sum(lqs)
-    q = torch.randn(T, num_heads, 576, generator=gen).to(dtype)
-    lat = torch.randn(T, 1, 576, generator=gen).to(dtype)
-    cache = torch.randn(num_blocks, block_size, 1, 576, generator=gen).to(dtype)
+    if dev.type == "cpu":
+        q = torch.randn(T, num_heads, 576, generator=gen).to(dtype)
+        lat = torch.randn(T, 1, 576, generator=gen).to(dtype)
+        cache = torch.randn(num_blocks, block_size, 1, 576, generator=gen).to(dtype)
+    else:
+        q = torch.randn(T, num_heads, 576, generator=gen, device=dev, dtype=dtype)
+        lat = torch.randn(T, 1, 576, generator=gen, device=dev, dtype=dtype)
+        cache = torch.randn(num_blocks, block_size, 1, 576, generator=gen, device=dev, dtype=dtype)
     slots, cu, acc = [], [], 0
     for b, (lq, lk) in enumerate(zip(lqs, lks)):
         for p in range(lk - lq, lk):
             slots.append(bt[b, p // block_size] * block_size + p % block_size)
         acc += lq
         cu.append(acc)
-    return MlaStep(q_latent=q, latent_new=lat, cache=cache, block_table=torch.from_numpy(bt),
-                   cu_seqlens_q=cu, seqlens_kv=list(lks),
-                   slot_mapping=torch.tensor(slots, dtype=torch.int32), scale=scale)
+    return MlaStep(q_latent=q, latent_new=lat, cache=cache,
+                   block_table=torch.from_numpy(bt).to(dev), cu_seqlens_q=cu,
+                   seqlens_kv=list(lks),
+                   slot_mapping=torch.tensor(slots, dtype=torch.int32, device=dev), scale=scale)
 
 
-def config3_mla(seed=0):
+def config3_mla(seed=0, device="cpu"):
     """absorbed MLA, 16 heads, latent 512 + rope 64,
     block 128, batch 64, query length 1, contexts log-uniform [512, 8192],
     values N(0,1), scale 1/sqrt(192)."""
     rng = np.random.default_rng(seed)
     lks = np.exp(rng.uniform(np.log(512), np.log(8192), size=64)).astype(int).tolist()
-    return make_mla_step(lqs=[1] * 64, lks=lks, num_heads=16, block_size=128, seed=seed + 1)
+    return make_mla_step(lqs=[1] * 64, lks=lks, num_heads=16, block_size=128, seed=seed + 1,
+                         device=device)
 
 
 def fragmented_block_tables(lks, *, num_blocks, block_size, ops=10000, seed=0):

@@ -41,6 +41,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-other-configs", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 256 MiB device copy 10 times (the reference "
                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -103,6 +104,125 @@ def cpu_baseline(step, budget_s):
     }
 
 
+def _time_graph(fn, stream, reps, inner):
+    """Capture `inner` calls of fn(i) in a HIP graph on `stream`; return the
+    average microseconds per call over `reps` replays (HIP events)."""
+    with torch.cuda.stream(stream):
+        for i in range(inner):
+            fn(i)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(inner):
+                fn(i)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * inner)
+
+
+def other_configs(stream):
+    """Attention (+ merge) time of BASELINE configs 2-5 at full size, each
+    with enough rotating caches to exceed the Infinity Cache."""
+    import time as _time
+    import numpy as np
+    from auto_infer_amd import ops, packing, workloads
+    from auto_infer_amd.execution import BatchPlan, RequestView, ScheduledRequest
+    dev = torch.device("cuda:0")
+    res = {}
+
+    def gqa(name, step, pools):
+        kcs = [step.k_cache] + [torch.empty_like(step.k_cache).copy_(step.k_cache)
+                                for _ in range(pools - 1)]
+        vcs = [step.v_cache] + [torch.empty_like(step.v_cache).copy_(step.v_cache)
+                                for _ in range(pools - 1)]
+        hq, hkv, d = step.q.shape[1], step.k_cache.shape[2], step.q.shape[2]
+        plan = ops.AttentionPlan.from_lists(step.block_table, step.cu_seqlens_q,
+                                            step.seqlens_kv, hq, hkv, d, step.k_cache.shape[1])
+        out = torch.empty(step.num_tokens, hq, d, dtype=torch.bfloat16, device=dev)
+        torch.cuda.synchronize()
+        us = _time_graph(lambda i: ops.paged_attention_gqa(step.q, kcs[i % pools],
+                                                           vcs[i % pools], plan, step.scale,
+                                                           out=out), stream, 5, 2 * pools)
+        by = step.kv_bytes_read() + 2 * out.numel() * 2
+        res[name] = {"attn_us": round(us, 2), "kv_MB": round(step.kv_bytes_read() / 1e6, 1),
+                     "GBps": round(by / us / 1e3, 1),
+                     "frac_of_peak": round(by / us / 1e3 / HBM_PEAK_GBS, 4),
+                     "tok_per_s": round(len(step.seqlens_kv) / (us * 1e-6), 1)}
+        del kcs, vcs
+
+    def note(msg):
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    note("configs[1] mixed prefill + decode")
+    gqa("configs[1]_mixed_prefill_decode", workloads.config2_mixed(seed=0, device=dev), 1)
+    note("configs[3] MTP verify")
+    gqa("configs[3]_mtp_verify", workloads.config4_mtp(seed=0, device=dev), 3)
+    note("configs[2] absorbed MLA")
+
+    mla = workloads.config3_mla(seed=0, device=dev)
+    caches = [mla.cache] + [torch.empty_like(mla.cache).copy_(mla.cache) for _ in range(2)]
+    plan = ops.AttentionPlan.from_lists(mla.block_table, mla.cu_seqlens_q, mla.seqlens_kv, 16,
+                                        1, 512, 128)
+    out = torch.empty(64, 16, 512, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    us = _time_graph(lambda i: ops.paged_attention_mla(mla.q_latent, caches[i % 3], plan,
+                                                       mla.scale, out=out), stream, 5, 6)
+    by = mla.kv_bytes_read()
+    res["configs[2]_absorbed_mla"] = {"attn_us": round(us, 2), "kv_MB": round(by / 1e6, 1),
+                                      "GBps": round(by / us / 1e3, 1),
+                                      "frac_of_peak": round(by / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del caches, mla
+
+    note("configs[4] stress: 80 GB pool")
+    # config 5: 80 GB fragmented pool, GPU packing of the 256-request plan
+    bs, hkv, d, hq = 128, 8, 128, 64
+    nb = int(80e9) // (bs * hkv * d * 2 * 2)
+    lks = workloads.config5_contexts(seed=0)
+    tables, _ = workloads.fragmented_block_tables(lks, num_blocks=nb, block_size=bs,
+                                                  ops=10000, seed=0)
+    step = workloads.make_gqa_step(lqs=[1] * 256, lks=lks, num_q_heads=hq, num_kv_heads=hkv,
+                                   block_size=bs, num_blocks=nb, seed=2, device=dev,
+                                   tables=tables)
+    views = {f"r{i}": RequestView(f"r{i}", tuple(range(lk)), lk - 1, 1, 1, ())
+             for i, lk in enumerate(lks)}
+    bplan = BatchPlan.make([ScheduledRequest(f"r{i}", 1, False, tuple(t))
+                            for i, t in enumerate(tables)], views,
+                           {f"r{i}": t for i, t in enumerate(tables)})
+    packer = packing.DeviceBatchPacker(bs, dev)
+    with torch.cuda.stream(stream):
+        packer.build(bplan)                     # first step uploads every block
+        torch.cuda.synchronize()
+        host = []
+        for _ in range(20):
+            t0 = _time.perf_counter()
+            ctx, _, _ = packer.build(bplan)     # steady state: nothing new to upload
+            host.append(_time.perf_counter() - t0)
+        torch.cuda.synchronize()
+    plan_a = ops.AttentionPlan(ctx.block_table, ctx.aia_cu_seqlens_q, ctx.aia_seqlens_kv, 256,
+                               hq, hkv, d, bs)
+    out = torch.empty(256, hq, d, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    us = _time_graph(lambda i: ops.paged_attention_gqa(step.q, step.k_cache, step.v_cache,
+                                                       plan_a, step.scale, out=out),
+                     stream, 5, 2)
+    plan_us = _time_graph(lambda i: plan_a.replan(), stream, 5, 10)
+    by = step.kv_bytes_read()
+    res["configs[4]_stress"] = {
+        "attn_us": round(us, 2), "kv_MB": round(by / 1e6, 1), "GBps": round(by / us / 1e3, 1),
+        "frac_of_peak": round(by / us / 1e3 / HBM_PEAK_GBS, 4),
+        "tok_per_s": round(256 / (us * 1e-6), 1),
+        "packing_host_us_per_step": round(sorted(host)[len(host) // 2] * 1e6, 1),
+        "attn_plan_us": round(plan_us, 2)}
+    del step
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -136,6 +256,7 @@ def main():
     cu = torch.tensor([0, *step.cu_seqlens_q], dtype=torch.int32, device=dev)
     kvl = torch.tensor(step.seqlens_kv, dtype=torch.int32, device=dev)
     plan = ops.AttentionPlan(bt, cu, kvl, T, hq, hkv, d, step.k_cache.shape[1])
+    torch.cuda.synchronize()
 
     def model_step():
         """Planner once, then L layers of (KV write + attention)."""
@@ -255,6 +376,11 @@ def main():
             "algorithmic_bytes": attn_alg_bytes,
         },
     }
+    if not args.no_other_configs:
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            result["other_configs"] = other_configs(stream)
+        torch.cuda.synchronize()
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(step, args.cpu_seconds)
     print(json.dumps(result), flush=True)

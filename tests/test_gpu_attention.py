@@ -128,3 +128,21 @@ def test_empty_context_rows_are_zero():
     step.seqlens_kv = [0, 40]        # request 0 sees nothing
     got = run_gpu(step)
     assert torch.count_nonzero(got[0]) == 0
+
+
+def test_plan_from_another_stream_is_waited_for():
+    """A plan made on one stream is used on another: the attention waits."""
+    step = workloads.make_gqa_step(lqs=[1, 3], lks=[700, 90], num_q_heads=8, num_kv_heads=2,
+                                   block_size=16, seed=17)
+    q, kc, vc = step.q.to(DEV), step.k_cache.to(DEV), step.v_cache.to(DEV)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, 8, 2, 128, 16)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        out = ops.paged_attention_gqa(q, kc, vc, plan, step.scale)
+    torch.cuda.synchronize()
+    assert (out.float().cpu() - oracle(step)).abs().max().item() <= TOL
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(ValueError, match="another stream"):
+        with torch.cuda.graph(g, stream=side):
+            ops.paged_attention_gqa(q, kc, vc, plan, step.scale)

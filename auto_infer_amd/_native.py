@@ -33,7 +33,8 @@ SIGNATURES = {
                       c_vp, c_i64, c_vp],
     "aia_paged_attention_gqa": [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp,
                                 c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32,
-                                c_vp, c_i64, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp],
+                                c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i32, c_i32,
+                                c_vp, c_i64, c_vp],
     "aia_paged_attention_mla": [c_vp, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp, c_vp, c_i32,
                                 c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp,
                                 c_i64, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp],

@@ -23,7 +23,7 @@ class GqaHipBackend(AttentionBackend):
 
     def __init__(self, n_q_heads: int, n_kv_heads: int, head_dim: int, scale: float,
                  num_layers: int, device, dtype, w: dict = None, layer_prefix=None,
-                 rms_eps=None):
+                 rms_eps=None, fuse_kv_write: bool = True):
         self.n_q_heads = n_q_heads
         self.n_kv_heads = n_kv_heads
         self.head_dim = head_dim
@@ -34,6 +34,11 @@ class GqaHipBackend(AttentionBackend):
         self.w = w
         self.layer_prefix = layer_prefix or (lambda i: f"model.layers.{i}.")
         self.rms_eps = rms_eps
+        # With fuse_kv_write, _write_kv defers the slot write to the attention
+        # kernel of the following _attn (same cache contents, one launch less);
+        # attention() always calls the two in that order.
+        self.fuse_kv_write = fuse_kv_write
+        self._pending = None
 
     def alloc_kv_caches(self, num_blocks: int, block_size: int) -> list:
         shape = (2, num_blocks, block_size, self.n_kv_heads, self.head_dim)
@@ -62,9 +67,20 @@ class GqaHipBackend(AttentionBackend):
 
     def _write_kv(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor, ctx) -> None:
         cache = ctx.kv_caches[layer_idx]
+        if self.fuse_kv_write and k.shape[0] == ctx.slot_mapping.shape[0]:
+            self._pending = (layer_idx, id(ctx), k, v)
+            return
         ops.write_kv(k, v, cache[0], cache[1], ctx.slot_mapping)
 
     def _attn(self, layer_idx: int, q, k, v, ctx) -> torch.Tensor:
         cache = ctx.kv_caches[layer_idx]
         plan = step_plan(ctx, self.n_q_heads, self.n_kv_heads, self.head_dim, cache.shape[2])
+        pending, self._pending = self._pending, None
+        if pending is not None and pending[:2] == (layer_idx, id(ctx)):
+            return ops.paged_attention_gqa(q, cache[0], cache[1], plan, self.scale,
+                                           key_new=pending[2], value_new=pending[3])
+        if pending is not None:      # a deferred write for another call: do it now
+            lay, _, pk, pv = pending
+            c = ctx.kv_caches[lay]
+            ops.write_kv(pk, pv, c[0], c[1], ctx.slot_mapping)
         return ops.paged_attention_gqa(q, cache[0], cache[1], plan, self.scale)

@@ -65,7 +65,7 @@ Geometry geometry(int32_t hq, int32_t hkv) {
 
 // Workspace layout (all offsets 256-byte aligned).
 struct Layout {
-  int64_t hdr, seg, wave, part_ml, part_o, cnt, total;
+  int64_t hdr, seg, wave, part_ml, part_o, cnt, req, total;
   int64_t seg_cap, part_cap;
 };
 
@@ -82,6 +82,7 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
   L.part_ml = off;  off = align256(off + L.part_cap * g.nw * kRows * 8);
   L.part_o = off;   off = align256(off + L.part_cap * g.nw * kRows * (int64_t)dv * 4);
   L.cnt = off;      off = align256(off + L.seg_cap * g.nw * 4);
+  L.req = off;      off = align256(off + ((int64_t)batch + 1) * 4);
   L.total = off;
   return L;
 }
@@ -125,27 +126,48 @@ __device__ int block_exclusive_scan(int v, int* wave_sums, int* total) {
   return before + x - v;
 }
 
-// Segment record, 8 ints: b, kv-head group | head block << 16, first query token (global row),
-// query tokens, lim_base = Lk - Lq + q0 (last key of the block's first
+// Segment record, 8 ints: b, kv-head group | head block << 16 | (last query
+// block of its request) << 30, first query
+// token (global row), query tokens | q0 << 8 (q0 = first query of the block
+// within its request), lim_base = Lk - Lq + q0 (last key of the block's first
 // row), tile_begin, tile_end, part_base.
+//
+// The planner keeps the request metadata (request offsets, cu_seqlens_q,
+// seqlens_kv) and later the segments' first tiles in LDS, and each thread
+// keeps its own segments' tile counts in registers, so its phases cost one
+// global round trip each (metadata in, block ids in) rather than one per
+// dependent lookup.
+constexpr int kPlanLds = 12288;          // ints of LDS scratch (48 KB)
+constexpr int kPlanRegChunks = 8;        // segments kept in registers: 8 x 1024
+
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ kvlen,
     const int32_t* __restrict__ block_table, int64_t bt_stride, int32_t block_size,
     int32_t batch, Geometry g, int32_t waves,
     int32_t* __restrict__ hdr, int32_t* __restrict__ seg, int32_t* __restrict__ wave_rec,
-    int32_t* __restrict__ counters) {
-  __shared__ int req_off[kMaxBatch + 1];
+    int32_t* __restrict__ counters, int32_t* __restrict__ req_scratch) {
+  __shared__ int lds[kPlanLds];
   __shared__ int wave_sums[kPlanThreads / 64];
   const int tid = threadIdx.x;
   const int per_req = g.nkvg * g.nhb;
+  // request metadata in LDS when it fits, else in the workspace / inputs
+  const bool req_lds = 3 * (batch + 1) <= kPlanLds;
+  int* req_off = req_lds ? lds : req_scratch;
+  int* cuv = req_lds ? lds + (batch + 1) : nullptr;
+  int* kvv = req_lds ? lds + 2 * (batch + 1) : nullptr;
 
-  // 1) segments per request -> request offsets (LDS)
+  // 1) segments per request -> request offsets
   int carry = 0;
   for (int base = 0; base < batch; base += kPlanThreads) {
     const int b = base + tid;
     int cnt = 0;
     if (b < batch) {
-      const int lq = cu_q[b + 1] - cu_q[b];
+      const int c0 = cu_q[b], c1 = cu_q[b + 1], lk = kvlen[b];
+      if (req_lds) {
+        cuv[b] = c0; kvv[b] = lk;
+        if (b == batch - 1) cuv[batch] = c1;
+      }
+      const int lq = c1 - c0;
       cnt = lq > 0 ? ((lq + g.qb - 1) / g.qb) * per_req : 0;
     }
     int tot;
@@ -156,13 +178,17 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   if (tid == 0) req_off[batch] = carry;
   __syncthreads();
   const int nseg = req_off[batch];
+  const int* cu_r = req_lds ? cuv : cu_q;
+  const int* kv_r = req_lds ? kvv : kvlen;
+  const bool regs = nseg <= kPlanRegChunks * kPlanThreads;
 
   // 2) segment records and their key tiles
+  int my_tb[kPlanRegChunks], my_nt[kPlanRegChunks];
   carry = 0;
-  for (int base = 0; base < nseg; base += kPlanThreads) {
+  for (int base = 0, c = 0; base < nseg; base += kPlanThreads, ++c) {
     const int s = base + tid;
     int ntiles = 0;
-    int rec[6];
+    int rec[5];
     if (s < nseg) {
       int lo = 0, hi = batch - 1;  // last b with req_off[b] <= s
       while (lo < hi) {
@@ -174,9 +200,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       const int hb = local % g.nhb;
       const int kvg = (local / g.nhb) % g.nkvg;
       const int qblk = local / per_req;
-      const int q_begin = cu_q[b];
-      const int lq = cu_q[b + 1] - q_begin;
-      const int lk = kvlen[b];
+      const int q_begin = cu_r[b];
+      const int lq = cu_r[b + 1] - q_begin;
+      const int lk = kv_r[b];
       const int q0 = qblk * g.qb;
       const int nq = min(g.qb, lq - q0);
       const int lim_base = lk - lq + q0;
@@ -184,8 +210,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       // at least one (fully masked) tile, so the work-group that owns it
       // writes the zero output of rows that see no key
       ntiles = max(1, (visible + kTile - 1) / kTile);
-      rec[0] = b; rec[1] = kvg | (hb << 16); rec[2] = q_begin + q0; rec[3] = nq;
-      rec[4] = lim_base; rec[5] = ntiles;
+      rec[0] = b; rec[1] = kvg | (hb << 16) | ((q0 + nq == lq) << 30);
+      rec[2] = q_begin + q0; rec[3] = nq | (q0 << 8);
+      rec[4] = lim_base;
     }
     int tot;
     const int ex = block_exclusive_scan(ntiles, wave_sums, &tot);
@@ -194,20 +221,42 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       r[0] = rec[0]; r[1] = rec[1]; r[2] = rec[2]; r[3] = rec[3]; r[4] = rec[4];
       r[5] = carry + ex; r[6] = carry + ex + ntiles;
     }
+#pragma unroll
+    for (int i = 0; i < kPlanRegChunks; ++i)
+      if (i == c) { my_tb[i] = carry + ex; my_nt[i] = ntiles; }
     carry += tot;
   }
   const int total_tiles = carry;
   const int tpw = max(1, (total_tiles + waves - 1) / waves);
-  __syncthreads();
+  __syncthreads();   // request metadata in LDS is no longer needed
 
-  // 3) partial slots: a segment split over k waves owns k consecutive slots
+  // segments' first tiles into LDS for the per-range search
+  const bool tb_lds = regs && nseg + 1 <= kPlanLds;
+  if (tb_lds) {
+#pragma unroll
+    for (int i = 0; i < kPlanRegChunks; ++i) {
+      const int s = i * kPlanThreads + tid;
+      if (s < nseg) lds[s] = my_tb[i];
+    }
+    if (tid == 0) lds[nseg] = total_tiles;
+  }
+
+  // 3) partial slots: a segment split over k ranges owns k consecutive slots
   carry = 0;
-  for (int base = 0; base < nseg; base += kPlanThreads) {
+  for (int base = 0, c = 0; base < nseg; base += kPlanThreads, ++c) {
     const int s = base + tid;
     int np = 0;
     if (s < nseg) {
-      const int tb = seg[(int64_t)s * 8 + 5], te = seg[(int64_t)s * 8 + 6];
-      np = te > tb ? (te - 1) / tpw - tb / tpw + 1 : 0;
+      int tb = 0, nt = 0;
+      if (regs) {
+#pragma unroll
+        for (int i = 0; i < kPlanRegChunks; ++i)
+          if (i == c) { tb = my_tb[i]; nt = my_nt[i]; }
+      } else {
+        tb = seg[(int64_t)s * 8 + 5];
+        nt = seg[(int64_t)s * 8 + 6] - tb;
+      }
+      np = (tb + nt - 1) / tpw - tb / tpw + 1;
     }
     int tot;
     const int ex = block_exclusive_scan(np, wave_sums, &tot);
@@ -237,19 +286,27 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     int lo = 0, hi = nseg - 1;  // last s with tile_begin <= t0
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (seg[(int64_t)mid * 8 + 5] <= t0) lo = mid; else hi = mid - 1;
+      const int tb = tb_lds ? lds[mid] : seg[(int64_t)mid * 8 + 5];
+      if (tb <= t0) lo = mid; else hi = mid - 1;
     }
     out[0] = lo; out[1] = t0; out[2] = min(total_tiles, t0 + tpw); out[3] = tpw;
     const int* r = seg + (int64_t)lo * 8;
-    for (int i = 0; i < 8; ++i) out[4 + i] = r[i];
-    const int b = r[0], nq = r[3], lim_base = r[4];
+    int rr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rr[i] = r[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[4 + i] = rr[i];
+    const int b = rr[0], nq = rr[3] & 0xff, lim_base = rr[4];
     const int visible = max(0, lim_base + nq);
     const int nblk_vis = (visible + block_size - 1) / block_size;
-    const int blk_base = ((t0 - r[5]) * kTile) / block_size;
+    const int blk_base = ((t0 - rr[5]) * kTile) / block_size;
     out[12] = blk_base; out[13] = 0; out[14] = 0; out[15] = 0;
     const int32_t* btrow = block_table + (int64_t)b * bt_stride;
-    for (int i = 0; i < kRecBlocks; ++i)
-      out[16 + i] = blk_base + i < nblk_vis ? btrow[blk_base + i] : 0;
+    int bv[kRecBlocks];
+#pragma unroll
+    for (int i = 0; i < kRecBlocks; ++i) bv[i] = blk_base + i < nblk_vis ? btrow[blk_base + i] : 0;
+#pragma unroll
+    for (int i = 0; i < kRecBlocks; ++i) out[16 + i] = bv[i];
   }
 }
 
@@ -258,8 +315,13 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
 struct AttnArgs {
   const uint16_t* q;
   int64_t q_ts, q_hs;
-  const uint16_t* kc;
-  const uint16_t* vc;
+  uint16_t* kc;
+  uint16_t* vc;
+  // this step's new K/V rows (T, Hkv, D); when set, keys at the new
+  // positions are read from them and written into the cache by the kernel
+  const uint16_t* kn;
+  const uint16_t* vn;
+  int64_t kn_ts, vn_ts;
   const int32_t* bt;
   int64_t bt_stride;
   int32_t hkv, group, hb, bs, nb, nw;
@@ -281,8 +343,8 @@ struct AttnArgs {
 // read before its planner finished, e.g. from another stream).
 __device__ __forceinline__ bool rec_ok(const int* r, int nseg_tiles, int batch, int tokens,
                                        int ngroups, int nhb) {
-  return r[0] >= 0 && r[0] < batch && (r[1] & 0xffff) < ngroups && (r[1] >> 16) < nhb &&
-         r[2] >= 0 && r[3] >= 1 && r[2] + r[3] <= tokens && r[5] >= 0 && r[5] < r[6] &&
+  return r[0] >= 0 && r[0] < batch && (r[1] & 0xffff) < ngroups && ((r[1] >> 16) & 0x3fff) < nhb &&
+         r[2] >= 0 && (r[3] & 0xff) >= 1 && r[2] + (r[3] & 0xff) <= tokens && r[5] >= 0 && r[5] < r[6] &&
          r[6] <= nseg_tiles;
 }
 
@@ -319,8 +381,8 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
                                             int lt1, int w, int tpw, uint16_t* vt, int lane,
                                             int wid, bool use_pre, int pre) {
   const int n = lane & 15, g = lane >> 4;
-  const int b = rec[0], kvh = (rec[1] & 0xffff) * a.nw + wid, hbi = rec[1] >> 16;
-  const int qtok0 = rec[2], nq = rec[3], lim_base = rec[4];
+  const int b = rec[0], kvh = (rec[1] & 0xffff) * a.nw + wid, hbi = (rec[1] >> 16) & 0x3fff;
+  const int qtok0 = rec[2], nq = rec[3] & 0xff, q0 = rec[3] >> 8, lim_base = rec[4];
   const int tile_begin = rec[5], tile_end = rec[6], part_base = rec[7];
   const int qi = n / a.hb, hh = n - qi * a.hb;
   const bool rv = qi < nq && hbi * a.hb + hh < a.group;
@@ -328,6 +390,11 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   const int lim = rv ? lim_base + qi : -1;
   const int visible = max(0, lim_base + nq);
   const int row_elems = a.hkv * kHeadDim;
+  // this step's new keys sit at positions [new_start, Lk); the request's last
+  // query block (head block 0) owns writing them into the cache
+  const int new_start = a.kn ? lim_base - q0 : 0x7fffffff;
+  const int q_begin = qtok0 - q0;
+  const bool writer = a.kn && ((rec[1] >> 30) & 1) && hbi == 0;
 
   const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
   const int nblk_vis = (visible + a.bs - 1) / a.bs;
@@ -355,7 +422,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   // Loads are issued unconditionally (tiles past the window read the first
   // key row again, an L1 hit) so the load stream is straight-line and the
   // compiler can wait for each tile with an exact count.
-  auto load = [&](int lt, uint4 (&kk)[4], uint4 (&vv)[4]) {
+  auto load = [&](int lt, uint4 (&kk)[4], uint4 (&vv)[4], int64_t& wdst) {
     const bool live = lt < w1;
     const int tok = live ? min(lt * kTile + n, visible - 1) : blk_base * a.bs;
     const int bi = tok / a.bs;
@@ -363,15 +430,27 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
     const int blk = min(max(__shfl(btv, bi - blk_base), 0), a.nb - 1);
     const int off = tok - bi * a.bs;
     const int64_t base = ((int64_t)blk * a.bs + off) * row_elems + (int64_t)kvh * kHeadDim;
-    const uint4* kp = reinterpret_cast<const uint4*>(a.kc + base);
-    const uint4* vp = reinterpret_cast<const uint4*>(a.vc + (live ? base : (int64_t)0) );
+    const bool fresh = live && tok >= new_start;
+    const int64_t nrow = (int64_t)(q_begin + tok - new_start);
+    const uint4* kp = reinterpret_cast<const uint4*>(
+        fresh ? a.kn + nrow * a.kn_ts + (int64_t)kvh * kHeadDim : a.kc + base);
+    const uint4* vp = reinterpret_cast<const uint4*>(
+        fresh ? a.vn + nrow * a.vn_ts + (int64_t)kvh * kHeadDim : a.vc + (live ? base : (int64_t)0));
+    // cache slot this lane writes after the tile arrives (-1: nothing)
+    wdst = (writer && fresh && lt * kTile + n < visible) ? base : (int64_t)-1;
 #pragma unroll
     for (int j = 0; j < 4; ++j) kk[j] = kp[4 * j + g];
 #pragma unroll
     for (int j = 0; j < 4; ++j) vv[j] = vp[4 * j + g];
   };
 
-  auto compute = [&](int lt, const uint4 (&kk)[4], const uint4 (&vv)[4]) {
+  auto compute = [&](int lt, const uint4 (&kk)[4], const uint4 (&vv)[4], int64_t wdst) {
+    if (wdst >= 0) {   // KV slot write of a new row (its bytes just arrived)
+      uint4* kd = reinterpret_cast<uint4*>(a.kc + wdst);
+      uint4* vd = reinterpret_cast<uint4*>(a.vc + wdst);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { kd[4 * j + g] = kk[j]; vd[4 * j + g] = vv[j]; }
+    }
 #ifdef AIA_NOCOMPUTE
     {
       uint32_t x = 0;
@@ -422,6 +501,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   };
 
   uint4 kbuf[kPipe][4], vbuf[kPipe][4];
+  int64_t wbuf[kPipe];
   for (int w0 = lt0; w0 < lt1;) {
     blk_base = (w0 * kTile) / a.bs;
     // tiles whose keys all fall inside blocks [blk_base, blk_base + win);
@@ -433,15 +513,15 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
     use_pre = false;
 #pragma unroll
     for (int i = 0; i < kPipe; ++i) {
-      load(w0 + i, kbuf[i], vbuf[i]);
+      load(w0 + i, kbuf[i], vbuf[i], wbuf[i]);
       __builtin_amdgcn_sched_barrier(0);
     }
     for (int base = w0; base < w1; base += kPipe) {
 #pragma unroll
       for (int i = 0; i < kPipe; ++i) {
         const int lt = base + i;
-        if (lt < w1) compute(lt, kbuf[i], vbuf[i]);
-        load(lt + kPipe, kbuf[i], vbuf[i]);
+        if (lt < w1) compute(lt, kbuf[i], vbuf[i], wbuf[i]);
+        load(lt + kPipe, kbuf[i], vbuf[i], wbuf[i]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -632,7 +712,8 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     const int tb = r1.y, te = r1.z;
     const int np = te > tb ? (te - 1) / tpw - tb / tpw + 1 : 0;
     if (np <= 1) continue;
-    const int kvh = (r0.y & 0xffff) * a.nw + wid, hbi = r0.y >> 16, qtok0 = r0.z, nq = r0.w;
+    const int kvh = (r0.y & 0xffff) * a.nw + wid, hbi = (r0.y >> 16) & 0x3fff, qtok0 = r0.z,
+              nq = r0.w & 0xff;
     if (kvh >= a.hkv || n >= nq * a.hb) continue;   // valid rows are a prefix
     const int qi = n / a.hb, hh = n - qi * a.hb;
     const int head = kvh * a.group + hbi * a.hb + hh;
@@ -702,8 +783,8 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
                                             int w, int tpw, uint16_t* vt, float* sx, int lane,
                                             int wid, bool use_pre, int pre) {
   const int n = lane & 15, g = lane >> 4;
-  const int b = rec[0], hbi = rec[1] >> 16;
-  const int qtok0 = rec[2], nq = rec[3], lim_base = rec[4];
+  const int b = rec[0], hbi = (rec[1] >> 16) & 0x3fff;
+  const int qtok0 = rec[2], nq = rec[3] & 0xff, q0 = rec[3] >> 8, lim_base = rec[4];
   const int tile_begin = rec[5], tile_end = rec[6], part_base = rec[7];
   const int qi = n / a.hb, hh = n - qi * a.hb;
   const bool rv = qi < nq && hbi * a.hb + hh < a.group;
@@ -949,7 +1030,7 @@ extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens
   plan_kernel<<<1, kPlanThreads, 0, (hipStream_t)stream>>>(
       cu_seqlens_q, seqlens_kv, block_table, block_table_stride, block_size, batch, g, waves, reinterpret_cast<int32_t*>(ws + L.hdr),
       reinterpret_cast<int32_t*>(ws + L.seg), reinterpret_cast<int32_t*>(ws + L.wave),
-      reinterpret_cast<int32_t*>(ws + L.cnt));
+      reinterpret_cast<int32_t*>(ws + L.cnt), reinterpret_cast<int32_t*>(ws + L.req));
   return check_hip(hipGetLastError(), "aia_attn_plan launch");
 }
 
@@ -959,7 +1040,9 @@ extern "C" int aia_paged_attention_gqa(
     const int32_t* cu_seqlens_q, const int32_t* seqlens_kv, int32_t batch, int32_t num_tokens,
     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
     int32_t num_blocks, float scale, void* out, int64_t out_token_stride, int64_t out_head_stride,
-    int32_t num_waves, int32_t flags, void* workspace, int64_t workspace_bytes, void* stream) {
+    const void* key_new, const void* value_new, int64_t new_key_token_stride,
+    int64_t new_value_token_stride, int32_t num_waves, int32_t flags, void* workspace,
+    int64_t workspace_bytes, void* stream) {
   using namespace aia;
   (void)cu_seqlens_q; (void)seqlens_kv;
   if (int rc = check_heads("aia_paged_attention_gqa", num_q_heads, num_kv_heads)) return rc;
@@ -975,6 +1058,12 @@ extern "C" int aia_paged_attention_gqa(
       ((uintptr_t)out & 15))
     return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: query/out/cache must be 16-byte aligned "
                 "with strides a multiple of 8 elements");
+  if ((key_new == nullptr) != (value_new == nullptr))
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: key_new and value_new go together");
+  if (key_new && (new_key_token_stride % 8 || new_value_token_stride % 8 ||
+                  ((uintptr_t)key_new & 15) || ((uintptr_t)value_new & 15)))
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: new K/V rows must be 16-byte aligned "
+                "with token strides a multiple of 8 elements");
   if (num_tokens == 0 || batch == 0) return AIA_OK;
   const Geometry g = geometry(num_q_heads, num_kv_heads);
   const int32_t waves = resolve_waves(num_waves, g, head_dim);
@@ -986,8 +1075,11 @@ extern "C" int aia_paged_attention_gqa(
   AttnArgs a;
   a.q = static_cast<const uint16_t*>(query);
   a.q_ts = q_token_stride; a.q_hs = q_head_stride;
-  a.kc = static_cast<const uint16_t*>(key_cache);
-  a.vc = static_cast<const uint16_t*>(value_cache);
+  a.kc = static_cast<uint16_t*>(const_cast<void*>(key_cache));
+  a.vc = static_cast<uint16_t*>(const_cast<void*>(value_cache));
+  a.kn = static_cast<const uint16_t*>(key_new);
+  a.vn = static_cast<const uint16_t*>(value_new);
+  a.kn_ts = new_key_token_stride; a.vn_ts = new_value_token_stride;
   a.bt = block_table; a.bt_stride = block_table_stride;
   a.hkv = g.hkv; a.group = g.group; a.hb = g.hb; a.bs = block_size; a.nb = num_blocks;
   a.nw = g.nw;

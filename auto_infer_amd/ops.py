@@ -197,12 +197,15 @@ ATTN_SKIP_MERGE = 1         # diagnostic: the split kernel alone, split rows unm
 ATTN_FUSED_MERGE = 2        # merge split rows inside the split kernel (default: 2nd kernel)
 
 
-def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None, flags=0):
+def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None, flags=0,
+                        key_new=None, value_new=None):
     """Paged GQA attention (reference base.py:48-61 FIA semantics).
 
     query (T, Hq, 128) bf16; key/value caches (NB, bs, Hkv, 128) bf16
     contiguous; ``plan`` an ``AttentionPlan`` of this step.  Returns
-    (T, Hq, 128) bf16.
+    (T, Hq, 128) bf16.  With ``key_new`` / ``value_new`` (this step's new rows,
+    (T, Hkv, 128)) the kernel also writes them into the caches at the slots
+    the block table assigns (the fused form of ``write_kv``).
     """
     _check_device_tensor(query, "query", _BF16)
     _check_device_tensor(key_cache, "key_cache", _BF16)
@@ -218,13 +221,20 @@ def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None, fl
              and bs == plan.block_size, "plan was made for another shape")
     if out is None:
         out = torch.empty(T, hq, d, dtype=_BF16, device=query.device)
+    kn_ts = vn_ts = 0
+    if key_new is not None or value_new is not None:
+        _check_device_tensor(key_new, "key_new", _BF16)
+        _check_device_tensor(value_new, "value_new", _BF16)
+        _require(tuple(key_new.shape) == (T, hkv, d) and tuple(value_new.shape) == (T, hkv, d),
+                 "new K/V rows must be (tokens, Hkv, D)")
+        kn_ts, vn_ts = _row_stride(key_new, "key_new"), _row_stride(value_new, "value_new")
     _ready(plan, query.device)
     _native.call("aia_paged_attention_gqa", _ptr(query), query.stride(0), query.stride(1),
                  _ptr(key_cache), _ptr(value_cache), _ptr(plan.block_table),
                  plan.block_table.stride(0), _ptr(plan.cu_seqlens_q), _ptr(plan.seqlens_kv),
                  plan.batch, T, hq, hkv, d, bs, nb, float(scale), _ptr(out), out.stride(0),
-                 out.stride(1), plan.num_waves, flags, _ptr(plan.workspace),
-                 plan.workspace.numel(), _stream(query.device))
+                 out.stride(1), _ptr(key_new), _ptr(value_new), kn_ts, vn_ts, plan.num_waves,
+                 flags, _ptr(plan.workspace), plan.workspace.numel(), _stream(query.device))
     return out
 
 

@@ -6,7 +6,8 @@ query length 1, contexts U[128, 2048] (seeded), block 128, a 512-block pool
 per layer, values N(0,1)/sqrt(128).
 
 One *step* = one layer's decode attention for the batch: the KV write of the
-16 new rows (slot mapping) + split-K paged attention + partial merge, plus
+16 new rows (fused into the attention kernel) + split-K paged attention +
+partial merge, plus
 1/L of the per-step planner launch (the plan is shared by the L layers of a
 model step).  L = 8 layer caches are rotated (8 x 268 MB > the 256 MB
 Infinity Cache) so KV reads come from HBM.  Steps are replayed from a HIP
@@ -262,8 +263,9 @@ def main():
         """Planner once, then L layers of (KV write + attention)."""
         plan.replan()
         for layer in range(L):
-            ops.write_kv(k_new, v_new, kcs[layer], vcs[layer], slots)
-            ops.paged_attention_gqa(q, kcs[layer], vcs[layer], plan, step.scale, out=out)
+            # the KV slot write of the 16 new rows runs inside the attention kernel
+            ops.paged_attention_gqa(q, kcs[layer], vcs[layer], plan, step.scale, out=out,
+                                    key_new=k_new, value_new=v_new)
 
     stream = torch.cuda.Stream(device=dev)
     with torch.cuda.stream(stream):

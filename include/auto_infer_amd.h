@@ -85,6 +85,12 @@ int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
  * out:    (num_tokens, Hq, head_dim) with the given strides.
  * head_dim must be 128.  The workspace must hold a plan made by
  * aia_attn_plan with the same metadata, head counts and num_waves.
+ * key_new / value_new (optional, both or neither): this step's new K/V rows
+ * (num_tokens, Hkv, 128), query token t being position Lk - Lq + i of its
+ * request.  When given, the kernel also performs the KV slot write of those
+ * rows (what aia_kv_write would do, at slot block_table[b, pos / bs] * bs +
+ * pos % bs -- the slot_mapping every packer produces) and reads the new keys
+ * from the rows themselves, saving the separate write launch.
  * Rows whose keys were split over several work-groups are merged from fp32
  * (O, max, sum) partials by log-sum-exp, by default in a second kernel.
  * flags: AIA_ATTN_FUSED_MERGE merges in the split kernel instead (the last
@@ -103,7 +109,10 @@ int aia_paged_attention_gqa(const void* query, int64_t q_token_stride,
                             int32_t head_dim, int32_t block_size,
                             int32_t num_blocks, float scale,
                             void* out, int64_t out_token_stride,
-                            int64_t out_head_stride, int32_t num_waves,
+                            int64_t out_head_stride,
+                            const void* key_new, const void* value_new,
+                            int64_t new_key_token_stride,
+                            int64_t new_value_token_stride, int32_t num_waves,
                             int32_t flags, void* workspace, int64_t workspace_bytes,
                             void* stream);
 

@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from auto_infer_amd import ops, workloads
-from oracle.paged_attn import paged_attention
+from oracle.paged_attn import kv_write, paged_attention
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -146,3 +146,31 @@ def test_plan_from_another_stream_is_waited_for():
     with pytest.raises(ValueError, match="another stream"):
         with torch.cuda.graph(g, stream=side):
             ops.paged_attention_gqa(q, kc, vc, plan, step.scale)
+
+
+@pytest.mark.parametrize("lqs,lks,hq,hkv,bs,waves", [
+    ([1] * 16, [300, 129, 2048, 17, 1, 700, 901, 64, 65, 128, 1000, 5, 6, 1500, 333, 2],
+     16, 8, 128, 0),                                    # decode, config-1 heads
+    ([37, 1, 5, 1, 64], [137, 300, 5, 77, 64], 28, 4, 16, 0),   # chunked prefill, many q-blocks
+    ([2, 2, 1], [513, 40, 999], 64, 2, 128, 7),        # head blocks (group 32), splits
+    ([2] * 4, [1024, 1500, 2, 4096], 32, 8, 128, 3),   # MTP verify shape
+])
+def test_fused_kv_write(lqs, lks, hq, hkv, bs, waves):
+    """The attention kernel performs the KV slot write of the step's new rows:
+    caches bit-exact with the oracle write, output within tolerance."""
+    step = workloads.make_gqa_step(lqs=lqs, lks=lks, num_q_heads=hq, num_kv_heads=hkv,
+                                   block_size=bs, seed=31, extra_blocks=2)
+    ek, ev = step.k_cache.clone(), step.v_cache.clone()
+    kv_write(step.k_new, step.v_new, ek, ev, step.slot_mapping)
+    exp = paged_attention(step.q, ek, ev, step.block_table, step.cu_seqlens_q, step.seqlens_kv,
+                          step.scale)
+    kc, vc = step.k_cache.to(DEV), step.v_cache.to(DEV)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, hq, hkv, 128, bs, num_waves=waves)
+    out = ops.paged_attention_gqa(step.q.to(DEV), kc, vc, plan, step.scale,
+                                  key_new=step.k_new.to(DEV), value_new=step.v_new.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(kc.cpu(), ek) and torch.equal(vc.cpu(), ev)
+    err = (out.float().cpu() - exp).abs().max().item()
+    print(f"max-abs err {err:.3e}", flush=True)
+    assert err <= TOL

@@ -1,0 +1,71 @@
+"""HIP-graph decode: capture once per gear, replay every step.
+
+The reference captures an ACL graph per decode gear and, after every replay,
+re-issues each layer's attention op with the step's new ``seqlens_kv`` on a
+side thread (auto_infer/worker/graph_decode_runner.py:416-541,
+layers/attention/graph_fia.py:66-95).  The kernels here read all step
+metadata from device buffers, so a captured graph needs no updates: the
+stager rewrites its fixed-address buffers in place (one upload + the packing
+kernel, outside the graph), and the graph -- planner once, then every
+layer's attention with the fused KV write -- is replayed as is.
+"""
+import torch
+
+from auto_infer_amd import ops
+
+
+class DecodeGraph:
+    """One decode gear of GQA layers captured in a HIP graph.
+
+    ``stager``: a ``packing.DecodeInputStager`` or ``SpecDecodeInputStager``
+    whose buffers (slots, block table, cu/kv lengths) the graph reads.
+    ``caches``: per-layer (key_cache, value_cache).  ``q``, ``k_new``,
+    ``v_new``: fixed-address per-layer input buffers (T, H, D) the caller
+    fills before each replay (the projections' outputs); ``out`` receives
+    each layer's attention output.
+    """
+
+    def __init__(self, stager, caches, *, num_q_heads, num_kv_heads, head_dim=128, scale=None,
+                 stream=None):
+        self.stager = stager
+        self.caches = caches
+        dev = stager.block_table.device
+        gear, width = stager.block_table.shape
+        T = stager.slots.shape[0]
+        L = len(caches)
+        self.q = torch.zeros(L, T, num_q_heads, head_dim, dtype=torch.bfloat16, device=dev)
+        self.k_new = torch.zeros(L, T, num_kv_heads, head_dim, dtype=torch.bfloat16, device=dev)
+        self.v_new = torch.zeros_like(self.k_new)
+        self.out = torch.zeros_like(self.q)
+        self.scale = head_dim ** -0.5 if scale is None else scale
+        self.stream = stream or torch.cuda.Stream(device=dev)
+        block_size = caches[0][0].shape[1]
+        with torch.cuda.stream(self.stream):
+            self.plan = ops.AttentionPlan(stager.block_table, stager._cu, stager._kv, T,
+                                          num_q_heads, num_kv_heads, head_dim, block_size)
+        self.graph = None
+
+    def _body(self):
+        self.plan.replan()
+        for layer, (kc, vc) in enumerate(self.caches):
+            ops.paged_attention_gqa(self.q[layer], kc, vc, self.plan, self.scale,
+                                    out=self.out[layer], key_new=self.k_new[layer],
+                                    value_new=self.v_new[layer])
+
+    def capture(self):
+        """Capture after one staged step (the buffers hold valid metadata)."""
+        with torch.cuda.stream(self.stream):
+            self._body()                       # warm-up outside the graph
+            torch.cuda.synchronize()
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph, stream=self.stream):
+                self._body()
+        return self
+
+    def stage(self, plan, scheduled=None):
+        with torch.cuda.stream(self.stream):
+            return self.stager.stage(plan, scheduled)
+
+    def replay(self):
+        with torch.cuda.stream(self.stream):
+            self.graph.replay()

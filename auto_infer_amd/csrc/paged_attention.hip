@@ -697,18 +697,27 @@ struct MergeArgs {
   uint16_t* out;
   int64_t o_ts, o_hs;
   int32_t group, hb, dv, nw, hkv;
+  int64_t seg_cap;
 };
 
-// One work-group per (split segment, kv head); thread = (row, 8 dims),
-// looping over the dims when dv > 128.  Single pass with a running rescale,
-// unrolled so the loads of successive partials are in flight together.
+// One work-group per (split segment, kv head, 64 output dims); thread =
+// (row, 4 dims).  The segment record is loaded together with the header (the
+// work items are ordered by segment, so an item past the live segments ends
+// the loop), and the partials are merged in one pass with a running rescale:
+// their loads do not depend on one another and are all in flight together.
+constexpr int kMergeDims = 64;
+
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
-  const int nseg = a.hdr[0], tpw = a.hdr[2];
   const int n = threadIdx.x >> 4;
-  for (int sw = blockIdx.x; sw < nseg * a.nw; sw += gridDim.x) {
+  const int nch = a.dv / kMergeDims;
+  const int64_t items = (int64_t)a.seg_cap * a.nw * nch;
+  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+    const int sw = (int)(item / nch), ch = (int)(item - (int64_t)sw * nch);
     const int s = sw / a.nw, wid = sw - s * a.nw;
     const int4 r0 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8);
     const int4 r1 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8 + 4);
+    const int nseg = a.hdr[0], tpw = a.hdr[2];
+    if (s >= nseg) break;
     const int tb = r1.y, te = r1.z;
     const int np = te > tb ? (te - 1) / tpw - tb / tpw + 1 : 0;
     if (np <= 1) continue;
@@ -719,33 +728,27 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     const int head = kvh * a.group + hbi * a.hb + hh;
     const int64_t row0 = ((int64_t)r1.w * a.nw + wid) * kRows + n;
     const int64_t pstride = (int64_t)a.nw * kRows;
-    uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs;
-    for (int c = (threadIdx.x & 15) * 8; c < a.dv; c += 128) {
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      float mx = -1e30f, ls = 0.f;
-#pragma unroll 4
-      for (int k = 0; k < np; ++k) {
-        const int64_t pr = row0 + k * pstride;
-        const float2 ml = a.part_ml[pr];
-        const float4* src = reinterpret_cast<const float4*>(a.part_o + pr * a.dv + c);
-        const float4 x0 = src[0], x1 = src[1];
-        const float mn = fmaxf(mx, ml.x);
-        const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
-        ls = ls * sa + ml.y * sb;
-        acc[0] = acc[0] * sa + x0.x * sb; acc[1] = acc[1] * sa + x0.y * sb;
-        acc[2] = acc[2] * sa + x0.z * sb; acc[3] = acc[3] * sa + x0.w * sb;
-        acc[4] = acc[4] * sa + x1.x * sb; acc[5] = acc[5] * sa + x1.y * sb;
-        acc[6] = acc[6] * sa + x1.z * sb; acc[7] = acc[7] * sa + x1.w * sb;
-        mx = mn;
-      }
-      const float inv = ls > 0.f ? 1.f / ls : 0.f;
-      uint4 wv;
-      wv.x = aia::pack_bf16x2(acc[0] * inv, acc[1] * inv);
-      wv.y = aia::pack_bf16x2(acc[2] * inv, acc[3] * inv);
-      wv.z = aia::pack_bf16x2(acc[4] * inv, acc[5] * inv);
-      wv.w = aia::pack_bf16x2(acc[6] * inv, acc[7] * inv);
-      *reinterpret_cast<uint4*>(op + c) = wv;
+    const int c = ch * kMergeDims + (threadIdx.x & 15) * 4;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float mx = -1e30f, ls = 0.f;
+#pragma unroll 8
+    for (int k = 0; k < np; ++k) {
+      const int64_t pr = row0 + k * pstride;
+      const float2 ml = a.part_ml[pr];
+      const float4 x = *reinterpret_cast<const float4*>(a.part_o + pr * a.dv + c);
+      const float mn = fmaxf(mx, ml.x);
+      const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
+      ls = ls * sa + ml.y * sb;
+      acc[0] = acc[0] * sa + x.x * sb; acc[1] = acc[1] * sa + x.y * sb;
+      acc[2] = acc[2] * sa + x.z * sb; acc[3] = acc[3] * sa + x.w * sb;
+      mx = mn;
     }
+    const float inv = ls > 0.f ? 1.f / ls : 0.f;
+    uint2 wv;
+    wv.x = aia::pack_bf16x2(acc[0] * inv, acc[1] * inv);
+    wv.y = aia::pack_bf16x2(acc[2] * inv, acc[3] * inv);
+    uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs;
+    *reinterpret_cast<uint2*>(op + c) = wv;
   }
 }
 
@@ -977,8 +980,9 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
   mg.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
   mg.seg = seg; mg.part_o = part_o; mg.part_ml = part_ml;
   mg.out = out; mg.o_ts = o_ts; mg.o_hs = o_hs; mg.group = g.group; mg.hb = g.hb; mg.dv = dv;
-  mg.nw = nw; mg.hkv = g.hkv;
-  int64_t mgrid = L.seg_cap * nw < 4096 ? L.seg_cap * nw : 4096;
+  mg.nw = nw; mg.hkv = g.hkv; mg.seg_cap = L.seg_cap;
+  const int64_t items = (int64_t)L.seg_cap * nw * (dv / kMergeDims);
+  int64_t mgrid = items < 2048 ? items : 2048;
   if (mgrid < 1) mgrid = 1;
   merge_kernel<<<(unsigned)mgrid, 256, 0, s>>>(mg);
   return aia::check_hip(hipGetLastError(), "merge_kernel launch");

@@ -700,55 +700,84 @@ struct MergeArgs {
   int64_t seg_cap;
 };
 
-// One work-group per (split segment, kv head, 64 output dims); thread =
-// (row, 4 dims).  The segment record is loaded together with the header (the
-// work items are ordered by segment, so an item past the live segments ends
-// the loop), and the partials are merged in one pass with a running rescale:
-// their loads do not depend on one another and are all in flight together.
-constexpr int kMergeDims = 64;
+// Merge of split partials.  A work item is (split segment, kv head, slice of
+// 64 output elements), an element being 4 dims of one valid row (valid rows
+// are a prefix of the 16, so decode items are small).  The 4 waves of the
+// work-group take every 4th partial each, so all partial loads of a
+// segment are in flight together, and combine their running (max, sum,
+// accumulator) through LDS.  The segment record is loaded together with the
+// header; items are ordered by segment, so one past the live segments ends
+// the loop.
+constexpr int kMergeGroups = 4;
 
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
-  const int n = threadIdx.x >> 4;
-  const int nch = a.dv / kMergeDims;
-  const int64_t items = (int64_t)a.seg_cap * a.nw * nch;
+  __shared__ float4 sacc[kMergeGroups - 1][64];
+  __shared__ float2 sml[kMergeGroups - 1][64];
+  const int lane = threadIdx.x & 63, kg = threadIdx.x >> 6;
+  const int epr = a.dv / 4;                               // elements per row
+  const int nsl = (kRows * epr + 63) / 64;                // slices per (segment, head)
+  const int64_t items = (int64_t)a.seg_cap * a.nw * nsl;
   for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
-    const int sw = (int)(item / nch), ch = (int)(item - (int64_t)sw * nch);
+    const int sw = (int)(item / nsl), sl = (int)(item - (int64_t)sw * nsl);
     const int s = sw / a.nw, wid = sw - s * a.nw;
     const int4 r0 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8);
     const int4 r1 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8 + 4);
     const int nseg = a.hdr[0], tpw = a.hdr[2];
-    if (s >= nseg) break;
+    if (s >= nseg) break;                                  // uniform over the group
     const int tb = r1.y, te = r1.z;
     const int np = te > tb ? (te - 1) / tpw - tb / tpw + 1 : 0;
-    if (np <= 1) continue;
     const int kvh = (r0.y & 0xffff) * a.nw + wid, hbi = (r0.y >> 16) & 0x3fff, qtok0 = r0.z,
               nq = r0.w & 0xff;
-    if (kvh >= a.hkv || n >= nq * a.hb) continue;   // valid rows are a prefix
-    const int qi = n / a.hb, hh = n - qi * a.hb;
-    const int head = kvh * a.group + hbi * a.hb + hh;
+    const int rows = nq * a.hb;
+    if (np <= 1 || kvh >= a.hkv || sl * 64 >= rows * epr) continue;   // uniform
+    const int e = sl * 64 + lane;
+    const bool live = e < rows * epr;
+    const int n = live ? e / epr : 0, c = (e - n * epr) * 4;
     const int64_t row0 = ((int64_t)r1.w * a.nw + wid) * kRows + n;
     const int64_t pstride = (int64_t)a.nw * kRows;
-    const int c = ch * kMergeDims + (threadIdx.x & 15) * 4;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     float mx = -1e30f, ls = 0.f;
-#pragma unroll 8
-    for (int k = 0; k < np; ++k) {
-      const int64_t pr = row0 + k * pstride;
-      const float2 ml = a.part_ml[pr];
-      const float4 x = *reinterpret_cast<const float4*>(a.part_o + pr * a.dv + c);
-      const float mn = fmaxf(mx, ml.x);
-      const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
-      ls = ls * sa + ml.y * sb;
-      acc[0] = acc[0] * sa + x.x * sb; acc[1] = acc[1] * sa + x.y * sb;
-      acc[2] = acc[2] * sa + x.z * sb; acc[3] = acc[3] * sa + x.w * sb;
-      mx = mn;
+    if (live) {
+#pragma unroll 4
+      for (int k = kg; k < np; k += kMergeGroups) {
+        const int64_t pr = row0 + k * pstride;
+        const float2 ml = a.part_ml[pr];
+        const float4 x = *reinterpret_cast<const float4*>(a.part_o + pr * a.dv + c);
+        const float mn = fmaxf(mx, ml.x);
+        const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
+        ls = ls * sa + ml.y * sb;
+        acc.x = acc.x * sa + x.x * sb; acc.y = acc.y * sa + x.y * sb;
+        acc.z = acc.z * sa + x.z * sb; acc.w = acc.w * sa + x.w * sb;
+        mx = mn;
+      }
     }
-    const float inv = ls > 0.f ? 1.f / ls : 0.f;
-    uint2 wv;
-    wv.x = aia::pack_bf16x2(acc[0] * inv, acc[1] * inv);
-    wv.y = aia::pack_bf16x2(acc[2] * inv, acc[3] * inv);
-    uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs;
-    *reinterpret_cast<uint2*>(op + c) = wv;
+    if (kg > 0) {
+      sacc[kg - 1][lane] = acc;
+      sml[kg - 1][lane] = make_float2(mx, ls);
+    }
+    __syncthreads();
+    if (kg == 0 && live) {
+#pragma unroll
+      for (int j = 0; j < kMergeGroups - 1; ++j) {
+        const float2 ml = sml[j][lane];
+        const float4 x = sacc[j][lane];
+        const float mn = fmaxf(mx, ml.x);
+        const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
+        ls = ls * sa + ml.y * sb;
+        acc.x = acc.x * sa + x.x * sb; acc.y = acc.y * sa + x.y * sb;
+        acc.z = acc.z * sa + x.z * sb; acc.w = acc.w * sa + x.w * sb;
+        mx = mn;
+      }
+      const float inv = ls > 0.f ? 1.f / ls : 0.f;
+      const int qi = n / a.hb, hh = n - qi * a.hb;
+      const int head = kvh * a.group + hbi * a.hb + hh;
+      uint2 wv;
+      wv.x = aia::pack_bf16x2(acc.x * inv, acc.y * inv);
+      wv.y = aia::pack_bf16x2(acc.z * inv, acc.w * inv);
+      uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs;
+      *reinterpret_cast<uint2*>(op + c) = wv;
+    }
+    __syncthreads();
   }
 }
 
@@ -981,7 +1010,7 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
   mg.seg = seg; mg.part_o = part_o; mg.part_ml = part_ml;
   mg.out = out; mg.o_ts = o_ts; mg.o_hs = o_hs; mg.group = g.group; mg.hb = g.hb; mg.dv = dv;
   mg.nw = nw; mg.hkv = g.hkv; mg.seg_cap = L.seg_cap;
-  const int64_t items = (int64_t)L.seg_cap * nw * (dv / kMergeDims);
+  const int64_t items = (int64_t)L.seg_cap * nw * ((kRows * (dv / 4) + 63) / 64);
   int64_t mgrid = items < 2048 ? items : 2048;
   if (mgrid < 1) mgrid = 1;
   merge_kernel<<<(unsigned)mgrid, 256, 0, s>>>(mg);

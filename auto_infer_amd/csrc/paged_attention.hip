@@ -29,7 +29,9 @@ using aia::short4_t;
 constexpr int kHeadDim = 128;
 constexpr int kTile = 16;         // keys per MFMA tile
 constexpr int kRows = 16;         // query rows per segment (MFMA N)
-constexpr int kVtStride = 20;     // LDS row stride (elements) of the V^T tile
+// LDS row stride (elements) of a staged V tile: 288 bytes puts the 16 rows
+// of a transposing read in distinct banks
+constexpr int kVStride = 144;
 constexpr int kMaxBatch = 8192;   // planner keeps the request offsets in LDS
 constexpr int kDefaultWaves = 2048;
 constexpr int kMaxWaves = 16384;
@@ -365,9 +367,36 @@ __device__ __forceinline__ short4_t as_s4(uint32_t a, uint32_t b) {
   return r;
 }
 
-__device__ __forceinline__ uint16_t half_of(uint4 v, int e) {
-  const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
-  return (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffff));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4_t as_u4(uint4 v) { return u32x4_t{v.x, v.y, v.z, v.w}; }
+__device__ __forceinline__ bf16x8_t as_b8(uint4 v) { return __builtin_bit_cast(bf16x8_t, as_u4(v)); }
+
+// S^T tile (16 keys x 16 rows) += K (16 keys x 32 dims) . Q^T: lane (key n,
+// group g) holds dims [32 j + 8 g, +8) of its key in kk and of its row in q.
+__device__ __forceinline__ float4_t qk_step(uint4 kk, uint4 q, float4_t acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(kk), as_b8(q), acc, 0, 0, 0);
+}
+
+// A V tile is staged in LDS key-major (row stride kVStride elements): lane
+// (key n, group g) stores its 16-byte pieces at dims 32 j + 8 g.  The
+// transposing LDS read works within each 16-lane group: local lane l receives
+// element l % 4 of the 8 bytes addressed by local lanes 4 k + l / 4, k = 0..3.
+// Lane (n, g) addressing key 4 g + n / 4, dims 16 dt + 4 (n % 4) therefore
+// receives V^T[16 dt + n][keys 4 g .. 4 g + 3], the A fragment of the
+// 16x16x16 MFMA, in one instruction.  (The stores take vector values: an
+// aggregate copy of the tile registers keeps them in a private array, which
+// the compiler then places in LDS, serialising the load pipeline.)
+__device__ __forceinline__ void stage_v(uint16_t* vs, int n, int g, const uint4 (&vv)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(vs + n * kVStride + 32 * j + 8 * g) = as_u4(vv[j]);
+}
+__device__ __forceinline__ short4_t vt_frag(const uint16_t* vs, int n, int g, int dt) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_short4_t*)(vs + (4 * g + (n >> 2)) * kVStride + 16 * dt + 4 * (n & 3)));
 }
 
 // Tiles kept in flight per wave (registers: 32 VGPRs per tile).
@@ -462,18 +491,8 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
 #endif
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s4(kk[j].x, kk[j].y),
-                                                      as_s4(qf[j].x, qf[j].y), acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s4(kk[j].z, kk[j].w),
-                                                      as_s4(qf[j].z, qf[j].w), acc, 0, 0, 0);
-    }
-    // V tile -> LDS, transposed: vt[d][key]
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vt[(32 * j + 8 * g + e) * kVtStride + n] = half_of(vv[j], e);
-    }
+    for (int j = 0; j < 4; ++j) acc = qk_step(kk[j], qf[j], acc);
+    stage_v(vt, n, g, vv);
     const int tb = lt * kTile + 4 * g;
     float sv[4];
 #pragma unroll
@@ -493,10 +512,8 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
     const short4_t pb = as_s4(aia::pack_bf16x2(p[0], p[1]), aia::pack_bf16x2(p[2], p[3]));
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const short4_t va = *reinterpret_cast<const short4_t*>(vt + (16 * dt + n) * kVtStride + 4 * g);
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[dt], 0, 0, 0);
-    }
+    for (int dt = 0; dt < 8; ++dt)
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt_frag(vt, n, g, dt), pb, o[dt], 0, 0, 0);
     __builtin_amdgcn_wave_barrier();
   };
 
@@ -653,7 +670,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
 template <int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gqa_attn_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t vt_all[NW][kHeadDim * kVtStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_all[NW][kTile * kVStride];
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int w = blockIdx.x;
@@ -868,19 +885,12 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
 #pragma unroll
     for (int j = 0; j < 5; ++j) {
       if (j == 4 && !has_rope) break;
-      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s4(kk[j].x, kk[j].y),
-                                                      as_s4(qf[j].x, qf[j].y), acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s4(kk[j].z, kk[j].w),
-                                                      as_s4(qf[j].z, qf[j].w), acc, 0, 0, 0);
+      acc = qk_step(kk[j], qf[j], acc);
     }
     float* xb = sx + parity * (4 * 256);
     *reinterpret_cast<float4_t*>(xb + wid * 256 + lane * 4) = acc;
-    // V^T slice of this wave: vt[d][key], d local to [0, 128)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vt[(32 * j + 8 * g + e) * kVtStride + n] = half_of(kk[j], e);
-    }
+    // this wave's V slice (latent dims [128 w, +128)) is the K it holds
+    stage_v(vt, n, g, reinterpret_cast<const uint4 (&)[4]>(kk));
     __syncthreads();
     float4_t tot = *reinterpret_cast<const float4_t*>(xb + lane * 4);
 #pragma unroll
@@ -904,10 +914,8 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
     for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
     const short4_t pb = as_s4(aia::pack_bf16x2(p[0], p[1]), aia::pack_bf16x2(p[2], p[3]));
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const short4_t va = *reinterpret_cast<const short4_t*>(vt + (16 * dt + n) * kVtStride + 4 * g);
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[dt], 0, 0, 0);
-    }
+    for (int dt = 0; dt < 8; ++dt)
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt_frag(vt, n, g, dt), pb, o[dt], 0, 0, 0);
     __builtin_amdgcn_wave_barrier();
   };
 
@@ -966,7 +974,7 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
 }
 
 __global__ __launch_bounds__(256) void mla_attn_kernel(MlaArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t vt_all[4][kHeadDim * kVtStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_all[4][kTile * kVStride];
   __shared__ __attribute__((aligned(16))) float sx[2 * 4 * 256];
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

@@ -37,9 +37,9 @@ constexpr int kDefaultWaves = 2048;
 constexpr int kMaxWaves = 16384;
 constexpr int kPlanThreads = 1024;
 // Per-range work record: {segment, first tile, end tile, tiles per range,
-// the segment's 8-int record, first logical block, 3 pad, the first 16
-// block ids of the range} -- everything a work-group needs to issue its
-// first K/V loads after one load.
+// the segment's 8-int record, first logical block, last segment of the
+// range, 2 pad, the first 16 block ids of the range} -- everything a
+// work-group needs to issue its first K/V loads after one load.
 constexpr int kRecInts = 32;
 constexpr int kRecBlocks = 16;
 
@@ -141,6 +141,7 @@ __device__ int block_exclusive_scan(int v, int* wave_sums, int* total) {
 // dependent lookup.
 constexpr int kPlanLds = 12288;          // ints of LDS scratch (48 KB)
 constexpr int kPlanRegChunks = 8;        // segments kept in registers: 8 x 1024
+constexpr int kPadBelow = 16;            // pad segments when ranges are shorter (tiles)
 
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ kvlen,
@@ -228,8 +229,69 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       if (i == c) { my_tb[i] = carry + ex; my_nt[i] = ntiles; }
     carry += tot;
   }
-  const int total_tiles = carry;
-  const int tpw = max(1, (total_tiles + waves - 1) / waves);
+  // Range length.  With few segments and short ranges each segment's tile
+  // span is padded to a multiple of it, so no range crosses a segment
+  // boundary (a crossing costs the range's work-group further dependent
+  // loads, and the slowest range sets the kernel time); waves - nseg ranges'
+  // worth of tiles plus at most one partial range per segment still fit in
+  // `waves` ranges.  Long ranges absorb a crossing and keep the even split.
+  const int real_tiles = carry;
+  int tpw = max(1, (real_tiles + waves - 1) / waves);
+  const bool pad = 2 * nseg <= waves && tpw < kPadBelow;
+  if (pad) {
+    // smallest length whose padded ranges fit in `waves`: the bound
+    // ceil(tiles / (waves - nseg)) always fits, and a few block reductions
+    // find the least one (an idle range slot is an idle work-group)
+    int hi = max(1, (real_tiles + waves - nseg - 1) / (waves - nseg));
+    while (tpw < hi) {
+      const int mid = (tpw + hi) >> 1;
+      int mine = 0;
+      for (int base = 0, c = 0; base < nseg; base += kPlanThreads, ++c) {
+        const int s = base + tid;
+        if (s >= nseg) break;
+        int nt = 0;
+        if (regs) {
+#pragma unroll
+          for (int i = 0; i < kPlanRegChunks; ++i)
+            if (i == c) nt = my_nt[i];
+        } else {
+          nt = seg[(int64_t)s * 8 + 6] - seg[(int64_t)s * 8 + 5];
+        }
+        mine += (nt + mid - 1) / mid;
+      }
+      int tot;
+      block_exclusive_scan(mine, wave_sums, &tot);
+      if (tot <= waves) hi = mid; else tpw = mid + 1;
+    }
+  }
+  int total_tiles = real_tiles;
+  if (pad) {
+    carry = 0;
+    for (int base = 0, c = 0; base < nseg; base += kPlanThreads, ++c) {
+      const int s = base + tid;
+      int nt = 0;
+      if (s < nseg) {
+        if (regs) {
+#pragma unroll
+          for (int i = 0; i < kPlanRegChunks; ++i)
+            if (i == c) nt = my_nt[i];
+        } else {
+          nt = seg[(int64_t)s * 8 + 6] - seg[(int64_t)s * 8 + 5];
+        }
+      }
+      int tot;
+      const int ex = block_exclusive_scan((nt + tpw - 1) / tpw * tpw, wave_sums, &tot);
+      if (s < nseg) {
+        seg[(int64_t)s * 8 + 5] = carry + ex;
+        seg[(int64_t)s * 8 + 6] = carry + ex + nt;
+      }
+#pragma unroll
+      for (int i = 0; i < kPlanRegChunks; ++i)
+        if (i == c) my_tb[i] = carry + ex;
+      carry += tot;
+    }
+    total_tiles = carry;
+  }
   __syncthreads();   // request metadata in LDS is no longer needed
 
   // segments' first tiles into LDS for the per-range search
@@ -285,13 +347,20 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       out[0] = -1; out[1] = 0; out[2] = 0; out[3] = tpw;
       continue;
     }
+    const int t1 = min(total_tiles, t0 + tpw);
     int lo = 0, hi = nseg - 1;  // last s with tile_begin <= t0
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       const int tb = tb_lds ? lds[mid] : seg[(int64_t)mid * 8 + 5];
       if (tb <= t0) lo = mid; else hi = mid - 1;
     }
-    out[0] = lo; out[1] = t0; out[2] = min(total_tiles, t0 + tpw); out[3] = tpw;
+    int lo2 = lo, hi2 = nseg - 1;  // last s with tile_begin < t1
+    while (lo2 < hi2) {
+      const int mid = (lo2 + hi2 + 1) >> 1;
+      const int tb = tb_lds ? lds[mid] : seg[(int64_t)mid * 8 + 5];
+      if (tb < t1) lo2 = mid; else hi2 = mid - 1;
+    }
+    out[0] = lo; out[1] = t0; out[2] = t1; out[3] = tpw;
     const int* r = seg + (int64_t)lo * 8;
     int rr[8];
 #pragma unroll
@@ -302,7 +371,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int visible = max(0, lim_base + nq);
     const int nblk_vis = (visible + block_size - 1) / block_size;
     const int blk_base = ((t0 - rr[5]) * kTile) / block_size;
-    out[12] = blk_base; out[13] = 0; out[14] = 0; out[15] = 0;
+    out[12] = blk_base; out[13] = lo2; out[14] = 0; out[15] = 0;
     const int32_t* btrow = block_table + (int64_t)b * bt_stride;
     int bv[kRecBlocks];
 #pragma unroll
@@ -399,9 +468,12 @@ __device__ __forceinline__ short4_t vt_frag(const uint16_t* vs, int n, int g, in
       (lds_short4_t*)(vs + (4 * g + (n >> 2)) * kVStride + 16 * dt + 4 * (n & 3)));
 }
 
-// Tiles kept in flight per wave (registers: 32 VGPRs per tile).
+// Tiles kept in flight per GQA wave (registers: 32 VGPRs per tile).  One is
+// fastest: with random blocks, more outstanding tiles per CU lowers the
+// delivered bandwidth (measured on config-1 decode: 18.7 us at 1, 20.1 at 2,
+// 24.9 at 5), and the planner keeps ranges short instead.
 #ifndef AIA_PIPE
-#define AIA_PIPE 2
+#define AIA_PIPE 1
 #endif
 constexpr int kPipe = AIA_PIPE;
 
@@ -448,9 +520,10 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   // Block ids are held one per lane for a window of 64 logical blocks; the
   // window is (re)loaded only between pipelined runs, so the per-tile address
   // shuffle never waits on an outstanding global load.
-  // Loads are issued unconditionally (tiles past the window read the first
-  // key row again, an L1 hit) so the load stream is straight-line and the
-  // compiler can wait for each tile with an exact count.
+  // Loads are issued unconditionally (tiles past the window read the
+  // window's first key row, K and V, again: an L1 hit, and a different row
+  // for every range, so no memory channel is hammered) so the load stream is
+  // straight-line and the compiler can wait for each tile with an exact count.
   auto load = [&](int lt, uint4 (&kk)[4], uint4 (&vv)[4], int64_t& wdst) {
     const bool live = lt < w1;
     const int tok = live ? min(lt * kTile + n, visible - 1) : blk_base * a.bs;
@@ -464,7 +537,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
     const uint4* kp = reinterpret_cast<const uint4*>(
         fresh ? a.kn + nrow * a.kn_ts + (int64_t)kvh * kHeadDim : a.kc + base);
     const uint4* vp = reinterpret_cast<const uint4*>(
-        fresh ? a.vn + nrow * a.vn_ts + (int64_t)kvh * kHeadDim : a.vc + (live ? base : (int64_t)0));
+        fresh ? a.vn + nrow * a.vn_ts + (int64_t)kvh * kHeadDim : a.vc + base);
     // cache slot this lane writes after the tile arrives (-1: nothing)
     wdst = (writer && fresh && lt * kTile + n < visible) ? base : (int64_t)-1;
 #pragma unroll
@@ -668,7 +741,10 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
 
 // One work-group per key range, one wave per kv head of the segment's group.
 template <int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+#ifndef AIA_GQA_WAVES_PER_EU
+#define AIA_GQA_WAVES_PER_EU 2
+#endif
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(AIA_GQA_WAVES_PER_EU, AIA_GQA_WAVES_PER_EU)))
 void gqa_attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vt_all[NW][kTile * kVStride];
   const int lane = threadIdx.x & 63;
@@ -681,8 +757,10 @@ void gqa_attn_kernel(AttnArgs a) {
   const int ngroups = (a.hkv + NW - 1) / NW, nhb = (a.group + a.hb - 1) / a.hb;
   int s = wr[0];
   int t = wr[1];
-  const int t_end = wr[2], tpw = wr[3];
-  if (s < 0 || s >= nseg || t < 0 || t >= t_end || t_end > total_tiles || tpw < 1) return;
+  const int t_end = wr[2], tpw = wr[3], s_last = wr[13];
+  if (s < 0 || s >= nseg || t < 0 || t >= t_end || t_end > total_tiles || tpw < 1 ||
+      s_last < s || s_last >= nseg)
+    return;
   int rec[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) rec[i] = wr[4 + i];
@@ -699,7 +777,7 @@ void gqa_attn_kernel(AttnArgs a) {
       t = chunk_end;
       if (t >= t_end) break;
     }
-    if (++s >= nseg) return;
+    if (++s > s_last) return;
     const int* r = a.seg + (int64_t)s * 8;
 #pragma unroll
     for (int i = 0; i < 8; ++i) rec[i] = r[i];
@@ -808,6 +886,13 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
 // runs the same softmax, and wave w accumulates output dims
 // [128w, 128w + 128) from the K registers it already holds (V = K).
 constexpr int kMlaK = 576, kMlaV = 512;
+// MLA tiles kept in flight per wave (registers: 20 VGPRs per tile).  Its
+// ranges are long and its work-groups small, so it keeps a deeper pipeline
+// than the GQA kernel.
+#ifndef AIA_MLA_PIPE
+#define AIA_MLA_PIPE 2
+#endif
+constexpr int kMlaPipe = AIA_MLA_PIPE;
 
 struct MlaArgs {
   const uint16_t* q;
@@ -919,7 +1004,7 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
     __builtin_amdgcn_wave_barrier();
   };
 
-  uint4 kbuf[kPipe][5];
+  uint4 kbuf[kMlaPipe][5];
   for (int w0 = lt0; w0 < lt1;) {
     blk_base = (w0 * kTile) / a.bs;
     const int win = use_pre ? kRecBlocks : 64;
@@ -928,16 +1013,16 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
     else btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
     use_pre = false;
 #pragma unroll
-    for (int i = 0; i < kPipe; ++i) {
+    for (int i = 0; i < kMlaPipe; ++i) {
       load(w0 + i, kbuf[i]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    for (int base = w0; base < w1; base += kPipe) {
+    for (int base = w0; base < w1; base += kMlaPipe) {
 #pragma unroll
-      for (int i = 0; i < kPipe; ++i) {
+      for (int i = 0; i < kMlaPipe; ++i) {
         const int lt = base + i;
         if (lt < w1) compute(lt, kbuf[i]);
-        load(lt + kPipe, kbuf[i]);
+        load(lt + kMlaPipe, kbuf[i]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -986,8 +1071,10 @@ __global__ __launch_bounds__(256) void mla_attn_kernel(MlaArgs a) {
   const int nhb = (a.group + a.hb - 1) / a.hb;
   int s = wr[0];
   int t = wr[1];
-  const int t_end = wr[2], tpw = wr[3];
-  if (s < 0 || s >= nseg || t < 0 || t >= t_end || t_end > total_tiles || tpw < 1) return;
+  const int t_end = wr[2], tpw = wr[3], s_last = wr[13];
+  if (s < 0 || s >= nseg || t < 0 || t >= t_end || t_end > total_tiles || tpw < 1 ||
+      s_last < s || s_last >= nseg)
+    return;
   int rec[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) rec[i] = wr[4 + i];
@@ -1002,7 +1089,7 @@ __global__ __launch_bounds__(256) void mla_attn_kernel(MlaArgs a) {
       t = chunk_end;
       if (t >= t_end) break;
     }
-    if (++s >= nseg) return;
+    if (++s > s_last) return;
     const int* r = a.seg + (int64_t)s * 8;
 #pragma unroll
     for (int i = 0; i < 8; ++i) rec[i] = r[i];

@@ -90,10 +90,11 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
 }
 
 // Number of key ranges (= work-groups).  Default: about kDefaultWaves waves
-// in flight for GQA (one per kv head of a group), 512 four-wave groups for
-// the 576-wide MLA latent.
+// in flight for GQA (one per kv head of a group), 768 four-wave groups (three
+// per CU) for the 576-wide MLA latent.
+constexpr int kDefaultMlaRanges = 768;
 int32_t resolve_waves(int32_t w, const Geometry& g, int32_t dv) {
-  if (w <= 0) w = dv == 512 ? 512 : (kDefaultWaves + g.nw - 1) / g.nw;
+  if (w <= 0) w = dv == 512 ? kDefaultMlaRanges : (kDefaultWaves + g.nw - 1) / g.nw;
   if (w > kMaxWaves) w = kMaxWaves;
   return w;
 }
@@ -890,7 +891,7 @@ constexpr int kMlaK = 576, kMlaV = 512;
 // ranges are long and its work-groups small, so it keeps a deeper pipeline
 // than the GQA kernel.
 #ifndef AIA_MLA_PIPE
-#define AIA_MLA_PIPE 2
+#define AIA_MLA_PIPE 3
 #endif
 constexpr int kMlaPipe = AIA_MLA_PIPE;
 
@@ -1058,7 +1059,13 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
   }
 }
 
-__global__ __launch_bounds__(256) void mla_attn_kernel(MlaArgs a) {
+// Three work-groups per CU (the register budget of 3 waves per SIMD fits a
+// 3-deep pipeline without spills); the default 768 ranges fill the chip once.
+#ifndef AIA_MLA_WAVES_PER_EU
+#define AIA_MLA_WAVES_PER_EU 3
+#endif
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AIA_MLA_WAVES_PER_EU)))
+void mla_attn_kernel(MlaArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vt_all[4][kTile * kVStride];
   __shared__ __attribute__((aligned(16))) float sx[2 * 4 * 256];
   const int lane = threadIdx.x & 63;

@@ -50,10 +50,14 @@ constexpr int kMaxGroupWaves = 8;  // kv heads (waves) per work-group
 // the group over the same keys, so every tile reads whole contiguous
 // (block_size x Hkv x D) cache slots.
 struct Geometry {
-  int32_t hkv, group, hb, nhb, qb, nw, nkvg;
+  int32_t hkv, group, hb, nhb, qb, nw, nkvg, rb, qs;
 };
 
-Geometry geometry(int32_t hq, int32_t hkv) {
+// rb: row blocks (of 16 query rows) per segment.  Two when a GQA launch has
+// multi-token requests (prefill, verify), so each K/V tile feeds 32 rows;
+// one for decode-only launches and MLA.  Planner and kernels derive it from
+// the same (batch, tokens, head_dim_v), so they always agree.
+Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_t dv) {
   Geometry g;
   g.hkv = hkv;
   g.group = hq / hkv;
@@ -62,6 +66,8 @@ Geometry geometry(int32_t hq, int32_t hkv) {
   g.qb = kRows / g.hb;                                  // query tokens per segment
   g.nw = hkv < kMaxGroupWaves ? hkv : kMaxGroupWaves;   // waves per work-group
   g.nkvg = (hkv + g.nw - 1) / g.nw;                     // kv-head groups
+  g.rb = (dv == kHeadDim && tokens > batch) ? 2 : 1;
+  g.qs = g.qb * g.rb;                                   // query tokens per segment
   return g;
 }
 
@@ -75,14 +81,14 @@ int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int32_t waves) {
   Layout L;
-  L.seg_cap = (int64_t)g.nkvg * g.nhb * (batch + (tokens + g.qb - 1) / g.qb);
+  L.seg_cap = (int64_t)g.nkvg * g.nhb * (batch + (tokens + g.qs - 1) / g.qs);
   L.part_cap = L.seg_cap + waves;
   int64_t off = 0;
   L.hdr = off;      off = align256(off + 64 * 4);
   L.seg = off;      off = align256(off + (L.seg_cap + 1) * 8 * 4);
   L.wave = off;     off = align256(off + (int64_t)waves * kRecInts * 4);
-  L.part_ml = off;  off = align256(off + L.part_cap * g.nw * kRows * 8);
-  L.part_o = off;   off = align256(off + L.part_cap * g.nw * kRows * (int64_t)dv * 4);
+  L.part_ml = off;  off = align256(off + L.part_cap * g.nw * kRows * g.rb * 8);
+  L.part_o = off;   off = align256(off + L.part_cap * g.nw * kRows * g.rb * (int64_t)dv * 4);
   L.cnt = off;      off = align256(off + L.seg_cap * g.nw * 4);
   L.req = off;      off = align256(off + ((int64_t)batch + 1) * 4);
   L.total = off;
@@ -172,7 +178,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
         if (b == batch - 1) cuv[batch] = c1;
       }
       const int lq = c1 - c0;
-      cnt = lq > 0 ? ((lq + g.qb - 1) / g.qb) * per_req : 0;
+      cnt = lq > 0 ? ((lq + g.qs - 1) / g.qs) * per_req : 0;
     }
     int tot;
     const int ex = block_exclusive_scan(cnt, wave_sums, &tot);
@@ -207,8 +213,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       const int q_begin = cu_r[b];
       const int lq = cu_r[b + 1] - q_begin;
       const int lk = kv_r[b];
-      const int q0 = qblk * g.qb;
-      const int nq = min(g.qb, lq - q0);
+      const int q0 = qblk * g.qs;
+      const int nq = min(g.qs, lq - q0);
       const int lim_base = lk - lq + q0;
       const int visible = max(0, min(lk, lim_base + nq));
       // at least one (fully masked) tile, so the work-group that owns it
@@ -479,6 +485,12 @@ __device__ __forceinline__ short4_t vt_frag(const uint16_t* vs, int n, int g, in
 constexpr int kPipe = AIA_PIPE;
 
 // Processes key tiles [lt0, lt1) of one segment; rec = the segment record.
+// A segment holds RB blocks of 16 query rows: block r has the segment's
+// query tokens [r qb, r qb + qb), row n being token n / hb, head n % hb
+// (qb = 16 / hb).  Every K/V tile is loaded once and used by all blocks, so a
+// prefill chunk reads its keys 1/RB as often; blocks past the segment's last
+// token are skipped (a uniform branch), so a decode segment costs one block.
+template <int RB>
 __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, int s, int lt0,
                                             int lt1, int w, int tpw, uint16_t* vt, int lane,
                                             int wid, bool use_pre, int pre) {
@@ -486,11 +498,25 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   const int b = rec[0], kvh = (rec[1] & 0xffff) * a.nw + wid, hbi = (rec[1] >> 16) & 0x3fff;
   const int qtok0 = rec[2], nq = rec[3] & 0xff, q0 = rec[3] >> 8, lim_base = rec[4];
   const int tile_begin = rec[5], tile_end = rec[6], part_base = rec[7];
-  const int qi = n / a.hb, hh = n - qi * a.hb;
-  const bool rv = qi < nq && hbi * a.hb + hh < a.group;
+  const int qb = kRows / a.hb;
+  const int nt = n / a.hb, hh = n - nt * a.hb;
+  const int nblk = (nq + qb - 1) / qb;               // row blocks holding tokens
   const int head = kvh * a.group + hbi * a.hb + hh;
-  const int lim = rv ? lim_base + qi : -1;
+  int qi[RB], lim[RB];
+  bool rv[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    qi[r] = r * qb + nt;
+    rv[r] = nt < qb && qi[r] < nq && hbi * a.hb + hh < a.group;
+    lim[r] = rv[r] ? lim_base + qi[r] : -1;
+  }
   const int visible = max(0, lim_base + nq);
+  // smallest key limit of the valid rows (wave-uniform)
+  int lim_lo = 0x7fffffff;
+#pragma unroll
+  for (int r = 0; r < RB; ++r) lim_lo = rv[r] ? min(lim_lo, lim[r]) : lim_lo;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) lim_lo = min(lim_lo, __shfl_xor(lim_lo, d));
   const int row_elems = a.hkv * kHeadDim;
   // this step's new keys sit at positions [new_start, Lk); the request's last
   // query block (head block 0) owns writing them into the cache
@@ -502,21 +528,29 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   const int nblk_vis = (visible + a.bs - 1) / a.bs;
   int blk_base = 0, btv = 0, w1 = 0;
 
-  uint4 qf[4];
-  if (rv) {
-    const uint4* qp = reinterpret_cast<const uint4*>(
-        a.q + (int64_t)(qtok0 + qi) * a.q_ts + (int64_t)head * a.q_hs);
+  uint4 qf[RB][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qf[j] = qp[4 * j + g];
-  } else {
+  for (int r = 0; r < RB; ++r) {
+    if (rv[r]) {
+      const uint4* qp = reinterpret_cast<const uint4*>(
+          a.q + (int64_t)(qtok0 + qi[r]) * a.q_ts + (int64_t)head * a.q_hs);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qf[j] = make_uint4(0, 0, 0, 0);
+      for (int j = 0; j < 4; ++j) qf[r][j] = qp[4 * j + g];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qf[r][j] = make_uint4(0, 0, 0, 0);
+    }
   }
 
-  float4_t o[8];
+  float4_t o[RB][8];
+  float m[RB], lsum[RB];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m = -1e30f, lsum = 0.f;
+  for (int r = 0; r < RB; ++r) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[r][dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    m[r] = -1e30f;
+    lsum[r] = 0.f;
+  }
 
   // Block ids are held one per lane for a window of 64 logical blocks; the
   // window is (re)loaded only between pipelined runs, so the per-tile address
@@ -559,35 +593,60 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
       uint32_t x = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) x ^= kk[j].x ^ kk[j].y ^ kk[j].z ^ kk[j].w ^ vv[j].x ^ vv[j].y ^ vv[j].z ^ vv[j].w;
-      o[0][0] += __uint_as_float(x & 0x3fffffu);
+      o[0][0][0] += __uint_as_float(x & 0x3fffffu);
       return;
     }
 #endif
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    float4_t acc[RB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc = qk_step(kk[j], qf[j], acc);
+    for (int r = 0; r < RB; ++r) {
+      acc[r] = float4_t{0.f, 0.f, 0.f, 0.f};
+      if (r == 0 || r < nblk) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[r] = qk_step(kk[j], qf[r][j], acc[r]);
+      }
+    }
     stage_v(vt, n, g, vv);
     const int tb = lt * kTile + 4 * g;
-    float sv[4];
+    // keys past a valid row's limit exist only in tiles that reach past the
+    // smallest limit (causal diagonal, sequence end); rows that are not valid
+    // are never written, so their scores need no mask
+    const bool masked = lt * kTile + kTile - 1 > lim_lo;
+    short4_t pb[RB];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) sv[v] = (tb + v <= lim) ? acc[v] * a.scale_log2 : -INFINITY;
-    float tmax = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float mnew = fmaxf(m, tmax);
-    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-    float p[4];
+    for (int r = 0; r < RB; ++r) {
+      // raw scores; scale (> 0) is applied inside the exponent
+      float sv[4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) p[v] = __builtin_amdgcn_exp2f(sv[v] - mnew);
-    lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    m = mnew;
+      for (int v = 0; v < 4; ++v) sv[v] = (!masked || tb + v <= lim[r]) ? acc[r][v] : -INFINITY;
+      float tmax = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const float mnew = fmaxf(m[r], tmax * a.scale_log2);
+      float p[4];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
-    const short4_t pb = as_s4(aia::pack_bf16x2(p[0], p[1]), aia::pack_bf16x2(p[2], p[3]));
+      for (int v = 0; v < 4; ++v) p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[v], a.scale_log2, -mnew));
+      const float psum = (p[0] + p[1]) + (p[2] + p[3]);
+      if (__any(mnew > m[r])) {   // rescale only when some row's max grew
+        const float alpha = __builtin_amdgcn_exp2f(m[r] - mnew);
+        lsum[r] = lsum[r] * alpha + psum;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[r][dt] *= alpha;
+      } else {
+        lsum[r] += psum;
+      }
+      m[r] = mnew;
+      pb[r] = as_s4(aia::pack_bf16x2(p[0], p[1]), aia::pack_bf16x2(p[2], p[3]));
+    }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt_frag(vt, n, g, dt), pb, o[dt], 0, 0, 0);
+    for (int dt = 0; dt < 8; ++dt) {
+      const short4_t va = vt_frag(vt, n, g, dt);
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+        if (r == 0 || r < nblk)
+          o[r][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb[r], o[r][dt], 0, 0, 0);
+    }
     __builtin_amdgcn_wave_barrier();
   };
 
@@ -619,19 +678,25 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
     w0 = w1;
   }
 
-  lsum += __shfl_xor(lsum, 16);
-  lsum += __shfl_xor(lsum, 32);
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    lsum[r] += __shfl_xor(lsum[r], 16);
+    lsum[r] += __shfl_xor(lsum[r], 32);
+  }
   const int first_wave = tile_begin / tpw;
   const int nparts = (tile_end - 1) / tpw - first_wave + 1;
+  constexpr int seg_rows = RB * kRows;
   if (nparts == 1) {
-    if (rv) {
-      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-      uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      if (!rv[r]) continue;
+      const float inv = lsum[r] > 0.f ? 1.f / lsum[r] : 0.f;
+      uint16_t* op = a.out + (int64_t)(qtok0 + qi[r]) * a.o_ts + (int64_t)head * a.o_hs;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         uint2 wv;
-        wv.x = aia::pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
-        wv.y = aia::pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
+        wv.x = aia::pack_bf16x2(o[r][dt][0] * inv, o[r][dt][1] * inv);
+        wv.y = aia::pack_bf16x2(o[r][dt][2] * inv, o[r][dt][3] * inv);
         *reinterpret_cast<uint2*>(op + 16 * dt + 4 * g) = wv;
       }
     }
@@ -644,19 +709,21 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
       // sees the last count reads the partials back with agent-coherent
       // loads, merges, and resets the counter for the next call on this
       // plan.  No L2 write-back / invalidate is needed.
-      if (rv) {
-        const int64_t prow = ((int64_t)part * a.nw + wid) * kRows + n;
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        if (!rv[r]) continue;
+        const int64_t prow = ((int64_t)part * a.nw + wid) * seg_rows + r * kRows + n;
         uint64_t* pp = reinterpret_cast<uint64_t*>(a.part_o + prow * kHeadDim);
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
           const int e = (16 * dt + 4 * g) / 2;
-          __hip_atomic_store(pp + e, pack_f2(o[dt][0], o[dt][1]), __ATOMIC_RELAXED,
+          __hip_atomic_store(pp + e, pack_f2(o[r][dt][0], o[r][dt][1]), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(pp + e + 1, pack_f2(o[dt][2], o[dt][3]), __ATOMIC_RELAXED,
+          __hip_atomic_store(pp + e + 1, pack_f2(o[r][dt][2], o[r][dt][3]), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
         }
         if (g == 0)
-          __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_ml + prow), pack_f2(m, lsum),
+          __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_ml + prow), pack_f2(m[r], lsum[r]),
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -671,12 +738,14 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
         // Merge, one row at a time: lane k holds part k's (m, l) (all parts
         // requested at once), then every lane accumulates two output dims
         // over the parts with all partial loads of a batch in flight.
-        const int rows = nq * a.hb;                 // valid rows are a prefix
-        for (int nr = 0; nr < rows; ++nr) {
-          const int qi2 = nr / a.hb, hh2 = nr - qi2 * a.hb;
+        for (int nr = 0; nr < nblk * kRows; ++nr) {
+          const int r2 = nr / kRows, n2 = nr - r2 * kRows;
+          const int t2 = n2 / a.hb, hh2 = n2 - t2 * a.hb;
+          const int qi2 = r2 * qb + t2;
+          if (t2 >= qb || qi2 >= nq) continue;
           const int head2 = kvh * a.group + hbi * a.hb + hh2;
-          const int64_t row0 = ((int64_t)part_base * a.nw + wid) * kRows + nr;
-          const int64_t pstride = (int64_t)a.nw * kRows;   // rows between parts
+          const int64_t row0 = ((int64_t)part_base * a.nw + wid) * seg_rows + nr;
+          const int64_t pstride = (int64_t)a.nw * seg_rows;   // rows between parts
           float mx = -1e30f;
           for (int k0 = 0; k0 < nparts; k0 += 64) {
             const int k = k0 + lane;
@@ -729,19 +798,35 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
         }
         if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-    } else if (rv) {
-      const int64_t prow = ((int64_t)part * a.nw + wid) * kRows + n;
-      float* pp = a.part_o + prow * kHeadDim;
+    } else {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-        *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * g) = o[dt];
-      if (g == 0) a.part_ml[prow] = make_float2(m, lsum);
+      for (int r = 0; r < RB; ++r) {
+        if (!rv[r]) continue;
+        const int64_t prow = ((int64_t)part * a.nw + wid) * seg_rows + r * kRows + n;
+        float* pp = a.part_o + prow * kHeadDim;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+          *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * g) = o[r][dt];
+        if (g == 0) a.part_ml[prow] = make_float2(m[r], lsum[r]);
+      }
     }
   }
 }
 
+// XCD-aware range order.  The hardware deals work-groups to the 8 XCDs
+// round-robin by id; mapping work-group b to range x q + min(x, r) + b / 8
+// (x = b % 8, n = 8 q + r) gives each XCD a contiguous run of ranges, so
+// the requests it serves -- and the keys their query blocks re-read -- stay
+// in its own L2.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_range(int b, int n) {
+  const int q = n / kXcds, r = n - q * kXcds;
+  const int x = b % kXcds, i = b / kXcds;
+  return x * q + min(x, r) + i;
+}
+
 // One work-group per key range, one wave per kv head of the segment's group.
-template <int NW>
+template <int NW, int RB>
 #ifndef AIA_GQA_WAVES_PER_EU
 #define AIA_GQA_WAVES_PER_EU 2
 #endif
@@ -750,8 +835,8 @@ void gqa_attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vt_all[NW][kTile * kVStride];
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int w = blockIdx.x;
-  if (w >= a.waves) return;
+  if ((int)blockIdx.x >= a.waves) return;
+  const int w = xcd_range(blockIdx.x, gridDim.x);
   const int* wr = a.wave_rec + (int64_t)w * kRecInts;
   const int pre = wr[16 + (lane & (kRecBlocks - 1))];   // issued with the header
   const int nseg = a.hdr[0], total_tiles = a.hdr[1];
@@ -772,8 +857,8 @@ void gqa_attn_kernel(AttnArgs a) {
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
       if ((rec[1] & 0xffff) * NW + wid < a.hkv)
-        gqa_segment(a, rec, s, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane, wid, first,
-                    pre);
+        gqa_segment<RB>(a, rec, s, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane, wid, first,
+                        pre);
       first = false;
       t = chunk_end;
       if (t >= t_end) break;
@@ -792,26 +877,31 @@ struct MergeArgs {
   const float2* part_ml;
   uint16_t* out;
   int64_t o_ts, o_hs;
-  int32_t group, hb, dv, nw, hkv;
+  int32_t group, hb, dv, nw, hkv, rb;
   int64_t seg_cap;
 };
 
 // Merge of split partials.  A work item is (split segment, kv head, slice of
-// 64 output elements), an element being 4 dims of one valid row (valid rows
-// are a prefix of the 16, so decode items are small).  The 4 waves of the
+// 64 output elements), an element being 16 dims of one row of the segment's
+// row span (rows up to its last valid one, so decode items are small; rows
+// of a block past its qb tokens are skipped).  The 4 waves of the
 // work-group take every 4th partial each, so all partial loads of a
 // segment are in flight together, and combine their running (max, sum,
 // accumulator) through LDS.  The segment record is loaded together with the
 // header; items are ordered by segment, so one past the live segments ends
-// the loop.
+// the loop.  An item is a chain of dependent loads, so elements are wide:
+// fewer items, fewer chains per work-group.
 constexpr int kMergeGroups = 4;
+constexpr int kMergeDims = 16;   // dims per element
 
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
-  __shared__ float4 sacc[kMergeGroups - 1][64];
+  __shared__ float4 sacc[kMergeGroups - 1][kMergeDims / 4][64];
   __shared__ float2 sml[kMergeGroups - 1][64];
   const int lane = threadIdx.x & 63, kg = threadIdx.x >> 6;
-  const int epr = a.dv / 4;                               // elements per row
-  const int nsl = (kRows * epr + 63) / 64;                // slices per (segment, head)
+  const int epr = a.dv / kMergeDims;                      // elements per row
+  const int seg_rows = kRows * a.rb;
+  const int nsl = (seg_rows * epr + 63) / 64;             // slices per (segment, head)
+  const int qb = kRows / a.hb;
   const int64_t items = (int64_t)a.seg_cap * a.nw * nsl;
   for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
     const int sw = (int)(item / nsl), sl = (int)(item - (int64_t)sw * nsl);
@@ -824,54 +914,70 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     const int np = te > tb ? (te - 1) / tpw - tb / tpw + 1 : 0;
     const int kvh = (r0.y & 0xffff) * a.nw + wid, hbi = (r0.y >> 16) & 0x3fff, qtok0 = r0.z,
               nq = r0.w & 0xff;
-    const int rows = nq * a.hb;
+    const int nblk = (nq + qb - 1) / qb;
+    const int rows = (nblk - 1) * kRows + min(kRows, (nq - (nblk - 1) * qb) * a.hb);
     if (np <= 1 || kvh >= a.hkv || sl * 64 >= rows * epr) continue;   // uniform
     const int e = sl * 64 + lane;
-    const bool live = e < rows * epr;
-    const int n = live ? e / epr : 0, c = (e - n * epr) * 4;
-    const int64_t row0 = ((int64_t)r1.w * a.nw + wid) * kRows + n;
-    const int64_t pstride = (int64_t)a.nw * kRows;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    int n = e / epr;
+    const int c = (e - n * epr) * kMergeDims;
+    const int rblk = n / kRows, t = (n - rblk * kRows) / a.hb;
+    const bool live = e < rows * epr && t < qb && rblk * qb + t < nq;
+    if (!live) n = 0;
+    const int64_t row0 = ((int64_t)r1.w * a.nw + wid) * seg_rows + n;
+    const int64_t pstride = (int64_t)a.nw * seg_rows;
+    float4 acc[kMergeDims / 4];
+#pragma unroll
+    for (int i = 0; i < kMergeDims / 4; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     float mx = -1e30f, ls = 0.f;
+    auto fold = [&](float2 ml, const float4 (&x)[kMergeDims / 4]) {
+      const float mn = fmaxf(mx, ml.x);
+      const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
+      ls = ls * sa + ml.y * sb;
+#pragma unroll
+      for (int i = 0; i < kMergeDims / 4; ++i) {
+        acc[i].x = acc[i].x * sa + x[i].x * sb; acc[i].y = acc[i].y * sa + x[i].y * sb;
+        acc[i].z = acc[i].z * sa + x[i].z * sb; acc[i].w = acc[i].w * sa + x[i].w * sb;
+      }
+      mx = mn;
+    };
     if (live) {
-#pragma unroll 4
+#pragma unroll 2
       for (int k = kg; k < np; k += kMergeGroups) {
         const int64_t pr = row0 + k * pstride;
         const float2 ml = a.part_ml[pr];
-        const float4 x = *reinterpret_cast<const float4*>(a.part_o + pr * a.dv + c);
-        const float mn = fmaxf(mx, ml.x);
-        const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
-        ls = ls * sa + ml.y * sb;
-        acc.x = acc.x * sa + x.x * sb; acc.y = acc.y * sa + x.y * sb;
-        acc.z = acc.z * sa + x.z * sb; acc.w = acc.w * sa + x.w * sb;
-        mx = mn;
+        const float4* src = reinterpret_cast<const float4*>(a.part_o + pr * a.dv + c);
+        float4 x[kMergeDims / 4];
+#pragma unroll
+        for (int i = 0; i < kMergeDims / 4; ++i) x[i] = src[i];
+        fold(ml, x);
       }
     }
     if (kg > 0) {
-      sacc[kg - 1][lane] = acc;
+#pragma unroll
+      for (int i = 0; i < kMergeDims / 4; ++i) sacc[kg - 1][i][lane] = acc[i];
       sml[kg - 1][lane] = make_float2(mx, ls);
     }
     __syncthreads();
     if (kg == 0 && live) {
 #pragma unroll
       for (int j = 0; j < kMergeGroups - 1; ++j) {
-        const float2 ml = sml[j][lane];
-        const float4 x = sacc[j][lane];
-        const float mn = fmaxf(mx, ml.x);
-        const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
-        ls = ls * sa + ml.y * sb;
-        acc.x = acc.x * sa + x.x * sb; acc.y = acc.y * sa + x.y * sb;
-        acc.z = acc.z * sa + x.z * sb; acc.w = acc.w * sa + x.w * sb;
-        mx = mn;
+        float4 x[kMergeDims / 4];
+#pragma unroll
+        for (int i = 0; i < kMergeDims / 4; ++i) x[i] = sacc[j][i][lane];
+        fold(sml[j][lane], x);
       }
       const float inv = ls > 0.f ? 1.f / ls : 0.f;
-      const int qi = n / a.hb, hh = n - qi * a.hb;
+      const int qi = rblk * qb + t, hh = n - rblk * kRows - t * a.hb;
       const int head = kvh * a.group + hbi * a.hb + hh;
-      uint2 wv;
-      wv.x = aia::pack_bf16x2(acc.x * inv, acc.y * inv);
-      wv.y = aia::pack_bf16x2(acc.z * inv, acc.w * inv);
-      uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs;
-      *reinterpret_cast<uint2*>(op + c) = wv;
+      uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs + c;
+      // 8-byte stores: the GQA output token stride need only be a multiple of 4
+#pragma unroll
+      for (int i = 0; i < kMergeDims / 4; ++i) {
+        uint2 wv;
+        wv.x = aia::pack_bf16x2(acc[i].x * inv, acc[i].y * inv);
+        wv.y = aia::pack_bf16x2(acc[i].z * inv, acc[i].w * inv);
+        *reinterpret_cast<uint2*>(op + 4 * i) = wv;
+      }
     }
     __syncthreads();
   }
@@ -1111,8 +1217,8 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
   mg.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
   mg.seg = seg; mg.part_o = part_o; mg.part_ml = part_ml;
   mg.out = out; mg.o_ts = o_ts; mg.o_hs = o_hs; mg.group = g.group; mg.hb = g.hb; mg.dv = dv;
-  mg.nw = nw; mg.hkv = g.hkv; mg.seg_cap = L.seg_cap;
-  const int64_t items = (int64_t)L.seg_cap * nw * ((kRows * (dv / 4) + 63) / 64);
+  mg.nw = nw; mg.hkv = g.hkv; mg.seg_cap = L.seg_cap; mg.rb = g.rb;
+  const int64_t items = (int64_t)L.seg_cap * nw * ((kRows * g.rb * (dv / kMergeDims) + 63) / 64);
   int64_t mgrid = items < 2048 ? items : 2048;
   if (mgrid < 1) mgrid = 1;
   merge_kernel<<<(unsigned)mgrid, 256, 0, s>>>(mg);
@@ -1136,7 +1242,7 @@ extern "C" int aia_attn_workspace_bytes(int32_t batch, int32_t num_tokens, int32
   if (int rc = check_heads("aia_attn_workspace_bytes", num_q_heads, num_kv_heads)) return rc;
   if (batch < 0 || num_tokens < 0 || head_dim_v <= 0 || !bytes)
     return aia::fail(AIA_ERR_INVALID, "aia_attn_workspace_bytes: bad arguments");
-  const Geometry g = geometry(num_q_heads, num_kv_heads);
+  const Geometry g = geometry(num_q_heads, num_kv_heads, batch, num_tokens, head_dim_v);
   *bytes = layout(batch, num_tokens, g, head_dim_v, kMaxWaves).total;
   return AIA_OK;
 }
@@ -1155,7 +1261,7 @@ extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens
     return fail(AIA_ERR_INVALID, "aia_attn_plan: null metadata");
   if (block_size <= 0) return fail(AIA_ERR_INVALID, "aia_attn_plan: block_size %d", block_size);
   if (!workspace) return fail(AIA_ERR_INVALID, "aia_attn_plan: null workspace");
-  const Geometry g = geometry(num_q_heads, num_kv_heads);
+  const Geometry g = geometry(num_q_heads, num_kv_heads, batch, num_tokens, head_dim_v);
   const int32_t waves = resolve_waves(num_waves, g, head_dim_v);
   const Layout L = layout(batch, num_tokens, g, head_dim_v, waves);
   if (workspace_bytes < L.total)
@@ -1183,6 +1289,8 @@ extern "C" int aia_paged_attention_gqa(
   if (int rc = check_heads("aia_paged_attention_gqa", num_q_heads, num_kv_heads)) return rc;
   if (head_dim != kHeadDim)
     return fail(AIA_ERR_UNSUPPORTED, "aia_paged_attention_gqa: head_dim %d (only 128)", head_dim);
+  if (!(scale > 0.f))
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: scale %g must be positive", (double)scale);
   if (block_size <= 0 || num_blocks <= 0)
     return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: block_size %d / num_blocks %d",
                 block_size, num_blocks);
@@ -1200,7 +1308,7 @@ extern "C" int aia_paged_attention_gqa(
     return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: new K/V rows must be 16-byte aligned "
                 "with token strides a multiple of 8 elements");
   if (num_tokens == 0 || batch == 0) return AIA_OK;
-  const Geometry g = geometry(num_q_heads, num_kv_heads);
+  const Geometry g = geometry(num_q_heads, num_kv_heads, batch, num_tokens, head_dim);
   const int32_t waves = resolve_waves(num_waves, g, head_dim);
   const Layout L = layout(batch, num_tokens, g, head_dim, waves);
   if (workspace_bytes < L.total)
@@ -1231,16 +1339,20 @@ extern "C" int aia_paged_attention_gqa(
   a.counters = reinterpret_cast<int32_t*>(ws + L.cnt);
   a.fused_merge = (flags & AIA_ATTN_FUSED_MERGE) && !(flags & AIA_ATTN_SKIP_MERGE) ? 1 : 0;
   hipStream_t s = (hipStream_t)stream;
+#define AIA_GQA_LAUNCH(NW)                                                      \
+  (g.rb == 2 ? gqa_attn_kernel<NW, 2><<<waves, 64 * NW, 0, s>>>(a)             \
+             : gqa_attn_kernel<NW, 1><<<waves, 64 * NW, 0, s>>>(a))
   switch (g.nw) {
-    case 1: gqa_attn_kernel<1><<<waves, 64, 0, s>>>(a); break;
-    case 2: gqa_attn_kernel<2><<<waves, 128, 0, s>>>(a); break;
-    case 3: gqa_attn_kernel<3><<<waves, 192, 0, s>>>(a); break;
-    case 4: gqa_attn_kernel<4><<<waves, 256, 0, s>>>(a); break;
-    case 5: gqa_attn_kernel<5><<<waves, 320, 0, s>>>(a); break;
-    case 6: gqa_attn_kernel<6><<<waves, 384, 0, s>>>(a); break;
-    case 7: gqa_attn_kernel<7><<<waves, 448, 0, s>>>(a); break;
-    default: gqa_attn_kernel<8><<<waves, 512, 0, s>>>(a); break;
+    case 1: AIA_GQA_LAUNCH(1); break;
+    case 2: AIA_GQA_LAUNCH(2); break;
+    case 3: AIA_GQA_LAUNCH(3); break;
+    case 4: AIA_GQA_LAUNCH(4); break;
+    case 5: AIA_GQA_LAUNCH(5); break;
+    case 6: AIA_GQA_LAUNCH(6); break;
+    case 7: AIA_GQA_LAUNCH(7); break;
+    default: AIA_GQA_LAUNCH(8); break;
   }
+#undef AIA_GQA_LAUNCH
   if (int rc = check_hip(hipGetLastError(), "gqa_attn_kernel launch")) return rc;
   if (a.fused_merge || (flags & AIA_ATTN_SKIP_MERGE)) return AIA_OK;
   return launch_merge(ws, L, g, g.nw, head_dim, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs, s);
@@ -1269,7 +1381,7 @@ extern "C" int aia_paged_attention_mla(
     return fail(AIA_ERR_INVALID, "aia_paged_attention_mla: tensors must be 16-byte aligned with "
                 "strides a multiple of 8 elements");
   if (num_tokens == 0 || batch == 0) return AIA_OK;
-  const Geometry g = geometry(num_heads, 1);
+  const Geometry g = geometry(num_heads, 1, batch, num_tokens, kMlaV);
   const int32_t waves = resolve_waves(num_waves, g, kMlaV);
   const Layout L = layout(batch, num_tokens, g, kMlaV, waves);
   if (workspace_bytes < L.total)

@@ -83,7 +83,8 @@ int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
  * query:  (num_tokens, Hq, head_dim) with the given token/head strides.
  * caches: contiguous (num_blocks, block_size, Hkv, head_dim).
  * out:    (num_tokens, Hq, head_dim) with the given strides.
- * head_dim must be 128.  The workspace must hold a plan made by
+ * head_dim must be 128 and scale positive (AIA_ERR_INVALID otherwise).
+ * The workspace must hold a plan made by
  * aia_attn_plan with the same metadata, head counts and num_waves.
  * key_new / value_new (optional, both or neither): this step's new K/V rows
  * (num_tokens, Hkv, 128), query token t being position Lk - Lq + i of its

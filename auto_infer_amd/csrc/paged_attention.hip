@@ -53,10 +53,11 @@ struct Geometry {
   int32_t hkv, group, hb, nhb, qb, nw, nkvg, rb, qs;
 };
 
-// rb: row blocks (of 16 query rows) per segment.  Two when a GQA launch has
-// multi-token requests (prefill, verify), so each K/V tile feeds 32 rows;
-// one for decode-only launches and MLA.  Planner and kernels derive it from
-// the same (batch, tokens, head_dim_v), so they always agree.
+// rb: row blocks (of 16 query rows) per segment.  Two when a GQA launch's
+// requests average more query tokens than one block holds (prefill chunks),
+// so each K/V tile feeds 32 rows; one for decode, short verify steps and
+// MLA, whose segments fit one block.  Planner and kernels derive it from the
+// same (batch, tokens, head_dim_v), so they always agree.
 Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_t dv) {
   Geometry g;
   g.hkv = hkv;
@@ -66,7 +67,7 @@ Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_
   g.qb = kRows / g.hb;                                  // query tokens per segment
   g.nw = hkv < kMaxGroupWaves ? hkv : kMaxGroupWaves;   // waves per work-group
   g.nkvg = (hkv + g.nw - 1) / g.nw;                     // kv-head groups
-  g.rb = (dv == kHeadDim && tokens > batch) ? 2 : 1;
+  g.rb = (dv == kHeadDim && tokens > (int64_t)batch * g.qb) ? 2 : 1;
   g.qs = g.qb * g.rb;                                   // query tokens per segment
   return g;
 }

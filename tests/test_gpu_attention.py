@@ -93,6 +93,23 @@ def test_chunked_prefill_and_decode_mixed():
     check(step)
 
 
+@pytest.mark.parametrize("lqs,lks,hq,hkv,bs", [
+    ([37, 1, 5, 1, 64], [137, 300, 5, 77, 64], 28, 4, 16),   # group 7: 2 tokens per block
+    ([3], [50], 7, 1, 16),                                  # second block holds one token
+    ([100, 1], [130, 40], 4, 4, 16),                        # group 1: 16 tokens per block
+    ([40, 3], [400, 3], 64, 2, 128),                        # group 32: head blocks
+])
+@pytest.mark.parametrize("waves", [1, 7, 64, 0])
+@pytest.mark.parametrize("flags", [0, ops.ATTN_FUSED_MERGE])
+def test_two_row_blocks(lqs, lks, hq, hkv, bs, waves, flags):
+    """Launches whose requests average more query tokens than a 16-row block
+    holds run segments of two row blocks (every K/V tile feeds both); the
+    result does not depend on it, nor on the split count or merge path."""
+    step = workloads.make_gqa_step(lqs=lqs, lks=lks, num_q_heads=hq, num_kv_heads=hkv,
+                                   block_size=bs, seed=41)
+    check(step, waves, flags)
+
+
 def test_block_size_not_multiple_of_tile():
     step = workloads.make_gqa_step(lqs=[1, 3], lks=[45, 90], num_q_heads=4,
                                    num_kv_heads=2, block_size=4, seed=2)

@@ -71,13 +71,25 @@ def cpu_model():
 
 
 def cpu_baseline(step, budget_s):
-    """The oracle (torch CPU eager restatement of write_kv + paged FIA) on
-    the host cores, timed on a bounded sample of the same workload."""
+    """The oracle on the host cores, timed on a bounded sample of the same
+    workload: the restated host packing of the step's BatchPlan (numpy,
+    model_runner.py:111-188) + torch CPU eager write_kv + paged FIA."""
+    from oracle.pack import build as pack_build
     from oracle.paged_attn import kv_write, paged_attention
+    from auto_infer_amd.execution import BatchPlan, RequestView, ScheduledRequest
     kc, vc = step.k_cache.clone(), step.v_cache.clone()
     threads = torch.get_num_threads()
+    bs = step.k_cache.shape[1]
+    tables = {}
+    for i, lk in enumerate(step.seqlens_kv):
+        tables[f"r{i}"] = tuple(int(b) for b in step.block_table[i, :(lk + bs - 1) // bs])
+    views = {f"r{i}": RequestView(f"r{i}", tuple(range(lk)), lk - 1, 1, 1, ())
+             for i, lk in enumerate(step.seqlens_kv)}
+    bplan = BatchPlan.make([ScheduledRequest(f"r{i}", 1, False, tables[f"r{i}"])
+                            for i in range(len(step.seqlens_kv))], views, tables)
 
     def one():
+        pack_build(bplan, bs)
         kv_write(step.k_new, step.v_new, kc, vc, step.slot_mapping)
         paged_attention(step.q, kc, vc, step.block_table, step.cu_seqlens_q,
                         step.seqlens_kv, step.scale).to(torch.bfloat16)
@@ -99,7 +111,8 @@ def cpu_baseline(step, budget_s):
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{len(times)} steps of config 1 (one layer: KV write + paged attention, "
+        "sample": f"{len(times)} steps of config 1 (packing of the step's plan + one layer: "
+                  f"KV write + paged attention, "
                   f"median {med * 1e3:.1f} ms), torch {torch.__version__} CPU eager, "
                   f"{threads} threads of {os.cpu_count()} ({cpu_model()})",
     }

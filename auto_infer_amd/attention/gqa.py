@@ -23,7 +23,7 @@ class GqaHipBackend(AttentionBackend):
 
     def __init__(self, n_q_heads: int, n_kv_heads: int, head_dim: int, scale: float,
                  num_layers: int, device, dtype, w: dict = None, layer_prefix=None,
-                 rms_eps=None, fuse_kv_write: bool = True):
+                 rms_eps=None, fuse_kv_write: bool = True, fuse_pre_attention: bool = True):
         self.n_q_heads = n_q_heads
         self.n_kv_heads = n_kv_heads
         self.head_dim = head_dim
@@ -38,6 +38,10 @@ class GqaHipBackend(AttentionBackend):
         # kernel of the following _attn (same cache contents, one launch less);
         # attention() always calls the two in that order.
         self.fuse_kv_write = fuse_kv_write
+        # With fuse_pre_attention, the split / QK-RMSNorm / RoPE steps run as
+        # one in-place kernel over the qkv projection (bf16 rounding where the
+        # torch ops round); q, k, v are then strided views of it.
+        self.fuse_pre_attention = fuse_pre_attention
         self._pending = None
 
     def alloc_kv_caches(self, num_blocks: int, block_size: int) -> list:
@@ -51,19 +55,31 @@ class GqaHipBackend(AttentionBackend):
         w = self.w
         p = self.layer_prefix(layer_idx) + "self_attn."
         qkv = lin(x, w[p + "qkv_proj.weight"], w.get(p + "qkv_proj.bias"))
-        q, k, v = qkv.split((n_q * hd, n_kv * hd, n_kv * hd), dim=-1)
-        q = q.view(T, n_q, hd)
-        k = k.view(T, n_kv, hd)
-        v = v.view(T, n_kv, hd)
         qn = w.get(p + "q_norm.weight")
-        if qn is not None:
-            q = rms_norm(q, qn, self.rms_eps)
-            k = rms_norm(k, w[p + "k_norm.weight"], self.rms_eps)
-        q = q * ctx.cos + rotate_half(q) * ctx.sin
-        k = k * ctx.cos + rotate_half(k) * ctx.sin
+        if self._fusable(qkv, ctx):
+            q, k, v = ops.qk_norm_rope(qkv, n_q, n_kv, ctx.cos, ctx.sin, qn,
+                                       w.get(p + "k_norm.weight") if qn is not None else None,
+                                       self.rms_eps if self.rms_eps is not None else 1e-6)
+        else:
+            q, k, v = qkv.split((n_q * hd, n_kv * hd, n_kv * hd), dim=-1)
+            q = q.view(T, n_q, hd)
+            k = k.view(T, n_kv, hd)
+            v = v.view(T, n_kv, hd)
+            if qn is not None:
+                q = rms_norm(q, qn, self.rms_eps)
+                k = rms_norm(k, w[p + "k_norm.weight"], self.rms_eps)
+            q = q * ctx.cos + rotate_half(q) * ctx.sin
+            k = k * ctx.cos + rotate_half(k) * ctx.sin
         self._write_kv(layer_idx, k, v, ctx)
         o = self._attn(layer_idx, q, k, v, ctx).reshape(T, n_q * hd)
         return lin(o, w[p + "o_proj.weight"])
+
+    def _fusable(self, qkv, ctx):
+        T = qkv.shape[0]
+        return (self.fuse_pre_attention and self.head_dim == 128 and qkv.dtype == torch.bfloat16
+                and qkv.is_cuda and qkv.stride(-1) == 1
+                and all(t.dtype == torch.bfloat16 and t.numel() == T * 128 and t.stride(-1) == 1
+                        for t in (ctx.cos, ctx.sin)))
 
     def _write_kv(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor, ctx) -> None:
         cache = ctx.kv_caches[layer_idx]

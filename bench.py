@@ -192,6 +192,36 @@ def other_configs(stream):
                                       "frac_of_peak": round(by / us / 1e3 / HBM_PEAK_GBS, 4)}
     del caches, mla
 
+    note("pre-attention: fused QK-norm + RoPE at the configs[1] shape")
+    from auto_infer_amd.attention.layers import rms_norm, rotate_half
+    T, hq, hkv, d = 2048, 28, 4, 128
+    g = torch.Generator(device=dev).manual_seed(5)
+    qkv0 = torch.randn(T, (hq + 2 * hkv) * d, device=dev, generator=g).bfloat16()
+    qkv = qkv0.clone()
+    pos = torch.arange(T, device=dev)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, d, 2, device=dev).float() / d))
+    emb = torch.cat([torch.outer(pos.float(), inv)] * 2, dim=-1)
+    cos, sin = emb.cos().bfloat16()[:, None], emb.sin().bfloat16()[:, None]
+    wq = torch.ones(d, device=dev, dtype=torch.bfloat16)
+    wk = torch.ones(d, device=dev, dtype=torch.bfloat16)
+
+    def torch_ops(i):
+        q, k, v = qkv.split((hq * d, hkv * d, hkv * d), dim=-1)
+        q = rms_norm(q.view(T, hq, d), wq, 1e-6)
+        k = rms_norm(k.view(T, hkv, d), wk, 1e-6)
+        return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
+
+    fused_us = _time_graph(lambda i: ops.qk_norm_rope(qkv, hq, hkv, cos, sin, wq, wk, 1e-6),
+                           stream, 5, 20)
+    torch_us = _time_graph(torch_ops, stream, 5, 20)
+    by = 2 * T * (hq + hkv) * d * 2 + 2 * T * d * 2     # Q, K read + written; cos, sin read
+    res["pre_attention_qk_norm_rope"] = {
+        "shape": f"T {T}, Hq {hq}, Hkv {hkv}, D {d}, QK-norm + NeoX RoPE, in place",
+        "fused_us": round(fused_us, 2), "torch_ops_us": round(torch_us, 2),
+        "GBps": round(by / fused_us / 1e3, 1),
+        "frac_of_peak": round(by / fused_us / 1e3 / HBM_PEAK_GBS, 4)}
+    del qkv, qkv0
+
     note("configs[4] stress: 80 GB pool")
     # config 5: 80 GB fragmented pool, GPU packing of the 256-request plan
     bs, hkv, d, hq = 128, 8, 128, 64

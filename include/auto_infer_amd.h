@@ -171,6 +171,22 @@ int aia_pack_rows(const int64_t* token_update_index, const int64_t* token_update
                   int32_t* seqlens_kv, int64_t* last_rows, int64_t* sample_rows,
                   int32_t sample_count, int32_t sample_cap, void* stream);
 
+/* Fused pre-attention, in place over a packed qkv projection (T rows of
+ * (Hq + 2 Hkv) x 128 bf16 values, token stride qkv_token_stride): per-head
+ * RMSNorm of the Q and K heads with the given weights (both or neither;
+ * Qwen3 QK-Norm) and NeoX RoPE x * cos + rotate_half(x) * sin with cos/sin
+ * (T, 128) bf16 rows.  V is left as is.  Replaces the split / rms_norm /
+ * rotary steps of _GqaProjRopeMixin.attention (auto_infer/layers/attention/
+ * gqa.py:27-49; auto_infer/layers/norm.py:5-8; auto_infer/layers/
+ * rotary_embedding/__init__.py:10-13), rounding to bf16 where those bf16
+ * ops round.  The Q, K and V slices then go to aia_paged_attention_gqa as
+ * query / key_new / value_new through their strides.  head_dim must be 128. */
+int aia_qk_norm_rope(void* qkv, int64_t qkv_token_stride, int32_t num_tokens,
+                     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                     const void* cos, int64_t cos_token_stride, const void* sin,
+                     int64_t sin_token_stride, const void* q_norm_weight,
+                     const void* k_norm_weight, float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

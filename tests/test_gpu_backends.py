@@ -162,3 +162,45 @@ def test_mla_backend_absorbed_prefill_then_decode():
     caches_r = twin.alloc_kv_caches(8, bs)
     steps = [[(0, 7, [2]), (0, 18, [5, 0])], [(7, 1, [2]), (18, 1, [5, 0])]]
     run_pair(hip, twin, steps, caches_h, caches_r, bs, hidden, seed=3)
+
+
+@pytest.mark.parametrize("qwen3", [False, True])
+def test_gqa_fused_pre_attention_matches_torch_path(qwen3):
+    """The in-place QK-norm + RoPE kernel against the torch ops it replaces
+    (split, rms_norm, rotate_half), end to end through attention(): without
+    QK-norm the KV caches are bit-exact, with it within one bf16 ulp of each
+    row's largest value."""
+    g = torch.Generator().manual_seed(7)
+    hq, hkv, d, hidden, bs = 8, 2, 128, 256, 16
+    p = "model.layers.0.self_attn."
+    w = {p + "qkv_proj.weight": (torch.randn((hq + 2 * hkv) * d, hidden, generator=g) / 16).bfloat16(),
+         p + "o_proj.weight": (torch.randn(hidden, hq * d, generator=g) / 32).bfloat16()}
+    if qwen3:
+        w[p + "q_norm.weight"] = (1 + 0.1 * torch.randn(d, generator=g)).bfloat16()
+        w[p + "k_norm.weight"] = (1 + 0.1 * torch.randn(d, generator=g)).bfloat16()
+    else:
+        w[p + "qkv_proj.bias"] = (0.1 * torch.randn((hq + 2 * hkv) * d, generator=g)).bfloat16()
+    w = {k: v.to(DEV) for k, v in w.items()}
+    kw = dict(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, scale=d ** -0.5, num_layers=1,
+              device=DEV, dtype=torch.bfloat16, w=w, rms_eps=1e-6 if qwen3 else None)
+    fused = GqaHipBackend(**kw)
+    plain = GqaHipBackend(fuse_pre_attention=False, **kw)
+    cf, cp = fused.alloc_kv_caches(10, bs), plain.alloc_kv_caches(10, bs)
+    for rows in ([(0, 9, [4]), (0, 30, [1, 6])], [(9, 1, [4]), (30, 1, [1, 6])]):
+        T = sum(n for _, n, _ in rows)
+        x = (torch.randn(T, hidden, generator=g) * 0.5).bfloat16().to(DEV)
+        ctx_f, positions = make_ctx(fused, cf, rows, bs)
+        ctx_p, _ = make_ctx(plain, cp, rows, bs)
+        cos, sin = rope_tables(positions * 37, d)
+        ctx_f.cos = ctx_p.cos = cos.to(DEV)
+        ctx_f.sin = ctx_p.sin = sin.to(DEV)
+        of = fused.attention(0, x, ctx_f)
+        op = plain.attention(0, x, ctx_p)
+        torch.cuda.synchronize()
+        if qwen3:
+            diff = (cf[0].float() - cp[0].float()).abs()
+            assert bool((diff <= cp[0].float().abs().amax(-1, keepdim=True) * 2.0 ** -7).all())
+        else:
+            assert torch.equal(cf[0].cpu(), cp[0].cpu())
+        scale = op.float().abs().max().item()
+        assert (of.float() - op.float()).abs().max().item() <= TOL * max(1.0, scale)

@@ -78,6 +78,54 @@ def qk_norm_rope(qkv, num_q_heads, num_kv_heads, cos, sin, q_norm_weight=None,
     return q.view(T, num_q_heads, D), k.view(T, num_kv_heads, D), v.view(T, num_kv_heads, D)
 
 
+def mtp_compact(preds, drafts, active_mask, hidden, positions, slots, scratch_positions,
+                scratch_slots, *, accepted=None, out_hidden=None, out_tokens=None,
+                out_positions=None, out_slots=None):
+    """Accepted draft counts and the compaction of confirmed target rows for
+    the MTP drafter, in one launch (reference: GraphMtpRunner._target_body,
+    auto_infer/worker/graph_mtp_runner.py:224-248).  Shapes: preds (g, w)
+    int64, drafts (g, w - 1) int64, active_mask (g,), hidden (g * w, H) bf16,
+    positions / scratch_positions (g * w,) int64, slots / scratch_slots
+    (g * w,) int32.  Outputs (allocated unless given, so a graph can pass
+    fixed buffers): accepted (g,) int64, hidden (g * w, H), tokens and
+    positions (g * w,) int64, slots (g * w,) int32.  Returns them as a tuple
+    (accepted, hidden, tokens, positions, slots)."""
+    _check_device_tensor(preds, "preds", torch.int64)
+    _require(preds.dim() == 2 and preds.is_contiguous(), "preds must be a contiguous (g, w) tensor")
+    g, w = preds.shape
+    _require(1 <= g <= 64 and w >= 2, "gear must be in [1, 64] and query width >= 2")
+    _check_device_tensor(drafts, "drafts", torch.int64)
+    _require(tuple(drafts.shape) == (g, w - 1) and drafts.is_contiguous(),
+             "drafts must be a contiguous (g, w - 1) tensor")
+    _check_device_tensor(active_mask, "active_mask")
+    active = active_mask.to(torch.int32).contiguous()
+    _require(active.numel() == g, "active_mask must have g entries")
+    _check_device_tensor(hidden, "hidden", _BF16)
+    _require(hidden.dim() == 2 and hidden.shape[0] == g * w and hidden.stride(1) == 1,
+             "hidden must be (g * w, H) with unit inner stride")
+    H = hidden.shape[1]
+    for t, name, dt in ((positions, "positions", torch.int64), (slots, "slots", torch.int32),
+                        (scratch_positions, "scratch_positions", torch.int64),
+                        (scratch_slots, "scratch_slots", torch.int32)):
+        _check_device_tensor(t, name, dt)
+        _require(t.numel() == g * w and t.is_contiguous(), f"{name} must hold g * w entries")
+    dev = preds.device
+    accepted = accepted if accepted is not None else torch.empty(g, dtype=torch.int64, device=dev)
+    out_hidden = out_hidden if out_hidden is not None else torch.empty(g * w, H, dtype=_BF16, device=dev)
+    out_tokens = out_tokens if out_tokens is not None else torch.empty(g * w, dtype=torch.int64, device=dev)
+    out_positions = (out_positions if out_positions is not None
+                     else torch.empty(g * w, dtype=torch.int64, device=dev))
+    out_slots = out_slots if out_slots is not None else torch.empty(g * w, dtype=torch.int32, device=dev)
+    _require(out_hidden.shape == (g * w, H) and out_hidden.stride(1) == 1 and out_hidden.dtype == _BF16,
+             "out_hidden must be (g * w, H) bf16 with unit inner stride")
+    _native.call("aia_mtp_compact", _ptr(preds), _ptr(drafts), _ptr(active), _ptr(hidden),
+                 hidden.stride(0), _ptr(positions), _ptr(slots), _ptr(scratch_positions),
+                 _ptr(scratch_slots), g, w, H, _ptr(accepted), _ptr(out_hidden),
+                 out_hidden.stride(0), _ptr(out_tokens), _ptr(out_positions), _ptr(out_slots),
+                 _stream(dev))
+    return accepted, out_hidden, out_tokens, out_positions, out_slots
+
+
 def write_kv(key, value, key_cache, value_cache, slot_mapping):
     """Scatter this step's K/V into the paged cache by slot index.
 

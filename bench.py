@@ -222,6 +222,44 @@ def other_configs(stream):
         "frac_of_peak": round(by / fused_us / 1e3 / HBM_PEAK_GBS, 4)}
     del qkv, qkv0
 
+    note("MTP verify compaction at the configs[3] gear")
+    gq, wq, hid = 16, 2, 4096
+    g2 = torch.Generator(device=dev).manual_seed(6)
+    preds = torch.randint(0, 100, (gq, wq), device=dev, generator=g2)
+    drafts = torch.where(torch.rand(gq, wq - 1, device=dev, generator=g2) < 0.7, preds[:, :-1],
+                         torch.randint(0, 100, (gq, wq - 1), device=dev, generator=g2))
+    amask = torch.ones(gq, dtype=torch.int32, device=dev)
+    hpre = torch.randn(gq * wq, hid, device=dev, generator=g2).bfloat16()
+    ppos = torch.arange(gq * wq, device=dev)
+    pslot = torch.arange(gq * wq, device=dev, dtype=torch.int32)
+    spos = torch.zeros(gq * wq, dtype=torch.int64, device=dev)
+    sslot = torch.zeros(gq * wq, dtype=torch.int32, device=dev)
+    bufs = dict(accepted=torch.empty(gq, dtype=torch.int64, device=dev),
+                out_hidden=torch.empty(gq * wq, hid, dtype=torch.bfloat16, device=dev),
+                out_tokens=torch.empty(gq * wq, dtype=torch.int64, device=dev),
+                out_positions=torch.empty(gq * wq, dtype=torch.int64, device=dev),
+                out_slots=torch.empty(gq * wq, dtype=torch.int32, device=dev))
+
+    def torch_chain(i):          # graph_mtp_runner.py:224-248 as torch ops
+        acc = torch.cumprod((drafts == preds[:, :-1]).to(torch.int32), 1).sum(1) * amask
+        lengths = amask * (1 + acc)
+        starts = lengths.cumsum(0) - lengths
+        dest = torch.arange(gq * wq, device=dev)
+        owner = ((dest[:, None] >= starts[None, :]).sum(1) - 1).clamp_min(0)
+        source = (wq * owner + dest - starts[owner]).clamp(0, gq * wq - 1)
+        valid = dest < lengths.sum()
+        bufs["out_hidden"].copy_(torch.where(valid[:, None], hpre[source], torch.zeros_like(hpre)))
+        bufs["out_tokens"].copy_(torch.where(valid, preds.reshape(-1)[source], torch.zeros_like(dest)))
+        bufs["out_positions"].copy_(torch.where(valid, ppos[source], spos))
+        bufs["out_slots"].copy_(torch.where(valid, pslot[source], sslot))
+
+    fused_us = _time_graph(lambda i: ops.mtp_compact(preds, drafts, amask, hpre, ppos, pslot,
+                                                     spos, sslot, **bufs), stream, 5, 20)
+    chain_us = _time_graph(torch_chain, stream, 5, 20)
+    res["mtp_verify_compaction"] = {
+        "shape": f"gear {gq}, query width {wq}, hidden {hid} bf16",
+        "fused_us": round(fused_us, 2), "torch_ops_us": round(chain_us, 2)}
+
     note("configs[4] stress: 80 GB pool")
     # config 5: 80 GB fragmented pool, GPU packing of the 256-request plan
     bs, hkv, d, hq = 128, 8, 128, 64

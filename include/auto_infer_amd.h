@@ -187,6 +187,28 @@ int aia_qk_norm_rope(void* qkv, int64_t qkv_token_stride, int32_t num_tokens,
                      int64_t sin_token_stride, const void* q_norm_weight,
                      const void* k_norm_weight, float eps, void* stream);
 
+/* On-device MTP verify compaction, one launch.  Replaces the accept/compact
+ * block of GraphMtpRunner._target_body (auto_infer/worker/
+ * graph_mtp_runner.py:224-248): for a gear of `gear` (<= 64) requests of
+ * query_width rows each (draft depth + 1), accepted[r] = the number of
+ * leading drafts equal to the target's predictions, times active_mask[r];
+ * then each request's 1 + accepted[r] confirmed rows are packed in request
+ * order (confirmed_layout, spec_decode/layout.py:17-43) into out_hidden /
+ * out_tokens / out_positions / out_slots (gear * query_width rows); rows past
+ * the confirmed total get zero hidden/token and the scratch position/slot.
+ * preds int64 [gear][query_width], drafts int64 [gear][query_width - 1],
+ * active_mask int32 [gear] (0/1, active requests a prefix), hidden bf16
+ * [gear * query_width][hidden_dim] (row stride in elements), positions
+ * int64 / slots int32 / scratch_* [gear * query_width], accepted int64
+ * [gear]. */
+int aia_mtp_compact(const int64_t* preds, const int64_t* drafts, const int32_t* active_mask,
+                    const void* hidden, int64_t hidden_row_stride, const int64_t* positions,
+                    const int32_t* slots, const int64_t* scratch_positions,
+                    const int32_t* scratch_slots, int32_t gear, int32_t query_width,
+                    int32_t hidden_dim, int64_t* accepted, void* out_hidden,
+                    int64_t out_hidden_row_stride, int64_t* out_tokens,
+                    int64_t* out_positions, int32_t* out_slots, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

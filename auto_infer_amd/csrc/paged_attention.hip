@@ -74,9 +74,17 @@ Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_
 
 // Workspace layout (all offsets 256-byte aligned).
 struct Layout {
-  int64_t hdr, seg, wave, part_ml, part_o, cnt, req, total;
-  int64_t seg_cap, part_cap;
+  int64_t hdr, seg, wave, part_ml, part_o, cnt, req, mrg, total;
+  int64_t seg_cap, part_cap, mrg_cap;
 };
+
+constexpr int kMergeDims = 16;   // output dims per merge element
+constexpr int kMrgInts = 8;      // merge record
+
+// Merge slices (64 elements of kMergeDims dims) per (segment, kv head) at most.
+int64_t merge_slices(const Geometry& g, int32_t dv) {
+  return ((int64_t)kRows * g.rb * (dv / kMergeDims) + 63) / 64;
+}
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
@@ -90,6 +98,8 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
   L.wave = off;     off = align256(off + (int64_t)waves * kRecInts * 4);
   L.part_ml = off;  off = align256(off + L.part_cap * g.nw * kRows * g.rb * 8);
   L.part_o = off;   off = align256(off + L.part_cap * g.nw * kRows * g.rb * (int64_t)dv * 4);
+  L.mrg_cap = L.seg_cap * g.nw * merge_slices(g, dv);
+  L.mrg = off;      off = align256(off + L.mrg_cap * kMrgInts * 4);
   L.cnt = off;      off = align256(off + L.seg_cap * g.nw * 4);
   L.req = off;      off = align256(off + ((int64_t)batch + 1) * 4);
   L.total = off;
@@ -136,6 +146,33 @@ __device__ int block_exclusive_scan(int v, int* wave_sums, int* total) {
   return before + x - v;
 }
 
+// The same for two values at once (one pass of barriers instead of two).
+__device__ int2 block_exclusive_scan2(int2 v, int2* wave_sums2, int2* total) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  int2 x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y0 = __shfl_up(x.x, d), y1 = __shfl_up(x.y, d);
+    if (lane >= d) { x.x += y0; x.y += y1; }
+  }
+  if (lane == 63) wave_sums2[wid] = x;
+  __syncthreads();
+  if (wid == 0) {
+    int2 s = lane < kPlanThreads / 64 ? wave_sums2[lane] : make_int2(0, 0);
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y0 = __shfl_up(s.x, d), y1 = __shfl_up(s.y, d);
+      if (lane >= d) { s.x += y0; s.y += y1; }
+    }
+    if (lane < kPlanThreads / 64) wave_sums2[lane] = s;  // inclusive
+  }
+  __syncthreads();
+  const int2 before = wid ? wave_sums2[wid - 1] : make_int2(0, 0);
+  *total = wave_sums2[kPlanThreads / 64 - 1];
+  __syncthreads();
+  return make_int2(before.x + x.x - v.x, before.y + x.y - v.y);
+}
+
 // Segment record, 8 ints: b, kv-head group | head block << 16 | (last query
 // block of its request) << 30, first query
 // token (global row), query tokens | q0 << 8 (q0 = first query of the block
@@ -154,11 +191,13 @@ constexpr int kPadBelow = 16;            // pad segments when ranges are shorter
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ kvlen,
     const int32_t* __restrict__ block_table, int64_t bt_stride, int32_t block_size,
-    int32_t batch, Geometry g, int32_t waves,
+    int32_t batch, Geometry g, int32_t waves, int32_t dv,
     int32_t* __restrict__ hdr, int32_t* __restrict__ seg, int32_t* __restrict__ wave_rec,
-    int32_t* __restrict__ counters, int32_t* __restrict__ req_scratch) {
+    int32_t* __restrict__ counters, int32_t* __restrict__ req_scratch,
+    int32_t* __restrict__ mrg) {
   __shared__ int lds[kPlanLds];
   __shared__ int wave_sums[kPlanThreads / 64];
+  __shared__ int2 wave_sums2[kPlanThreads / 64];
   const int tid = threadIdx.x;
   const int per_req = g.nkvg * g.nhb;
   // request metadata in LDS when it fits, else in the workspace / inputs
@@ -315,6 +354,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
 
   // 3) partial slots: a segment split over k ranges owns k consecutive slots
   carry = 0;
+  int mcarry = 0;
   for (int base = 0, c = 0; base < nseg; base += kPlanThreads, ++c) {
     const int s = base + tid;
     int np = 0;
@@ -330,16 +370,48 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       }
       np = (tb + nt - 1) / tpw - tb / tpw + 1;
     }
-    int tot;
-    const int ex = block_exclusive_scan(np, wave_sums, &tot);
+    // merge work of a split segment: one record per (kv head, slice of 64
+    // elements of its row span), so the merge kernel visits only real work
+    int mcnt = 0, nwv = 0, nsl = 0, rows = 0;
+    int r0[4] = {0, 0, 0, 0};
     if (s < nseg) {
-      seg[(int64_t)s * 8 + 7] = carry + ex;
       for (int i = 0; i < g.nw; ++i) counters[(int64_t)s * g.nw + i] = 0;
+      if (np > 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r0[i] = seg[(int64_t)s * 8 + i];
+        const int nq = r0[3] & 0xff;
+        const int nblk = (nq + g.qb - 1) / g.qb;
+        rows = (nblk - 1) * kRows + min(kRows, (nq - (nblk - 1) * g.qb) * g.hb);
+        nwv = min(g.nw, g.hkv - (r0[1] & 0xffff) * g.nw);
+        nsl = (rows * (dv / kMergeDims) + 63) / 64;
+        mcnt = nwv * nsl;
+      }
     }
+    int2 tot2;
+    const int2 ex2 = block_exclusive_scan2(make_int2(np, mcnt), wave_sums2, &tot2);
+    const int ex = ex2.x, tot = tot2.x, mex = ex2.y, mtot = tot2.y;
+    if (s < nseg) seg[(int64_t)s * 8 + 7] = carry + ex;
+    if (mcnt > 0) {
+      const int seg_rows = kRows * g.rb;
+      for (int i = 0; i < mcnt; ++i) {
+        const int w = i / nsl, sl = i - w * nsl;
+        int* m = mrg + (int64_t)(mcarry + mex + i) * kMrgInts;
+        m[0] = r0[2];                                        // first query token
+        m[1] = r0[3] & 0xff;                                 // query tokens
+        m[2] = (r0[1] & 0xffff) * g.nw + w;                  // kv head
+        m[3] = (r0[1] >> 16) & 0x3fff;                       // head block
+        m[4] = ((carry + ex) * g.nw + w) * seg_rows;         // first partial row
+        m[5] = np;
+        m[6] = sl;
+        m[7] = rows;
+      }
+    }
+    mcarry += mtot;
     carry += tot;
   }
   if (tid == 0) {
     hdr[0] = nseg; hdr[1] = total_tiles; hdr[2] = tpw; hdr[3] = carry; hdr[4] = waves;
+    hdr[5] = mcarry;
     // sentinel record so readers may look one past the end
     int* r = seg + (int64_t)nseg * 8;
     r[0] = 0; r[1] = 0; r[2] = 0; r[3] = 0; r[4] = 0;
@@ -879,21 +951,19 @@ struct MergeArgs {
   uint16_t* out;
   int64_t o_ts, o_hs;
   int32_t group, hb, dv, nw, hkv, rb;
-  int64_t seg_cap;
+  const int32_t* mrg;
+  int64_t mrg_cap;
 };
 
-// Merge of split partials.  A work item is (split segment, kv head, slice of
-// 64 output elements), an element being 16 dims of one row of the segment's
-// row span (rows up to its last valid one, so decode items are small; rows
-// of a block past its qb tokens are skipped).  The 4 waves of the
-// work-group take every 4th partial each, so all partial loads of a
-// segment are in flight together, and combine their running (max, sum,
-// accumulator) through LDS.  The segment record is loaded together with the
-// header; items are ordered by segment, so one past the live segments ends
-// the loop.  An item is a chain of dependent loads, so elements are wide:
-// fewer items, fewer chains per work-group.
+// Merge of split partials.  The planner lists the merge work: one record per
+// (split segment, kv head, slice of 64 output elements), an element being 16
+// dims of one row of the segment's row span (rows of a block past its qb
+// tokens are skipped), and nothing for segments that one range covers.  The
+// 4 waves of a work-group take every 4th partial each, so all partial loads
+// of an item are in flight together, and combine their running (max, sum,
+// accumulator) through LDS.  The item count is loaded together with the
+// first record.
 constexpr int kMergeGroups = 4;
-constexpr int kMergeDims = 16;   // dims per element
 
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   __shared__ float4 sacc[kMergeGroups - 1][kMergeDims / 4][64];
@@ -901,31 +971,21 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int lane = threadIdx.x & 63, kg = threadIdx.x >> 6;
   const int epr = a.dv / kMergeDims;                      // elements per row
   const int seg_rows = kRows * a.rb;
-  const int nsl = (seg_rows * epr + 63) / 64;             // slices per (segment, head)
   const int qb = kRows / a.hb;
-  const int64_t items = (int64_t)a.seg_cap * a.nw * nsl;
-  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
-    const int sw = (int)(item / nsl), sl = (int)(item - (int64_t)sw * nsl);
-    const int s = sw / a.nw, wid = sw - s * a.nw;
-    const int4 r0 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8);
-    const int4 r1 = *reinterpret_cast<const int4*>(a.seg + (int64_t)s * 8 + 4);
-    const int nseg = a.hdr[0], tpw = a.hdr[2];
-    if (s >= nseg) break;                                  // uniform over the group
-    const int tb = r1.y, te = r1.z;
-    const int np = te > tb ? (te - 1) / tpw - tb / tpw + 1 : 0;
-    const int kvh = (r0.y & 0xffff) * a.nw + wid, hbi = (r0.y >> 16) & 0x3fff, qtok0 = r0.z,
-              nq = r0.w & 0xff;
-    const int nblk = (nq + qb - 1) / qb;
-    const int rows = (nblk - 1) * kRows + min(kRows, (nq - (nblk - 1) * qb) * a.hb);
-    if (np <= 1 || kvh >= a.hkv || sl * 64 >= rows * epr) continue;   // uniform
+  const int64_t pstride = (int64_t)a.nw * seg_rows;
+  for (int64_t item = blockIdx.x; item < a.mrg_cap; item += gridDim.x) {
+    const int4 m0 = *reinterpret_cast<const int4*>(a.mrg + item * kMrgInts);
+    const int4 m1 = *reinterpret_cast<const int4*>(a.mrg + item * kMrgInts + 4);
+    if (item >= a.hdr[5]) break;                           // uniform over the group
+    const int qtok0 = m0.x, nq = m0.y, kvh = m0.z, hbi = m0.w;
+    const int row_base = m1.x, np = m1.y, sl = m1.z, rows = m1.w;
     const int e = sl * 64 + lane;
     int n = e / epr;
     const int c = (e - n * epr) * kMergeDims;
     const int rblk = n / kRows, t = (n - rblk * kRows) / a.hb;
     const bool live = e < rows * epr && t < qb && rblk * qb + t < nq;
     if (!live) n = 0;
-    const int64_t row0 = ((int64_t)r1.w * a.nw + wid) * seg_rows + n;
-    const int64_t pstride = (int64_t)a.nw * seg_rows;
+    const int64_t row0 = (int64_t)row_base + n;
     float4 acc[kMergeDims / 4];
 #pragma unroll
     for (int i = 0; i < kMergeDims / 4; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1218,8 +1278,9 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
   mg.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
   mg.seg = seg; mg.part_o = part_o; mg.part_ml = part_ml;
   mg.out = out; mg.o_ts = o_ts; mg.o_hs = o_hs; mg.group = g.group; mg.hb = g.hb; mg.dv = dv;
-  mg.nw = nw; mg.hkv = g.hkv; mg.seg_cap = L.seg_cap; mg.rb = g.rb;
-  const int64_t items = (int64_t)L.seg_cap * nw * ((kRows * g.rb * (dv / kMergeDims) + 63) / 64);
+  mg.nw = nw; mg.hkv = g.hkv; mg.rb = g.rb;
+  mg.mrg = reinterpret_cast<const int32_t*>(ws + L.mrg); mg.mrg_cap = L.mrg_cap;
+  const int64_t items = L.mrg_cap;
   int64_t mgrid = items < 2048 ? items : 2048;
   if (mgrid < 1) mgrid = 1;
   merge_kernel<<<(unsigned)mgrid, 256, 0, s>>>(mg);
@@ -1270,9 +1331,11 @@ extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens
                 (long long)workspace_bytes, (long long)L.total);
   char* ws = static_cast<char*>(workspace);
   plan_kernel<<<1, kPlanThreads, 0, (hipStream_t)stream>>>(
-      cu_seqlens_q, seqlens_kv, block_table, block_table_stride, block_size, batch, g, waves, reinterpret_cast<int32_t*>(ws + L.hdr),
+      cu_seqlens_q, seqlens_kv, block_table, block_table_stride, block_size, batch, g, waves,
+      head_dim_v, reinterpret_cast<int32_t*>(ws + L.hdr),
       reinterpret_cast<int32_t*>(ws + L.seg), reinterpret_cast<int32_t*>(ws + L.wave),
-      reinterpret_cast<int32_t*>(ws + L.cnt), reinterpret_cast<int32_t*>(ws + L.req));
+      reinterpret_cast<int32_t*>(ws + L.cnt), reinterpret_cast<int32_t*>(ws + L.req),
+      reinterpret_cast<int32_t*>(ws + L.mrg));
   return check_hip(hipGetLastError(), "aia_attn_plan launch");
 }
 

@@ -186,7 +186,10 @@ __device__ int2 block_exclusive_scan2(int2 v, int2* wave_sums2, int2* total) {
 // dependent lookup.
 constexpr int kPlanLds = 12288;          // ints of LDS scratch (48 KB)
 constexpr int kPlanRegChunks = 8;        // segments kept in registers: 8 x 1024
-constexpr int kPadBelow = 16;            // pad segments when ranges are shorter (tiles)
+#ifndef AIA_PAD_BELOW
+#define AIA_PAD_BELOW 16
+#endif
+constexpr int kPadBelow = AIA_PAD_BELOW;  // pad segments when ranges are shorter (tiles)
 
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ kvlen,
@@ -1134,6 +1137,15 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
 
   int parity = 0;
   auto compute = [&](int lt, const uint4 (&kk)[5]) {
+#ifdef AIA_NOCOMPUTE
+    {
+      uint32_t x = 0;
+#pragma unroll
+      for (int j = 0; j < 5; ++j) x ^= kk[j].x ^ kk[j].y ^ kk[j].z ^ kk[j].w;
+      o[0][0] += __uint_as_float(x & 0x3fffffu);
+      return;
+    }
+#endif
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 5; ++j) {

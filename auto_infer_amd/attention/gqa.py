@@ -76,10 +76,12 @@ class GqaHipBackend(AttentionBackend):
 
     def _fusable(self, qkv, ctx):
         T = qkv.shape[0]
+        def aligned(t):          # 16-byte accesses: 8-element strides, 16-byte base
+            return t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
         return (self.fuse_pre_attention and self.head_dim == 128 and qkv.dtype == torch.bfloat16
-                and qkv.is_cuda and qkv.stride(-1) == 1
+                and qkv.is_cuda and qkv.stride(-1) == 1 and aligned(qkv)
                 and all(t.dtype == torch.bfloat16 and t.numel() == T * 128 and t.stride(-1) == 1
-                        for t in (ctx.cos, ctx.sin)))
+                        and aligned(t) for t in (ctx.cos, ctx.sin)))
 
     def _write_kv(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor, ctx) -> None:
         cache = ctx.kv_caches[layer_idx]

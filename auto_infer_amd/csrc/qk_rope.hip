@@ -13,16 +13,17 @@
 // fp32 sum rounded once, as torch computes them), which makes the RoPE part
 // bit-identical for identical inputs.
 //
-// Layout: a half-wave (32 lanes) owns one (token, head) row of 128 dims;
-// lane j holds dims {2j, 2j+1} and their rotation partners {2j+64, 2j+65},
-// so rotate_half needs no cross-lane traffic and every access is a 4-byte
-// load/store of a contiguous pair.  V is not touched: the attention kernel
+// Layout: 8 lanes own one (token, head) row of 128 dims; lane j holds dims
+// 8j .. 8j+7 and their rotation partners 64 + 8j .. 64 + 8j + 7, so
+// rotate_half needs no cross-lane traffic and every access is a 16-byte
+// load/store of 8 contiguous values.  V is not touched: the attention kernel
 // reads it (and the rotated K) straight from the qkv buffer.
 #include "common.h"
 
 namespace {
 
 constexpr int kDim = 128;
+constexpr int kRowsPerBlock = 32;   // row slots per work-group (8 lanes each)
 
 struct RopeArgs {
   uint16_t* qkv;
@@ -40,41 +41,64 @@ __device__ __forceinline__ float bf(uint32_t bits16) { return __uint_as_float(bi
 __device__ __forceinline__ uint32_t rnd(float x) { return aia::pack_bf16x2(x, 0.f) & 0xffffu; }
 __device__ __forceinline__ float rbf(float x) { return bf(rnd(x)); }   // round to bf16
 
+__device__ __forceinline__ void unpack8(uint4 w, float (&v)[16], int at) {
+  const uint32_t p[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { v[at + 2 * i] = bf(p[i] & 0xffffu); v[at + 2 * i + 1] = bf(p[i] >> 16); }
+}
+
+// One work-group per token: its cos/sin (and the norm weights) are loaded
+// once and reused by the 32 row slots, which loop over the token's heads.
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
   const int heads = a.hq + a.hkv;
-  const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
-  if (row >= (int64_t)a.tokens * heads) return;
-  const int j = threadIdx.x & 31;
-  const int t = (int)(row / heads), h = (int)(row - (int64_t)t * heads);
-  uint16_t* x = a.qkv + (int64_t)t * a.qkv_ts + (int64_t)h * kDim;
-  const uint32_t lo = *reinterpret_cast<const uint32_t*>(x + 2 * j);        // dims 2j, 2j+1
-  const uint32_t hi = *reinterpret_cast<const uint32_t*>(x + 64 + 2 * j);   // dims 2j+64, +65
-  float v[4] = {bf(lo & 0xffffu), bf(lo >> 16), bf(hi & 0xffffu), bf(hi >> 16)};
-  const uint16_t* w = h < a.hq ? a.wq : a.wk;
-  if (w) {
-    float ss = (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
-#pragma unroll
-    for (int d = 16; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 32);
-    const float r = 1.0f / __builtin_sqrtf(ss * (1.0f / kDim) + a.eps);
-    const uint32_t wlo = *reinterpret_cast<const uint32_t*>(w + 2 * j);
-    const uint32_t whi = *reinterpret_cast<const uint32_t*>(w + 64 + 2 * j);
-    const float wv[4] = {bf(wlo & 0xffffu), bf(wlo >> 16), bf(whi & 0xffffu), bf(whi >> 16)};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = rbf((v[i] * r) * wv[i]);
+  const int t = blockIdx.x;
+  const int j = threadIdx.x & 7, slot = threadIdx.x >> 3;
+  const uint16_t* cp = a.cos + (int64_t)t * a.cos_ts;
+  const uint16_t* sp = a.sin + (int64_t)t * a.sin_ts;
+  // dims 8j .. 8j+7 and their rotation partners 64 + 8j .. 64 + 8j + 7
+  float c[16], sn[16], wq[16], wk[16];
+  unpack8(*reinterpret_cast<const uint4*>(cp + 8 * j), c, 0);
+  unpack8(*reinterpret_cast<const uint4*>(cp + 64 + 8 * j), c, 8);
+  unpack8(*reinterpret_cast<const uint4*>(sp + 8 * j), sn, 0);
+  unpack8(*reinterpret_cast<const uint4*>(sp + 64 + 8 * j), sn, 8);
+  const bool norm = a.wq != nullptr;
+  if (norm) {
+    unpack8(*reinterpret_cast<const uint4*>(a.wq + 8 * j), wq, 0);
+    unpack8(*reinterpret_cast<const uint4*>(a.wq + 64 + 8 * j), wq, 8);
+    unpack8(*reinterpret_cast<const uint4*>(a.wk + 8 * j), wk, 0);
+    unpack8(*reinterpret_cast<const uint4*>(a.wk + 64 + 8 * j), wk, 8);
   }
-  const uint32_t clo = *reinterpret_cast<const uint32_t*>(a.cos + (int64_t)t * a.cos_ts + 2 * j);
-  const uint32_t chi = *reinterpret_cast<const uint32_t*>(a.cos + (int64_t)t * a.cos_ts + 64 + 2 * j);
-  const uint32_t slo = *reinterpret_cast<const uint32_t*>(a.sin + (int64_t)t * a.sin_ts + 2 * j);
-  const uint32_t shi = *reinterpret_cast<const uint32_t*>(a.sin + (int64_t)t * a.sin_ts + 64 + 2 * j);
-  const float c[4] = {bf(clo & 0xffffu), bf(clo >> 16), bf(chi & 0xffffu), bf(chi >> 16)};
-  const float sn[4] = {bf(slo & 0xffffu), bf(slo >> 16), bf(shi & 0xffffu), bf(shi >> 16)};
-  // rotate_half: first half takes -x[d + 64], second half x[d - 64]
-  const float rot[4] = {-v[2], -v[3], v[0], v[1]};
-  float o[4];
+  for (int h = slot; h < heads; h += kRowsPerBlock) {
+    uint16_t* x = a.qkv + (int64_t)t * a.qkv_ts + (int64_t)h * kDim;
+    float v[16];
+    unpack8(*reinterpret_cast<const uint4*>(x + 8 * j), v, 0);
+    unpack8(*reinterpret_cast<const uint4*>(x + 64 + 8 * j), v, 8);
+    if (norm) {
+      float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = rbf(rbf(v[i] * c[i]) + rbf(rot[i] * sn[i]));
-  *reinterpret_cast<uint32_t*>(x + 2 * j) = aia::pack_bf16x2(o[0], o[1]);
-  *reinterpret_cast<uint32_t*>(x + 64 + 2 * j) = aia::pack_bf16x2(o[2], o[3]);
+      for (int i = 0; i < 16; ++i) ss += v[i] * v[i];
+#pragma unroll
+      for (int d = 4; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 8);
+      const float r = 1.0f / __builtin_sqrtf(ss * (1.0f / kDim) + a.eps);
+      const bool isq = h < a.hq;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = rbf((v[i] * r) * (isq ? wq[i] : wk[i]));
+    }
+    // rotate_half: first half takes -x[d + 64], second half x[d - 64]
+    float o[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float rot = i < 8 ? -v[i + 8] : v[i - 8];
+      o[i] = rbf(rbf(v[i] * c[i]) + rbf(rot * sn[i]));
+    }
+    uint4 lo, hi;
+    lo.x = aia::pack_bf16x2(o[0], o[1]); lo.y = aia::pack_bf16x2(o[2], o[3]);
+    lo.z = aia::pack_bf16x2(o[4], o[5]); lo.w = aia::pack_bf16x2(o[6], o[7]);
+    hi.x = aia::pack_bf16x2(o[8], o[9]); hi.y = aia::pack_bf16x2(o[10], o[11]);
+    hi.z = aia::pack_bf16x2(o[12], o[13]); hi.w = aia::pack_bf16x2(o[14], o[15]);
+    *reinterpret_cast<uint4*>(x + 8 * j) = lo;
+    *reinterpret_cast<uint4*>(x + 64 + 8 * j) = hi;
+  }
 }
 
 }  // namespace
@@ -94,11 +118,11 @@ extern "C" int aia_qk_norm_rope(void* qkv, int64_t qkv_token_stride, int32_t num
   if (num_tokens == 0) return AIA_OK;
   if (!qkv || !cos || !sin) return fail(AIA_ERR_INVALID, "aia_qk_norm_rope: null pointer argument");
   if (qkv_token_stride < (int64_t)(num_q_heads + 2 * num_kv_heads) * kDim ||
-      qkv_token_stride % 2 || cos_token_stride % 2 || sin_token_stride % 2 ||
-      ((uintptr_t)qkv & 3) || ((uintptr_t)cos & 3) || ((uintptr_t)sin & 3) ||
-      ((uintptr_t)q_norm_weight & 3) || ((uintptr_t)k_norm_weight & 3))
-    return fail(AIA_ERR_INVALID, "aia_qk_norm_rope: tensors must be 4-byte aligned with even "
-                "strides, and a qkv row must hold (Hq + 2 Hkv) x 128 values");
+      qkv_token_stride % 8 || cos_token_stride % 8 || sin_token_stride % 8 ||
+      ((uintptr_t)qkv & 15) || ((uintptr_t)cos & 15) || ((uintptr_t)sin & 15) ||
+      ((uintptr_t)q_norm_weight & 15) || ((uintptr_t)k_norm_weight & 15))
+    return fail(AIA_ERR_INVALID, "aia_qk_norm_rope: tensors must be 16-byte aligned with strides "
+                "a multiple of 8, and a qkv row must hold (Hq + 2 Hkv) x 128 values");
   RopeArgs a;
   a.qkv = static_cast<uint16_t*>(qkv);
   a.qkv_ts = qkv_token_stride;
@@ -109,9 +133,6 @@ extern "C" int aia_qk_norm_rope(void* qkv, int64_t qkv_token_stride, int32_t num
   a.wq = static_cast<const uint16_t*>(q_norm_weight);
   a.wk = static_cast<const uint16_t*>(k_norm_weight);
   a.eps = eps;
-  const int64_t rows = (int64_t)num_tokens * (num_q_heads + num_kv_heads);
-  const int64_t grid = (rows + 7) / 8;
-  if (grid > 0x7fffffff) return fail(AIA_ERR_CAPACITY, "aia_qk_norm_rope: %lld rows", (long long)rows);
-  qk_norm_rope_kernel<<<(unsigned)grid, 256, 0, (hipStream_t)stream>>>(a);
+  qk_norm_rope_kernel<<<(unsigned)num_tokens, 256, 0, (hipStream_t)stream>>>(a);
   return check_hip(hipGetLastError(), "qk_norm_rope launch");
 }

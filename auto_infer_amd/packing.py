@@ -51,6 +51,7 @@ class DeviceRequestTable:
         self._last_use = {}       # rid -> step counter
         self._free = list(range(max_slots - 1, -1, -1))
         self._step = 0
+        self._cap_blocks, self._cap_tokens = max_blocks, max_len
         self.uploaded_block_rows = 0
         self.uploaded_block_elements = 0
 
@@ -71,6 +72,7 @@ class DeviceRequestTable:
             self.token_pool = tp
         if s1 > s0:
             self._free = list(range(s1 - 1, s0 - 1, -1)) + self._free
+        self._cap_blocks, self._cap_tokens = b1, t1
 
     def release(self, rid):
         slot = self._slot.pop(rid, None)
@@ -104,14 +106,20 @@ class DeviceRequestTable:
         """Make slot rows hold ``blocks`` and token ids [0, upto) of the
         request (drafts written right after position upto - 1 - len(drafts)
         + 1, i.e. at the query positions they occupy); returns the slot."""
-        slot = self._slot_for(rid, live)
+        slot = self._slot.get(rid)
+        if slot is None:
+            slot = self._slot_for(rid, live)
+        else:
+            self._last_use[rid] = self._step
         nb = len(blocks)
-        if nb > self.block_pool.shape[1]:
-            self._grow(blocks=max(nb, 2 * self.block_pool.shape[1]))
-        if upto > self.token_pool.shape[1]:
-            self._grow(tokens=max(upto, 2 * self.token_pool.shape[1]))
+        if nb > self._cap_blocks:
+            self._grow(blocks=max(nb, 2 * self._cap_blocks))
+        if upto > self._cap_tokens:
+            self._grow(tokens=max(upto, 2 * self._cap_tokens))
         prev = self._blocks.get(rid)
-        if prev is not None and len(prev) <= nb and tuple(blocks[:len(prev)]) == prev:
+        if prev is not None and len(prev) == nb and prev == blocks:
+            first = nb                                    # steady state: nothing new
+        elif prev is not None and len(prev) <= nb and tuple(blocks[:len(prev)]) == prev:
             first = len(prev)
         else:
             first = 0
@@ -273,33 +281,42 @@ class DeviceBatchPacker:
 
     def build(self, plan, attn_backend=None, kv_caches=None, attn_mask=None):
         bs = self.block_size
-        upd = self.table.begin_step()
-        live = {sr.request_id for sr in plan.scheduled}
+        table = self.table
+        upd = table.begin_step()
+        scheduled = plan.scheduled
+        live = {sr.request_id for sr in scheduled}
         cu, kv = [], []
         sample_idx, decode_splice = {}, []
         all_decode = True
         qacc, width = 0, 0
-        for sr in plan.scheduled:
+        get_request, tables = plan.get_request, plan.block_tables
+        sync, rows = table.sync, upd.rows
+        for sr in scheduled:
             rid = sr.request_id
-            req = plan.get_request(rid)
+            req = get_request(rid)
             n = sr.num_tokens_to_compute
             start = req.num_computed_tokens
-            blocks = plan.block_tables[rid]
-            _check_blocks(rid, blocks, start + n, bs)
-            draft = tuple(getattr(req, "spec_draft", ()) or ())
-            drafts = draft if (draft and not sr.is_prefill) else ()
-            slot = self.table.sync(upd, rid, req, blocks, start + n, live, drafts)
-            upd.row(slot, start, n, len(blocks), 0, qacc, 0, -1)
+            blocks = tables[rid]
+            nb = len(blocks)
+            end = start + n
+            if end > nb * bs:
+                _check_blocks(rid, blocks, end, bs)
+            draft = getattr(req, "spec_draft", ())
+            drafts = tuple(draft) if (draft and not sr.is_prefill) else ()
+            slot = sync(upd, rid, req, blocks, end, live, drafts)
+            rows.append((slot, start, n, nb, 0, qacc, 0, -1))
             npr = req.num_prompt_tokens
-            for li in range(max(npr - start, 0), n):          # positions >= prompt length
-                decode_splice.append((qacc + li, rid))
+            if end > npr:                                      # positions >= prompt length
+                for li in range(max(npr - start, 0), n):
+                    decode_splice.append((qacc + li, rid))
             if start < npr:
                 all_decode = False
             qacc += n
             cu.append(qacc)
-            kv.append(start + n)
+            kv.append(end)
             sample_idx[rid] = qacc - 1
-            width = max(width, len(blocks))
+            if nb > width:
+                width = nb
         T, B = qacc, len(plan.scheduled)
         if T > self._tokens or B > self._seqs or width > self._blocks:
             self._alloc(T * 2 if T > self._tokens else T, B * 2 if B > self._seqs else B,

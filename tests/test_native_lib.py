@@ -46,3 +46,31 @@ def test_workspace_query():
     out = ctypes.c_int64(0)
     _native.call("aia_attn_workspace_bytes", 16, 16, 16, 8, 128, ctypes.byref(out))
     assert out.value > 0
+
+
+def test_argument_validation_of_the_fused_kernels_without_gpu():
+    """Bad arguments are rejected before any device call, with the mapped
+    exception types."""
+    lib = _native.load()
+    vp = ctypes.c_void_p
+    # qk norm + rope: head_dim other than 128 is unsupported
+    rc = lib.aia_qk_norm_rope(vp(16), 1024, 4, 4, 2, 64, vp(16), 64, vp(16), 64, None, None,
+                              ctypes.c_float(1e-6), None)
+    assert rc == _native.AIA_ERR_UNSUPPORTED
+    with pytest.raises(NotImplementedError, match="head_dim"):
+        _native.check(rc, "aia_qk_norm_rope")
+    # norm weights go together
+    rc = lib.aia_qk_norm_rope(vp(16), 1024, 4, 4, 2, 128, vp(16), 128, vp(16), 128, vp(16), None,
+                              ctypes.c_float(1e-6), None)
+    assert rc == _native.AIA_ERR_INVALID and "together" in _native.last_error()
+    # MTP compaction: gear limits
+    for gear in (0, 65):
+        rc = lib.aia_mtp_compact(*([vp(16)] * 4), 8, vp(16), vp(16), vp(16), vp(16), gear, 2, 8,
+                                 vp(16), vp(16), 8, vp(16), vp(16), vp(16), None)
+        assert rc == _native.AIA_ERR_INVALID and "gear" in _native.last_error()
+    # paged GQA: the scale must be positive
+    rc = lib.aia_paged_attention_gqa(vp(16), 2048, 128, vp(16), vp(16), vp(16), 16, vp(16),
+                                     vp(16), 1, 1, 16, 8, 128, 16, 4, ctypes.c_float(0.0),
+                                     vp(16), 2048, 128, None, None, 0, 0, 0, 0, vp(16), 1 << 20,
+                                     None)
+    assert rc == _native.AIA_ERR_INVALID and "scale" in _native.last_error()

@@ -1,11 +1,13 @@
 """Compile the gfx950 HIP sources into the package's C-ABI shared library.
 
 Usage: ``python -m auto_infer_amd.csrc.build`` (or ``build()`` from Python).
-Output: ``auto_infer_amd/_lib/libautoinfer_amd.so``.  Always recompiles.
+Output: ``auto_infer_amd/_lib/libautoinfer_amd.so`` and the packer's host
+extension ``auto_infer_amd/_hostpack*.so``.  Always recompiles.
 """
 import os
 import subprocess
 import sys
+import sysconfig
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
@@ -28,7 +30,23 @@ def hipcc():
     return os.path.join(rocm, "bin", "hipcc")
 
 
+HOSTPACK = os.path.join(PKG, "_hostpack" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_hostpack(verbose=False):
+    """The packer's native host loop (CPython extension, g++)."""
+    tmp = HOSTPACK + ".tmp"
+    cmd = ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall",
+           "-I", sysconfig.get_paths()["include"], os.path.join(HERE, "hostpack.cpp"), "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, HOSTPACK)
+    return HOSTPACK
+
+
 def build(verbose=False):
+    build_hostpack(verbose)
     os.makedirs(OUT_DIR, exist_ok=True)
     srcs = [os.path.join(HERE, s) for s in SOURCES]
     tmp = LIB + ".tmp"

@@ -1,0 +1,310 @@
+// Native host loop of the GPU batch packer (CPython extension _hostpack).
+//
+// DeviceBatchPacker.build (auto_infer_amd/packing.py) walks every scheduled
+// request of a step: look up its device-table slot, compare its block row
+// with what the device table already holds, queue the new block ids / token
+// ids / drafts for upload, and append the request's 8-int row descriptor and
+// its cu_seqlens_q / seqlens_kv / sample_idx / decode_splice entries.  That
+// is the reference's per-request packing loop (auto_infer/worker/
+// model_runner.py:126-166) minus everything the packing kernel does on the
+// device.  In Python it costs 1-2 us per request; this is the same loop over
+// the same Python objects through the CPython API.  The request table's
+// state stays in its Python dicts; the rare paths (a request seen for the
+// first time, pool growth) call back into the table's Python methods, so the
+// two implementations cannot drift apart on them.
+#define PY_SSIZE_T_CLEAN
+#include <Python.h>
+
+namespace {
+
+struct Ref {            // owned reference
+  PyObject* p;
+  explicit Ref(PyObject* o = nullptr) : p(o) {}
+  ~Ref() { Py_XDECREF(p); }
+  Ref(const Ref&) = delete;
+  Ref& operator=(const Ref&) = delete;
+  PyObject* get() const { return p; }
+  PyObject* release() { PyObject* o = p; p = nullptr; return o; }
+  explicit operator bool() const { return p != nullptr; }
+};
+
+long long as_ll(PyObject* o, bool* err) {
+  const long long v = PyLong_AsLongLong(o);
+  if (v == -1 && PyErr_Occurred()) *err = true;
+  return v;
+}
+
+bool append_ll(PyObject* list, long long v) {
+  Ref x(PyLong_FromLongLong(v));
+  return x && PyList_Append(list, x.get()) == 0;
+}
+
+long long attr_ll(PyObject* o, PyObject* name, bool* err) {
+  Ref v(PyObject_GetAttr(o, name));
+  if (!v) { *err = true; return 0; }
+  return as_ll(v.get(), err);
+}
+
+// int attribute of the table that may change when the table grows
+bool table_caps(PyObject* table, PyObject* n_blocks, PyObject* n_tokens, long long* cb,
+                long long* ct) {
+  bool err = false;
+  *cb = attr_ll(table, n_blocks, &err);
+  *ct = attr_ll(table, n_tokens, &err);
+  return !err;
+}
+
+PyObject* build_rows(PyObject*, PyObject* args) {
+  PyObject *table, *scheduled, *get_request, *tables, *upd, *live;
+  long long bs;
+  if (!PyArg_ParseTuple(args, "OOOOLOO", &table, &scheduled, &get_request, &tables, &bs, &upd,
+                        &live))
+    return nullptr;
+  // interned attribute names
+  static PyObject *s_rid, *s_n, *s_prefill, *s_ncomp, *s_ids, *s_nprompt, *s_draft, *s_slot,
+      *s_blocks, *s_ntok, *s_last, *s_step, *s_capb, *s_capt, *s_slot_for, *s_grow, *s_rows,
+      *s_ts, *s_ti, *s_tv, *s_bs_, *s_bi, *s_bv, *s_ubr, *s_ube;
+  if (!s_rid) {
+    s_rid = PyUnicode_InternFromString("request_id");
+    s_n = PyUnicode_InternFromString("num_tokens_to_compute");
+    s_prefill = PyUnicode_InternFromString("is_prefill");
+    s_ncomp = PyUnicode_InternFromString("num_computed_tokens");
+    s_ids = PyUnicode_InternFromString("all_token_ids");
+    s_nprompt = PyUnicode_InternFromString("num_prompt_tokens");
+    s_draft = PyUnicode_InternFromString("spec_draft");
+    s_slot = PyUnicode_InternFromString("_slot");
+    s_blocks = PyUnicode_InternFromString("_blocks");
+    s_ntok = PyUnicode_InternFromString("_ntok");
+    s_last = PyUnicode_InternFromString("_last_use");
+    s_step = PyUnicode_InternFromString("_step");
+    s_capb = PyUnicode_InternFromString("_cap_blocks");
+    s_capt = PyUnicode_InternFromString("_cap_tokens");
+    s_slot_for = PyUnicode_InternFromString("_slot_for");
+    s_grow = PyUnicode_InternFromString("_grow");
+    s_rows = PyUnicode_InternFromString("rows");
+    s_ts = PyUnicode_InternFromString("tok_slot");
+    s_ti = PyUnicode_InternFromString("tok_idx");
+    s_tv = PyUnicode_InternFromString("tok_val");
+    s_bs_ = PyUnicode_InternFromString("blk_slot");
+    s_bi = PyUnicode_InternFromString("blk_idx");
+    s_bv = PyUnicode_InternFromString("blk_val");
+    s_ubr = PyUnicode_InternFromString("uploaded_block_rows");
+    s_ube = PyUnicode_InternFromString("uploaded_block_elements");
+  }
+  Ref slot_d(PyObject_GetAttr(table, s_slot)), blocks_d(PyObject_GetAttr(table, s_blocks)),
+      ntok_d(PyObject_GetAttr(table, s_ntok)), last_d(PyObject_GetAttr(table, s_last)),
+      step_o(PyObject_GetAttr(table, s_step));
+  Ref rows(PyObject_GetAttr(upd, s_rows)), ts(PyObject_GetAttr(upd, s_ts)),
+      ti(PyObject_GetAttr(upd, s_ti)), tv(PyObject_GetAttr(upd, s_tv)),
+      bsl(PyObject_GetAttr(upd, s_bs_)), bi(PyObject_GetAttr(upd, s_bi)),
+      bv(PyObject_GetAttr(upd, s_bv));
+  if (!slot_d || !blocks_d || !ntok_d || !last_d || !step_o || !rows || !ts || !ti || !tv ||
+      !bsl || !bi || !bv)
+    return nullptr;
+  long long capb, capt;
+  if (!table_caps(table, s_capb, s_capt, &capb, &capt)) return nullptr;
+  bool err = false;
+  long long up_rows = attr_ll(table, s_ubr, &err), up_elems = attr_ll(table, s_ube, &err);
+  if (err) return nullptr;
+
+  Ref cu(PyList_New(0)), kv(PyList_New(0)), sample(PyDict_New()), splice(PyList_New(0));
+  if (!cu || !kv || !sample || !splice) return nullptr;
+  Ref seq(PySequence_Fast(scheduled, "scheduled must be a sequence"));
+  if (!seq) return nullptr;
+  const Py_ssize_t count = PySequence_Fast_GET_SIZE(seq.get());
+  PyObject** items = PySequence_Fast_ITEMS(seq.get());
+  long long qacc = 0, width = 0;
+  bool all_decode = true;
+
+  for (Py_ssize_t r = 0; r < count; ++r) {
+    PyObject* sr = items[r];
+    Ref rid(PyObject_GetAttr(sr, s_rid));
+    if (!rid) return nullptr;
+    Ref req(PyObject_CallOneArg(get_request, rid.get()));
+    if (!req) return nullptr;
+    const long long n = attr_ll(sr, s_n, &err);
+    const long long start = attr_ll(req.get(), s_ncomp, &err);
+    if (err) return nullptr;
+    PyObject* blocks = PyObject_GetItem(tables, rid.get());
+    Ref blocks_ref(blocks);
+    if (!blocks) return nullptr;
+    const Py_ssize_t nb = PyObject_Length(blocks);
+    if (nb < 0) return nullptr;
+    const long long end = start + n;
+    if (end > nb * bs) {
+      PyErr_Format(PyExc_ValueError, "request %S: %zd blocks cannot hold position %lld", rid.get(),
+                   nb, end - 1);
+      return nullptr;
+    }
+    // drafts (verify rows of a decode request)
+    Ref drafts;
+    Py_ssize_t ndraft = 0;
+    {
+      Ref draft(PyObject_GetAttr(req.get(), s_draft));
+      if (!draft) { PyErr_Clear(); }
+      else {
+        const int truthy = PyObject_IsTrue(draft.get());
+        if (truthy < 0) return nullptr;
+        Ref pre(PyObject_GetAttr(sr, s_prefill));
+        if (!pre) return nullptr;
+        const int is_pre = PyObject_IsTrue(pre.get());
+        if (is_pre < 0) return nullptr;
+        if (truthy && !is_pre) {
+          drafts.p = PySequence_Tuple(draft.get());
+          if (!drafts) return nullptr;
+          ndraft = PyTuple_GET_SIZE(drafts.get());
+        }
+      }
+    }
+    // ---- table sync (DeviceRequestTable.sync)
+    long long slot;
+    {
+      PyObject* so = PyDict_GetItemWithError(slot_d.get(), rid.get());   // borrowed
+      if (!so && PyErr_Occurred()) return nullptr;
+      if (!so) {
+        Ref s(PyObject_CallMethodObjArgs(table, s_slot_for, rid.get(), live, nullptr));
+        if (!s) return nullptr;
+        slot = as_ll(s.get(), &err);
+        // a new slot may have come with a grown pool
+        if (!table_caps(table, s_capb, s_capt, &capb, &capt)) return nullptr;
+      } else {
+        slot = as_ll(so, &err);
+        if (PyDict_SetItem(last_d.get(), rid.get(), step_o.get()) < 0) return nullptr;
+      }
+      if (err) return nullptr;
+    }
+    if (nb > capb || end > capt) {
+      Ref kw(PyDict_New());
+      if (!kw) return nullptr;
+      if (nb > capb) {
+        Ref v(PyLong_FromLongLong(nb > 2 * capb ? nb : 2 * capb));
+        if (!v || PyDict_SetItemString(kw.get(), "blocks", v.get()) < 0) return nullptr;
+      }
+      if (end > capt) {
+        Ref v(PyLong_FromLongLong(end > 2 * capt ? end : 2 * capt));
+        if (!v || PyDict_SetItemString(kw.get(), "tokens", v.get()) < 0) return nullptr;
+      }
+      Ref grow(PyObject_GetAttr(table, s_grow));
+      Ref empty(PyTuple_New(0));
+      if (!grow || !empty) return nullptr;
+      Ref res(PyObject_Call(grow.get(), empty.get(), kw.get()));
+      if (!res) return nullptr;
+      if (!table_caps(table, s_capb, s_capt, &capb, &capt)) return nullptr;
+    }
+    Py_ssize_t first = 0;
+    PyObject* prev = PyDict_GetItemWithError(blocks_d.get(), rid.get());   // borrowed
+    if (!prev && PyErr_Occurred()) return nullptr;
+    if (prev) {
+      const Py_ssize_t np_ = PyObject_Length(prev);
+      if (np_ < 0) return nullptr;
+      if (np_ == nb) {
+        const int eq = PyObject_RichCompareBool(prev, blocks, Py_EQ);
+        if (eq < 0) return nullptr;
+        if (eq) first = nb;
+        else if (PyTuple_Check(blocks)) first = 0;
+        else {
+          Ref tb(PySequence_Tuple(blocks));
+          if (!tb) return nullptr;
+          const int eq2 = PyObject_RichCompareBool(prev, tb.get(), Py_EQ);
+          if (eq2 < 0) return nullptr;
+          first = eq2 ? nb : 0;
+        }
+      }
+      if (first == 0 && np_ <= nb) {
+        Ref head(PySequence_GetSlice(blocks, 0, np_));
+        if (!head) return nullptr;
+        Ref th(PySequence_Tuple(head.get()));
+        if (!th) return nullptr;
+        const int eq = PyObject_RichCompareBool(th.get(), prev, Py_EQ);
+        if (eq < 0) return nullptr;
+        if (eq) first = np_;
+      }
+    }
+    if (first < nb) {
+      for (Py_ssize_t c = first; c < nb; ++c) {
+        Ref b(PySequence_GetItem(blocks, c));
+        if (!b || PyList_Append(bv.get(), b.get()) < 0) return nullptr;
+        if (!append_ll(bsl.get(), slot) || !append_ll(bi.get(), c)) return nullptr;
+      }
+      up_rows += 1;
+      up_elems += nb - first;
+      Ref tb(PySequence_Tuple(blocks));
+      if (!tb || PyDict_SetItem(blocks_d.get(), rid.get(), tb.get()) < 0) return nullptr;
+    } else if (!prev) {
+      Ref tb(PySequence_Tuple(blocks));
+      if (!tb || PyDict_SetItem(blocks_d.get(), rid.get(), tb.get()) < 0) return nullptr;
+    }
+    {
+      Ref ids(PyObject_GetAttr(req.get(), s_ids));
+      if (!ids) return nullptr;
+      const Py_ssize_t nids = PyObject_Length(ids.get());
+      if (nids < 0) return nullptr;
+      PyObject* ho = PyDict_GetItemWithError(ntok_d.get(), rid.get());
+      if (!ho && PyErr_Occurred()) return nullptr;
+      long long have = ho ? as_ll(ho, &err) : 0;
+      if (err) return nullptr;
+      long long real_hi = end - ndraft;
+      if (real_hi > nids) real_hi = nids;
+      if (real_hi > have) {
+        for (long long p = have; p < real_hi; ++p) {
+          Ref t(PySequence_GetItem(ids.get(), p));
+          if (!t || PyList_Append(tv.get(), t.get()) < 0) return nullptr;
+          if (!append_ll(ts.get(), slot) || !append_ll(ti.get(), p)) return nullptr;
+        }
+        Ref hv(PyLong_FromLongLong(real_hi));
+        if (!hv || PyDict_SetItem(ntok_d.get(), rid.get(), hv.get()) < 0) return nullptr;
+        have = real_hi;
+      }
+      if (ndraft) {
+        const long long base = end - ndraft;
+        for (Py_ssize_t d = 0; d < ndraft; ++d) {
+          if (PyList_Append(tv.get(), PyTuple_GET_ITEM(drafts.get(), d)) < 0) return nullptr;
+          if (!append_ll(ts.get(), slot) || !append_ll(ti.get(), base + d)) return nullptr;
+        }
+        // drafted positions are not real tokens: resync them later
+        Ref hv(PyLong_FromLongLong(have < base ? have : base));
+        if (!hv || PyDict_SetItem(ntok_d.get(), rid.get(), hv.get()) < 0) return nullptr;
+      }
+    }
+    // ---- row descriptor and step lists
+    {
+      Ref row(Py_BuildValue("(LLLnLLii)", slot, start, n, nb, 0LL, qacc, 0, -1));
+      if (!row || PyList_Append(rows.get(), row.get()) < 0) return nullptr;
+    }
+    const long long npr = attr_ll(req.get(), s_nprompt, &err);
+    if (err) return nullptr;
+    if (end > npr) {
+      for (long long li = (npr - start > 0 ? npr - start : 0); li < n; ++li) {
+        Ref e(Py_BuildValue("(LO)", qacc + li, rid.get()));
+        if (!e || PyList_Append(splice.get(), e.get()) < 0) return nullptr;
+      }
+    }
+    if (start < npr) all_decode = false;
+    qacc += n;
+    if (!append_ll(cu.get(), qacc) || !append_ll(kv.get(), end)) return nullptr;
+    Ref last(PyLong_FromLongLong(qacc - 1));
+    if (!last || PyDict_SetItem(sample.get(), rid.get(), last.get()) < 0) return nullptr;
+    if (nb > width) width = nb;
+  }
+  {
+    Ref a(PyLong_FromLongLong(up_rows)), b(PyLong_FromLongLong(up_elems));
+    if (!a || !b || PyObject_SetAttr(table, s_ubr, a.get()) < 0 ||
+        PyObject_SetAttr(table, s_ube, b.get()) < 0)
+      return nullptr;
+  }
+  return Py_BuildValue("(NNNNOLL)", cu.release(), kv.release(), sample.release(), splice.release(),
+                       all_decode ? Py_True : Py_False, qacc, width);
+}
+
+PyMethodDef methods[] = {
+    {"build_rows", build_rows, METH_VARARGS,
+     "build_rows(table, scheduled, get_request, block_tables, block_size, updates, live) -> "
+     "(cu_seqlens_q, seqlens_kv, sample_idx, decode_splice, all_decode, tokens, width)"},
+    {nullptr, nullptr, 0, nullptr}};
+
+PyModuleDef module = {PyModuleDef_HEAD_INIT, "_hostpack",
+                      "Native per-request loop of DeviceBatchPacker.build.", -1, methods};
+
+}  // namespace
+
+PyMODINIT_FUNC PyInit__hostpack(void) { return PyModule_Create(&module); }

@@ -26,6 +26,11 @@ import torch
 
 from auto_infer_amd import _native
 from auto_infer_amd.attention.base import ForwardContext
+
+try:        # native per-request host loop (auto_infer_amd/csrc/hostpack.cpp)
+    from auto_infer_amd import _hostpack
+except ImportError:
+    _hostpack = None
 from auto_infer_amd.ops import _check_device_tensor, _ptr, _stream
 
 _ROW_INTS = 8
@@ -247,6 +252,47 @@ def _check_blocks(rid, blocks, end, block_size):
         raise ValueError(f"request {rid}: {len(blocks)} blocks cannot hold position {end - 1}")
 
 
+def build_rows_py(table, scheduled, get_request, tables, bs, upd, live):
+    """Per-request loop of ``DeviceBatchPacker.build`` (the reference's
+    model_runner.py:126-166 minus the device work): sync each request into
+    the device table, queue its row descriptor, and collect cu_seqlens_q,
+    seqlens_kv, sample_idx and decode_splice.  The native extension
+    ``_hostpack.build_rows`` runs the same loop; this is its specification.
+    Returns (cu, kv, sample_idx, decode_splice, all_decode, tokens, width)."""
+    cu, kv = [], []
+    sample_idx, decode_splice = {}, []
+    all_decode = True
+    qacc, width = 0, 0
+    sync, rows = table.sync, upd.rows
+    for sr in scheduled:
+        rid = sr.request_id
+        req = get_request(rid)
+        n = sr.num_tokens_to_compute
+        start = req.num_computed_tokens
+        blocks = tables[rid]
+        nb = len(blocks)
+        end = start + n
+        if end > nb * bs:
+            _check_blocks(rid, blocks, end, bs)
+        draft = getattr(req, "spec_draft", ())
+        drafts = tuple(draft) if (draft and not sr.is_prefill) else ()
+        slot = sync(upd, rid, req, blocks, end, live, drafts)
+        rows.append((slot, start, n, nb, 0, qacc, 0, -1))
+        npr = req.num_prompt_tokens
+        if end > npr:                                      # positions >= prompt length
+            for li in range(max(npr - start, 0), n):
+                decode_splice.append((qacc + li, rid))
+        if start < npr:
+            all_decode = False
+        qacc += n
+        cu.append(qacc)
+        kv.append(end)
+        sample_idx[rid] = qacc - 1
+        if nb > width:
+            width = nb
+    return cu, kv, sample_idx, decode_splice, all_decode, qacc, width
+
+
 class DeviceBatchPacker:
     """GPU version of the eager runner's per-step packing (``_build``,
     model_runner.py:111-188): persistent grow-only device buffers, one
@@ -285,38 +331,9 @@ class DeviceBatchPacker:
         upd = table.begin_step()
         scheduled = plan.scheduled
         live = {sr.request_id for sr in scheduled}
-        cu, kv = [], []
-        sample_idx, decode_splice = {}, []
-        all_decode = True
-        qacc, width = 0, 0
-        get_request, tables = plan.get_request, plan.block_tables
-        sync, rows = table.sync, upd.rows
-        for sr in scheduled:
-            rid = sr.request_id
-            req = get_request(rid)
-            n = sr.num_tokens_to_compute
-            start = req.num_computed_tokens
-            blocks = tables[rid]
-            nb = len(blocks)
-            end = start + n
-            if end > nb * bs:
-                _check_blocks(rid, blocks, end, bs)
-            draft = getattr(req, "spec_draft", ())
-            drafts = tuple(draft) if (draft and not sr.is_prefill) else ()
-            slot = sync(upd, rid, req, blocks, end, live, drafts)
-            rows.append((slot, start, n, nb, 0, qacc, 0, -1))
-            npr = req.num_prompt_tokens
-            if end > npr:                                      # positions >= prompt length
-                for li in range(max(npr - start, 0), n):
-                    decode_splice.append((qacc + li, rid))
-            if start < npr:
-                all_decode = False
-            qacc += n
-            cu.append(qacc)
-            kv.append(end)
-            sample_idx[rid] = qacc - 1
-            if nb > width:
-                width = nb
+        rows_fn = _hostpack.build_rows if _hostpack is not None else build_rows_py
+        cu, kv, sample_idx, decode_splice, all_decode, qacc, width = rows_fn(
+            table, scheduled, plan.get_request, plan.block_tables, bs, upd, live)
         T, B = qacc, len(plan.scheduled)
         if T > self._tokens or B > self._seqs or width > self._blocks:
             self._alloc(T * 2 if T > self._tokens else T, B * 2 if B > self._seqs else B,

@@ -191,3 +191,38 @@ def test_fused_kv_write(lqs, lks, hq, hkv, bs, waves):
     err = (out.float().cpu() - exp).abs().max().item()
     print(f"max-abs err {err:.3e}", flush=True)
     assert err <= TOL
+
+
+def test_two_host_threads_on_two_streams():
+    """The boundary is reentrant (no mutable global state; errors are
+    thread-local): two host threads, each with its own stream and plan,
+    call the attention concurrently and both match the oracle."""
+    import threading
+    steps = [workloads.make_gqa_step(lqs=[1, 3, 1], lks=[500, 90, 1500], num_q_heads=16,
+                                     num_kv_heads=8, block_size=128, seed=s) for s in (51, 52)]
+    exp = [oracle(st) for st in steps]
+    got, errors = [None, None], []
+
+    def worker(i):
+        try:
+            st = steps[i]
+            stream = torch.cuda.Stream()
+            with torch.cuda.stream(stream):
+                q, kc, vc = st.q.to(DEV), st.k_cache.to(DEV), st.v_cache.to(DEV)
+                plan = ops.AttentionPlan.from_lists(st.block_table.to(DEV), st.cu_seqlens_q,
+                                                    st.seqlens_kv, 16, 8, 128, 128)
+                for _ in range(20):
+                    out = ops.paged_attention_gqa(q, kc, vc, plan, st.scale)
+                stream.synchronize()
+                got[i] = out.float().cpu()
+        except Exception as e:          # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for g, e in zip(got, exp):
+        assert (g - e).abs().max().item() <= TOL

@@ -1370,6 +1370,7 @@ extern "C" int aia_paged_attention_gqa(
   if (block_size <= 0 || num_blocks <= 0)
     return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: block_size %d / num_blocks %d",
                 block_size, num_blocks);
+  if (num_tokens == 0 || batch == 0) return AIA_OK;    // empty step (zero-size tensors)
   if (!query || !key_cache || !value_cache || !block_table || !out || !workspace)
     return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: null pointer argument");
   if (q_token_stride % 8 || q_head_stride % 8 || out_token_stride % 4 || out_head_stride % 8 ||
@@ -1383,7 +1384,6 @@ extern "C" int aia_paged_attention_gqa(
                   ((uintptr_t)key_new & 15) || ((uintptr_t)value_new & 15)))
     return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: new K/V rows must be 16-byte aligned "
                 "with token strides a multiple of 8 elements");
-  if (num_tokens == 0 || batch == 0) return AIA_OK;
   const Geometry g = geometry(num_q_heads, num_kv_heads, batch, num_tokens, head_dim);
   const int32_t waves = resolve_waves(num_waves, g, head_dim);
   const Layout L = layout(batch, num_tokens, g, head_dim, waves);
@@ -1450,13 +1450,13 @@ extern "C" int aia_paged_attention_mla(
   if (block_size <= 0 || num_blocks <= 0)
     return fail(AIA_ERR_INVALID, "aia_paged_attention_mla: block_size %d / num_blocks %d",
                 block_size, num_blocks);
+  if (num_tokens == 0 || batch == 0) return AIA_OK;    // empty step (zero-size tensors)
   if (!q_latent || !latent_cache || !block_table || !out || !workspace)
     return fail(AIA_ERR_INVALID, "aia_paged_attention_mla: null pointer argument");
   if (q_token_stride % 8 || q_head_stride % 8 || out_token_stride % 8 || out_head_stride % 8 ||
       ((uintptr_t)q_latent & 15) || ((uintptr_t)latent_cache & 15) || ((uintptr_t)out & 15))
     return fail(AIA_ERR_INVALID, "aia_paged_attention_mla: tensors must be 16-byte aligned with "
                 "strides a multiple of 8 elements");
-  if (num_tokens == 0 || batch == 0) return AIA_OK;
   const Geometry g = geometry(num_heads, 1, batch, num_tokens, kMlaV);
   const int32_t waves = resolve_waves(num_waves, g, kMlaV);
   const Layout L = layout(batch, num_tokens, g, kMlaV, waves);

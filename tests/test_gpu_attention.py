@@ -226,3 +226,57 @@ def test_two_host_threads_on_two_streams():
     assert not errors, errors
     for g, e in zip(got, exp):
         assert (g - e).abs().max().item() <= TOL
+
+
+def _fast_decode_step(B, hq, hkv, bs, lks, seed):
+    """A decode step built without per-request Python loops (large batches):
+    consecutive blocks per request, random bf16 Q and caches."""
+    g = torch.Generator().manual_seed(seed)
+    lks = np.asarray(lks)
+    nblk = (lks + bs - 1) // bs
+    first = np.concatenate([[0], np.cumsum(nblk)[:-1]])
+    width = int(nblk.max())
+    cols = np.arange(width)[None, :]
+    bt = np.where(cols < nblk[:, None], first[:, None] + cols, 0).astype(np.int32)
+    NB = int(nblk.sum())
+    s = workloads.GqaStep(
+        q=(torch.randn(B, hq, 128, generator=g) * 0.5).bfloat16(),
+        k_new=None, v_new=None,
+        k_cache=torch.randn(NB, bs, hkv, 128, generator=g).bfloat16(),
+        v_cache=torch.randn(NB, bs, hkv, 128, generator=g).bfloat16(),
+        block_table=torch.from_numpy(bt), cu_seqlens_q=list(range(1, B + 1)),
+        seqlens_kv=lks.tolist(), slot_mapping=None, scale=128 ** -0.5)
+    return s
+
+
+@pytest.mark.parametrize("B,hq,hkv", [(5000, 8, 8), (8192, 16, 16)])
+def test_planner_large_batch_paths(B, hq, hkv):
+    """Batches past the planner's LDS copy of the request metadata (> 4095
+    requests) and past its register copy of the segment tile counts (> 8192
+    segments: 8192 requests x 2 kv-head groups)."""
+    lks = [1 + (i * 7) % 40 for i in range(B)]
+    check(_fast_decode_step(B, hq, hkv, 16, lks, seed=B))
+
+
+def test_planner_rejects_batches_past_its_limit():
+    st = _fast_decode_step(8193, 8, 8, 16, [1] * 8193, seed=1)
+    with pytest.raises(ValueError, match="exceeds planner limit"):
+        ops.AttentionPlan.from_lists(st.block_table.to(DEV), st.cu_seqlens_q, st.seqlens_kv,
+                                     8, 8, 128, 16)
+
+
+@pytest.mark.parametrize("lq", [1, 3])
+def test_very_long_context(lq):
+    """131072 keys: many 64-block windows of block ids per range."""
+    check(workloads.make_gqa_step(lqs=[lq], lks=[131072], num_q_heads=4, num_kv_heads=1,
+                                  block_size=128, seed=4), 0)
+
+
+def test_empty_step():
+    """No query tokens: nothing is launched and the output is empty."""
+    plan = ops.AttentionPlan.from_lists(torch.zeros(0, 1, dtype=torch.int32, device=DEV), [],
+                                        [], 16, 8, 128, 16)
+    q = torch.zeros(0, 16, 128, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(4, 16, 8, 128, dtype=torch.bfloat16, device=DEV)
+    out = ops.paged_attention_gqa(q, kc, kc, plan, 128 ** -0.5)
+    assert out.shape == (0, 16, 128)

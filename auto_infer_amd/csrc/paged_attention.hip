@@ -696,8 +696,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
 #pragma unroll
       for (int v = 0; v < 4; ++v) sv[v] = (!masked || tb + v <= lim[r]) ? acc[r][v] : -INFINITY;
       float tmax = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      tmax = aia::group4_max(tmax);
       const float mnew = fmaxf(m[r], tmax * a.scale_log2);
       float p[4];
 #pragma unroll
@@ -756,8 +755,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
 
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
-    lsum[r] += __shfl_xor(lsum[r], 16);
-    lsum[r] += __shfl_xor(lsum[r], 32);
+    lsum[r] = aia::group4_sum(lsum[r]);
   }
   const int first_wave = tile_begin / tpw;
   const int nparts = (tile_end - 1) / tpw - first_wave + 1;
@@ -1166,8 +1164,7 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
 #pragma unroll
     for (int v = 0; v < 4; ++v) sv[v] = (tb + v <= lim) ? tot[v] * a.scale_log2 : -INFINITY;
     float tmax = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    tmax = aia::group4_max(tmax);
     const float mnew = fmaxf(m, tmax);
     const float alpha = __builtin_amdgcn_exp2f(m - mnew);
     float p[4];
@@ -1209,8 +1206,7 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
     w0 = w1;
   }
 
-  lsum += __shfl_xor(lsum, 16);
-  lsum += __shfl_xor(lsum, 32);
+  lsum = aia::group4_sum(lsum);
   const int first_wave = tile_begin / tpw;
   const int nparts = (tile_end - 1) / tpw - first_wave + 1;
   const int d0 = 128 * wid;

@@ -30,6 +30,7 @@ import torch  # noqa: E402
 
 METRIC = "paged decode attn HBM GB/s (% of 8 TB/s peak), tok/s at bs=16; packing µs/step"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA peak of MI355X
 
 
 def parse():
@@ -146,7 +147,8 @@ def other_configs(stream, only=None):
     """Attention (+ merge) time of BASELINE configs 2-5 at full size, each
     with enough rotating caches to exceed the Infinity Cache, and the fused
     kernels either side of the path.  `only` selects one entry (its key:
-    configs[1] .. configs[4], pre_attention, mtp_compaction)."""
+    configs[1] .. configs[4], configs[1]_prefill, configs[1]_decode,
+    pre_attention, mtp_compaction)."""
     import time as _time
     import numpy as np
     from auto_infer_amd import ops, packing, workloads
@@ -171,11 +173,23 @@ def other_configs(stream, only=None):
                                                            vcs[i % pools], plan, step.scale,
                                                            out=out), stream, 5, 2 * pools)
         by = step.kv_bytes_read() + 2 * out.numel() * 2
+        # QK^T and PV flops over the visible (causal) keys of every query row
+        starts = [0] + list(step.cu_seqlens_q[:-1])
+        vis = sum(lq * (lk - lq) + lq * (lq + 1) // 2 for lq, lk in
+                  ((e - b, k) for b, e, k in zip(starts, step.cu_seqlens_q, step.seqlens_kv)))
+        fl = 4.0 * hq * d * vis
         res[name] = {"attn_us": round(us, 2), "kv_MB": round(step.kv_bytes_read() / 1e6, 1),
                      "GBps": round(by / us / 1e3, 1),
                      "frac_of_peak": round(by / us / 1e3 / HBM_PEAK_GBS, 4),
+                     "TFLOPs": round(fl / us / 1e6, 1),
+                     "frac_of_bf16_mfma_peak": round(fl / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
                      "tok_per_s": round(len(step.seqlens_kv) / (us * 1e-6), 1)}
         del kcs, vcs
+
+    def on_device(step):
+        for n in ("q", "k_new", "v_new", "k_cache", "v_cache", "block_table"):
+            setattr(step, n, getattr(step, n).to(dev))
+        return step
 
     def note(msg):
         print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -183,6 +197,18 @@ def other_configs(stream, only=None):
     if want("configs[1]"):
         note("configs[1] mixed prefill + decode")
         gqa("configs[1]_mixed_prefill_decode", workloads.config2_mixed(seed=0, device=dev), 1)
+    if want("configs[1]_prefill") or want("configs[1]_decode"):
+        # the two halves of configs[1] alone: its three 512-token prefill
+        # chunks (the dense QK^T / PV contraction) and its 512 decode rows
+        full = workloads.config2_mixed(seed=0, device=dev)
+        if want("configs[1]_prefill"):
+            note("configs[1] prefill chunks alone")
+            gqa("configs[1]_prefill_only", on_device(workloads.subset(full, [0, 1, 2])[0]), 1)
+        if want("configs[1]_decode"):
+            note("configs[1] decode rows alone")
+            gqa("configs[1]_decode_only",
+                on_device(workloads.subset(full, list(range(3, 515)))[0]), 1)
+        del full
     if want("configs[3]"):
         note("configs[3] MTP verify")
         gqa("configs[3]_mtp_verify", workloads.config4_mtp(seed=0, device=dev), 3)

@@ -19,6 +19,8 @@
 //   gqa_merge     log-sum-exp merge of the partials of each split segment.
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -50,8 +52,29 @@ constexpr int kMaxGroupWaves = 8;  // kv heads (waves) per work-group
 // the group over the same keys, so every tile reads whole contiguous
 // (block_size x Hkv x D) cache slots.
 struct Geometry {
-  int32_t hkv, group, hb, nhb, qb, nw, nkvg, rb, qs;
+  int32_t hkv, group, hb, nhb, qb, nw, nkvg, rb, qs, pf;
 };
+
+// Prefill routing: a GQA request whose query rows (query tokens x group
+// heads) fill at least one prefill work item is planned for the prefill
+// kernel (all its rows' keys staged once per 128 rows in LDS) instead of
+// split-K segments.  AIA_PREFILL=0 builds the split-K-only planner.
+#ifndef AIA_PREFILL
+#define AIA_PREFILL 1
+#endif
+#ifndef AIA_PF_WAVES
+#define AIA_PF_WAVES 4
+#endif
+#ifndef AIA_PF_KEYS
+#define AIA_PF_KEYS 64
+#endif
+#ifndef AIA_PF_RT
+#define AIA_PF_RT 2
+#endif
+constexpr int kPfWaves = AIA_PF_WAVES;       // waves per prefill work-group
+constexpr int kPfRt = AIA_PF_RT;             // 16-row MFMA tiles per wave
+constexpr int kPfRows = 16 * kPfRt * kPfWaves;   // rows per prefill work item
+constexpr int kPfKeys = AIA_PF_KEYS;         // keys per staged K/V tile (32 or 64)
 
 // rb: row blocks (of 16 query rows) per segment.  Two when a GQA launch's
 // requests average more query tokens than one block holds (prefill chunks),
@@ -67,15 +90,23 @@ Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_
   g.qb = kRows / g.hb;                                  // query tokens per segment
   g.nw = hkv < kMaxGroupWaves ? hkv : kMaxGroupWaves;   // waves per work-group
   g.nkvg = (hkv + g.nw - 1) / g.nw;                     // kv-head groups
-  g.rb = (dv == kHeadDim && tokens > (int64_t)batch * g.qb) ? 2 : 1;
+  // Prefill routing is possible when some request can hold a full item of
+  // rows: with at least one query token per request, none holds more than
+  // tokens - batch + 1.  (The planner routes nothing when this says no, so a
+  // batch that breaks the assumption still runs, on split-K.)
+  g.pf = (AIA_PREFILL && dv == kHeadDim && batch > 0 &&
+          ((int64_t)tokens - batch + 1) * g.group >= kPfRows) ? 1 : 0;
+  // with prefill routing, requests with many query rows leave the split-K
+  // kernel, whose segments are then decode / short-verify sized
+  g.rb = (!g.pf && dv == kHeadDim && tokens > (int64_t)batch * g.qb) ? 2 : 1;
   g.qs = g.qb * g.rb;                                   // query tokens per segment
   return g;
 }
 
 // Workspace layout (all offsets 256-byte aligned).
 struct Layout {
-  int64_t hdr, seg, wave, part_ml, part_o, cnt, req, mrg, total;
-  int64_t seg_cap, part_cap, mrg_cap;
+  int64_t hdr, seg, wave, part_ml, part_o, cnt, req, mrg, pf, total;
+  int64_t seg_cap, part_cap, mrg_cap, pf_cap;
 };
 
 constexpr int kMergeDims = 16;   // output dims per merge element
@@ -102,6 +133,12 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
   L.mrg = off;      off = align256(off + L.mrg_cap * kMrgInts * 4);
   L.cnt = off;      off = align256(off + L.seg_cap * g.nw * 4);
   L.req = off;      off = align256(off + ((int64_t)batch + 1) * 4);
+  // prefill items: a routed request has >= kPfRows rows, so at most
+  // rows / kPfRows of them, each adding at most one partial item
+  const int64_t pf_rows = g.pf ? (int64_t)tokens * g.group : 0;
+  const int64_t pf_reqs = pf_rows / kPfRows < batch ? pf_rows / kPfRows : batch;
+  L.pf_cap = (pf_rows + kPfRows - 1) / kPfRows + pf_reqs;
+  L.pf = off;       off = align256(off + L.pf_cap * 8);
   L.total = off;
   return L;
 }
@@ -197,7 +234,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     int32_t batch, Geometry g, int32_t waves, int32_t dv,
     int32_t* __restrict__ hdr, int32_t* __restrict__ seg, int32_t* __restrict__ wave_rec,
     int32_t* __restrict__ counters, int32_t* __restrict__ req_scratch,
-    int32_t* __restrict__ mrg) {
+    int32_t* __restrict__ mrg, int2* __restrict__ pf_items, int32_t pf_cap, int32_t seg_cap) {
   __shared__ int lds[kPlanLds];
   __shared__ int wave_sums[kPlanThreads / 64];
   __shared__ int2 wave_sums2[kPlanThreads / 64];
@@ -209,11 +246,13 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   int* cuv = req_lds ? lds + (batch + 1) : nullptr;
   int* kvv = req_lds ? lds + 2 * (batch + 1) : nullptr;
 
-  // 1) segments per request -> request offsets
-  int carry = 0;
+  // 1) segments per request -> request offsets; prefill-routed requests
+  // get no segments and list their prefill items instead (last rows first:
+  // under the causal mask they see the most keys)
+  int carry = 0, pcarry = 0;
   for (int base = 0; base < batch; base += kPlanThreads) {
     const int b = base + tid;
-    int cnt = 0;
+    int cnt = 0, pcnt = 0;
     if (b < batch) {
       const int c0 = cu_q[b], c1 = cu_q[b + 1], lk = kvlen[b];
       if (req_lds) {
@@ -221,13 +260,25 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
         if (b == batch - 1) cuv[batch] = c1;
       }
       const int lq = c1 - c0;
-      cnt = lq > 0 ? ((lq + g.qs - 1) / g.qs) * per_req : 0;
+      if (g.pf && (int64_t)lq * g.group >= kPfRows)
+        pcnt = (lq * g.group + kPfRows - 1) / kPfRows;
+      else
+        cnt = lq > 0 ? ((lq + g.qs - 1) / g.qs) * per_req : 0;
     }
-    int tot;
-    const int ex = block_exclusive_scan(cnt, wave_sums, &tot);
-    if (b < batch) req_off[b] = carry + ex;
-    carry += tot;
+    int2 tot2;
+    const int2 ex2 = block_exclusive_scan2(make_int2(cnt, pcnt), wave_sums2, &tot2);
+    if (b < batch) req_off[b] = carry + ex2.x;
+    // (the capacity holds whenever cu_seqlens_q ends at the step's token
+    // count; metadata that does not is cut off here, never written past)
+    for (int i = 0; i < pcnt && pcarry + ex2.y + i < pf_cap; ++i)
+      pf_items[pcarry + ex2.y + i] = make_int2(b, (pcnt - 1 - i) * kPfRows);
+    carry += tot2.x;
+    pcarry += tot2.y;
   }
+  // Query lengths that do not sum to the step's token count can ask for
+  // more work than the workspace was sized for: plan nothing rather than
+  // write past it.
+  if (carry > seg_cap || pcarry > pf_cap) { carry = 0; pcarry = 0; }
   if (tid == 0) req_off[batch] = carry;
   __syncthreads();
   const int nseg = req_off[batch];
@@ -414,7 +465,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   }
   if (tid == 0) {
     hdr[0] = nseg; hdr[1] = total_tiles; hdr[2] = tpw; hdr[3] = carry; hdr[4] = waves;
-    hdr[5] = mcarry;
+    hdr[5] = mcarry; hdr[6] = min(pcarry, pf_cap);
     // sentinel record so readers may look one past the end
     int* r = seg + (int64_t)nseg * 8;
     r[0] = 0; r[1] = 0; r[2] = 0; r[3] = 0; r[4] = 0;
@@ -546,9 +597,10 @@ __device__ __forceinline__ void stage_v(uint16_t* vs, int n, int g, const uint4 
 #pragma unroll
   for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(vs + n * kVStride + 32 * j + 8 * g) = as_u4(vv[j]);
 }
+template <int STRIDE = kVStride>
 __device__ __forceinline__ short4_t vt_frag(const uint16_t* vs, int n, int g, int dt) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_short4_t*)(vs + (4 * g + (n >> 2)) * kVStride + 16 * dt + 4 * (n & 3)));
+      (lds_short4_t*)(vs + (4 * g + (n >> 2)) * STRIDE + 16 * dt + 4 * (n & 3)));
 }
 
 // Tiles kept in flight per GQA wave (registers: 32 VGPRs per tile).  One is
@@ -941,6 +993,378 @@ void gqa_attn_kernel(AttnArgs a) {
     const int* r = a.seg + (int64_t)s * 8;
 #pragma unroll
     for (int i = 0; i < 8; ++i) rec[i] = r[i];
+  }
+}
+
+// ---------------------------------------------------------------- prefill
+
+struct PrefillArgs {
+  const uint16_t* q;
+  int64_t q_ts, q_hs;
+  uint16_t* kc;
+  uint16_t* vc;
+  const uint16_t* kn;
+  const uint16_t* vn;
+  int64_t kn_ts, vn_ts;
+  const int32_t* bt;
+  int64_t bt_stride;
+  const int32_t* cu_q;
+  const int32_t* kvlen;
+  int32_t hkv, group, bs, nb, batch, tokens;
+  float scale_log2;
+  uint16_t* out;
+  int64_t o_ts, o_hs;
+  const int2* items;
+  const int32_t* hdr;
+};
+
+// LDS row strides (elements) of the staged K and V tiles: 272 bytes puts the
+// 16 keys of a K fragment read in distinct banks; V keeps the transposing
+// read's 288 bytes.  (Measured on the configs[1] prefill chunks: 288-byte K
+// rows are as fast, unpadded 256-byte rows 25% slower, 264-byte rows 75%.)
+constexpr int kKStride = 136;
+constexpr int kPfVStride = kVStride;
+constexpr int kPfDtBatch = 4;      // V^T fragments read ahead of their MFMAs
+// Wave priority raised around each MFMA block, so a wave entering its MFMA
+// phase issues ahead of the co-resident wave, which runs its softmax VALU
+// meanwhile (measured about 3% faster on the configs[1] prefill chunks).
+#ifndef AIA_PF_PRIO
+#define AIA_PF_PRIO 1
+#endif
+#ifndef AIA_PF_LAZY
+#define AIA_PF_LAZY 8.0f
+#endif
+constexpr float kLazyLog2 = AIA_PF_LAZY;              // max growth (log2) before a rescale
+
+// Prefill attention: one work-group per (prefill item, kv head).  An item is
+// kPfRows consecutive rows of one request's (query token, group head) row
+// list, row = token * group + head-in-group; each of the 4 waves owns 32
+// rows (two 16-row MFMA tiles).  The work-group walks the keys its rows can
+// see in tiles of 64: every K/V tile is loaded once (registers, then one of
+// two LDS buffers, one barrier per tile) and used by all 128 rows.
+//   S^T = K Q^T   v_mfma_f32_16x16x32_bf16, K fragments ds_read_b128 from LDS
+//                 (lane (key n, group g) reads dims 32 j + 8 g of key n), Q^T
+//                 fragments held in registers for the whole item;
+//   O^T += V^T P^T  v_mfma_f32_16x16x32_bf16 over 32 keys taken from two
+//                 16-key sub-tiles s0, s1: operand position 8 g + i holds key
+//                 16 s0 + 4 g + i (i < 4) or 16 s1 + 4 g + i - 4, which is
+//                 exactly where the S^T accumulators of s0 and s1 leave P,
+//                 and V^T comes from two transposing LDS reads.
+// Online softmax per row with the scale inside exp2; masks only in tiles
+// that reach past a wave's smallest row limit.  Outputs bf16 directly (a
+// work-group covers all keys of its rows).  With new K/V rows, keys at this
+// step's new positions are read from them, and the work-group writes the new
+// rows of the tokens whose first row it holds into the cache.
+#ifndef AIA_PF_WPE
+#define AIA_PF_WPE 2
+#endif
+template <bool ONE_BLOCK, bool FUSED>
+__global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(AIA_PF_WPE, AIA_PF_WPE)))
+void gqa_prefill_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kPfKeys * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[2][kPfKeys * kPfVStride];
+  // Work-group b takes (kv head, item) pair xcd_range(b, pairs), kv-head
+  // major: each XCD gets a contiguous run of pairs, so the items that re-read
+  // one request's keys for one kv head share an XCD's L2.
+  const int count = a.hdr[6];
+  const int pairs = count * a.hkv;
+  if ((int)blockIdx.x >= pairs) return;
+  const int pair = xcd_range(blockIdx.x, pairs);
+  const int kvh = pair / count, item = pair - kvh * count;
+  const int2 it = a.items[item];
+  const int b = it.x, row0 = it.y;
+  if (b < 0 || b >= a.batch || kvh >= a.hkv) return;
+  const int q_begin = a.cu_q[b], lq = a.cu_q[b + 1] - q_begin, lk = a.kvlen[b];
+  const int G = a.group;
+  const int nrows = lq * G;
+  if (row0 < 0 || row0 >= nrows || q_begin < 0 || q_begin + lq > a.tokens) return;
+  const int ctx0 = lk - lq;                       // position of the first query token
+  const int row_end = min(nrows, row0 + kPfRows);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int row_elems = a.hkv * kHeadDim;
+  const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
+
+  // new K/V rows of the tokens whose first row lies in this item
+  if (FUSED) {
+    const int t_lo = (row0 + G - 1) / G, t_hi = min(lq, (row_end - 1) / G + 1);
+    for (int e = tid; e < (t_hi - t_lo) * 16; e += kPfWaves * 64) {
+      const int t = t_lo + (e >> 4), c = e & 15;
+      const int p = ctx0 + t;
+      if (p < 0) continue;
+      const int blk = min(max(btrow[p / a.bs], 0), a.nb - 1);
+      const int64_t dst = ((int64_t)blk * a.bs + p % a.bs) * row_elems + (int64_t)kvh * kHeadDim;
+      const int64_t tok = q_begin + t;
+      reinterpret_cast<uint4*>(a.kc + dst)[c] =
+          reinterpret_cast<const uint4*>(a.kn + tok * a.kn_ts + (int64_t)kvh * kHeadDim)[c];
+      reinterpret_cast<uint4*>(a.vc + dst)[c] =
+          reinterpret_cast<const uint4*>(a.vn + tok * a.vn_ts + (int64_t)kvh * kHeadDim)[c];
+    }
+  }
+
+  // this wave's rows
+  int lim[kPfRt], tokr[kPfRt], headr[kPfRt];
+  bool rv[kPfRt];
+  int wlim_lo = 0x7fffffff, wlim_hi = -1;
+#pragma unroll
+  for (int rt = 0; rt < kPfRt; ++rt) {
+    const int row = row0 + (wid * kPfRt + rt) * kRows + n;
+    rv[rt] = row < row_end;
+    tokr[rt] = row / G;
+    headr[rt] = kvh * G + (row - tokr[rt] * G);
+    lim[rt] = rv[rt] ? min(ctx0 + tokr[rt], lk - 1) : -1;
+    if (rv[rt]) { wlim_lo = min(wlim_lo, lim[rt]); wlim_hi = max(wlim_hi, lim[rt]); }
+  }
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    wlim_lo = min(wlim_lo, __shfl_xor(wlim_lo, d));
+    wlim_hi = max(wlim_hi, __shfl_xor(wlim_hi, d));
+  }
+  uint4 qf[kPfRt][4];
+#pragma unroll
+  for (int rt = 0; rt < kPfRt; ++rt) {
+    if (rv[rt]) {
+      const uint4* qp = reinterpret_cast<const uint4*>(
+          a.q + (int64_t)(q_begin + tokr[rt]) * a.q_ts + (int64_t)headr[rt] * a.q_hs);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qf[rt][j] = qp[4 * j + g];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qf[rt][j] = make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // keys the work-group's last row sees
+  const int kend = max(0, min(lk, ctx0 + (row_end - 1) / G + 1));
+  const int ntiles = (kend + kPfKeys - 1) / kPfKeys;
+
+  // loader: thread tid moves 16-byte chunk (tid % 16) of keys kLdKeys i + tid / 16.
+  // Block ids are fetched one tile ahead (their loads are in flight during a
+  // tile's math), so a tile's K/V loads never wait on a table lookup.  When
+  // the block size is a multiple of the tile, a tile lies in one block: its
+  // id is one scalar load and a key's address one multiply-add.  Keys past
+  // the last visible one re-read it (never a slot that may hold stale
+  // bytes); keys at this step's new positions come from the new rows.
+  const int lkey = tid >> 4, lc = tid & 15;
+  const int64_t kvoff = (int64_t)kvh * kHeadDim;
+  const uint16_t* kcb = a.kc + kvoff;
+  const uint16_t* vcb = a.vc + kvoff;
+  const uint16_t* knb = FUSED ? a.kn + kvoff : nullptr;
+  const uint16_t* vnb = FUSED ? a.vn + kvoff : nullptr;
+  constexpr int kLdKeys = kPfWaves * 4;                // keys per loader round
+  constexpr int kLdRounds = kPfKeys / kLdKeys;
+  uint4 kr[kLdRounds], vr[kLdRounds];
+  int bid[kLdRounds];
+  auto fetch_ids = [&](int t) {
+    if (ONE_BLOCK) {
+      bid[0] = btrow[min(t * kPfKeys, kend - 1) / a.bs];
+    } else {
+#pragma unroll
+      for (int i = 0; i < kLdRounds; ++i) bid[i] = btrow[min(t * kPfKeys + kLdKeys * i + lkey, kend - 1) / a.bs];
+    }
+  };
+  auto fetch_row = [&](int i, int p, int slot) {
+    const int64_t e = (int64_t)slot * row_elems;
+    const uint4* kp = reinterpret_cast<const uint4*>(kcb + e);
+    const uint4* vp = reinterpret_cast<const uint4*>(vcb + e);
+    if (FUSED) {
+      const bool fresh = p >= ctx0;
+      const int64_t tok = q_begin + (p - ctx0);
+      kp = fresh ? reinterpret_cast<const uint4*>(knb + tok * a.kn_ts) : kp;
+      vp = fresh ? reinterpret_cast<const uint4*>(vnb + tok * a.vn_ts) : vp;
+    }
+    kr[i] = kp[lc];
+    vr[i] = vp[lc];
+  };
+  auto load = [&](int t) {
+    const int k0 = t * kPfKeys;
+    if (ONE_BLOCK) {
+      const int blk = min(max(bid[0], 0), a.nb - 1);
+      const int slot0 = blk * a.bs + k0 % a.bs;
+      const int last = kend - 1 - k0;
+#pragma unroll
+      for (int i = 0; i < kLdRounds; ++i) {
+        const int off = min(kLdKeys * i + lkey, last);
+        fetch_row(i, k0 + off, slot0 + off);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kLdRounds; ++i) {
+        const int p = min(k0 + kLdKeys * i + lkey, kend - 1);
+        const int blk = min(max(bid[i], 0), a.nb - 1);
+        fetch_row(i, p, blk * a.bs + p % a.bs);
+      }
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kLdRounds; ++i) {
+      *reinterpret_cast<u32x4_t*>(&ks[buf][(kLdKeys * i + lkey) * kKStride + 8 * lc]) = as_u4(kr[i]);
+      *reinterpret_cast<u32x4_t*>(&vs[buf][(kLdKeys * i + lkey) * kPfVStride + 8 * lc]) = as_u4(vr[i]);
+    }
+  };
+
+  float4_t o[kPfRt][8];
+  float m[kPfRt], lsum[kPfRt];
+#pragma unroll
+  for (int rt = 0; rt < kPfRt; ++rt) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[rt][dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    m[rt] = -INFINITY;
+    lsum[rt] = 0.f;
+  }
+
+  auto compute = [&](int t, int buf, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const int kbase = t * kPfKeys;
+    if (MASK && kbase > wlim_hi) return;         // no row of this wave sees these keys
+    const uint16_t* kt = ks[buf];
+    const uint16_t* vt = vs[buf];
+    constexpr int kSt = kPfKeys / 16;      // 16-key sub-tiles
+    float4_t acc[kPfRt][kSt];
+#if AIA_PF_PRIO
+    __builtin_amdgcn_s_setprio(1);
+#endif
+#pragma unroll
+    for (int st = 0; st < kSt; ++st) {
+      uint4 kf[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        kf[j] = *reinterpret_cast<const uint4*>(kt + (16 * st + n) * kKStride + 32 * j + 8 * g);
+#pragma unroll
+      for (int rt = 0; rt < kPfRt; ++rt) {
+        // (a row tile with no valid row computes rows that are never written)
+        acc[rt][st] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[rt][st] = qk_step(kf[j], qf[rt][j], acc[rt][st]);
+      }
+    }
+#if AIA_PF_PRIO
+    __builtin_amdgcn_s_setprio(0);
+#endif
+    uint4 pb[kPfRt][kSt / 2];
+#pragma unroll
+    for (int rt = 0; rt < kPfRt; ++rt) {
+      float sv[kSt][4];
+      float tmax = -INFINITY;
+      if (MASK) {     // causal diagonal / sequence end: per-key limits
+        const int rel = lim[rt] - kbase - 4 * g;
+#pragma unroll
+        for (int st = 0; st < kSt; ++st)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) sv[st][v] = 16 * st + v <= rel ? acc[rt][st][v] : -INFINITY;
+      } else {
+#pragma unroll
+        for (int st = 0; st < kSt; ++st)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) sv[st][v] = acc[rt][st][v];
+      }
+#pragma unroll
+      for (int st = 0; st < kSt; ++st)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) tmax = fmaxf(tmax, sv[st][v]);
+      tmax = aia::group4_max(tmax);
+      // Lazy rescale: the running max m only moves when some row's tile max
+      // exceeds it by more than kLazyLog2, so P stays below 2^kLazyLog2 and O
+      // and l (which share m) need no rescale on most tiles.  m = -inf until
+      // a row sees a key; exp2(-inf) = 0 then.
+      const float tm = tmax * a.scale_log2;
+      const bool grow = __any(tm > m[rt] + kLazyLog2);
+      const float mnew = grow ? fmaxf(m[rt], tm) : m[rt];
+      const float msub = mnew == -INFINITY ? 0.f : mnew;
+      float p[kSt][4];
+      float psum = 0.f;
+#pragma unroll
+      for (int st = 0; st < kSt; ++st)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          p[st][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[st][v], a.scale_log2, -msub));
+          psum += p[st][v];
+        }
+      if (grow) {
+        const float alpha = __builtin_amdgcn_exp2f(m[rt] - msub);
+        lsum[rt] = lsum[rt] * alpha + psum;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[rt][dt] *= alpha;
+      } else {
+        lsum[rt] += psum;
+      }
+      m[rt] = mnew;
+#pragma unroll
+      for (int pp = 0; pp < kSt / 2; ++pp) {
+        pb[rt][pp].x = aia::pack_bf16x2(p[2 * pp][0], p[2 * pp][1]);
+        pb[rt][pp].y = aia::pack_bf16x2(p[2 * pp][2], p[2 * pp][3]);
+        pb[rt][pp].z = aia::pack_bf16x2(p[2 * pp + 1][0], p[2 * pp + 1][1]);
+        pb[rt][pp].w = aia::pack_bf16x2(p[2 * pp + 1][2], p[2 * pp + 1][3]);
+      }
+    }
+#if AIA_PF_PRIO
+    __builtin_amdgcn_s_setprio(1);
+#endif
+    // V^T fragments of half the dims at a time are read before their MFMAs,
+    // so the transposing reads overlap instead of waiting one by one
+#pragma unroll
+    for (int pp = 0; pp < kSt / 2; ++pp) {
+#pragma unroll
+      for (int dh = 0; dh < 8; dh += kPfDtBatch) {
+        bf16x8_t va[kPfDtBatch];
+#pragma unroll
+        for (int d = 0; d < kPfDtBatch; ++d) {
+          const short4_t v0 = vt_frag<kPfVStride>(vt + (32 * pp) * kPfVStride, n, g, dh + d);
+          const short4_t v1 = vt_frag<kPfVStride>(vt + (32 * pp + 16) * kPfVStride, n, g, dh + d);
+          va[d] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+#pragma unroll
+        for (int d = 0; d < kPfDtBatch; ++d)
+#pragma unroll
+          for (int rt = 0; rt < kPfRt; ++rt)
+            o[rt][dh + d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[d], as_b8(pb[rt][pp]),
+                                                                     o[rt][dh + d], 0, 0, 0);
+      }
+    }
+#if AIA_PF_PRIO
+    __builtin_amdgcn_s_setprio(0);
+#endif
+  };
+
+  if (ntiles > 0) {
+    fetch_ids(0);
+    load(0);
+    fetch_ids(1);
+    store(0);
+    __syncthreads();
+    // tiles below the wave's smallest row limit need no mask; the two runs
+    // together take every tile, so all waves pass the same barriers
+    const int t_um = min(ntiles, (wlim_lo + 1) / kPfKeys);
+    auto step = [&](int t, auto mask_tag) {
+      const int buf = t & 1;
+      if (t + 1 < ntiles) {
+        load(t + 1);
+        fetch_ids(t + 2);
+      }
+      compute(t, buf, mask_tag);
+      if (t + 1 < ntiles) store(buf ^ 1);
+      __syncthreads();
+    };
+    int t = 0;
+    for (; t < t_um; ++t) step(t, std::false_type{});
+    for (; t < ntiles; ++t) step(t, std::true_type{});
+  }
+
+#pragma unroll
+  for (int rt = 0; rt < kPfRt; ++rt) {
+    lsum[rt] = aia::group4_sum(lsum[rt]);
+    if (!rv[rt]) continue;
+    const float inv = lsum[rt] > 0.f ? 1.f / lsum[rt] : 0.f;
+    uint16_t* op = a.out + (int64_t)(q_begin + tokr[rt]) * a.o_ts + (int64_t)headr[rt] * a.o_hs;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      uint2 wv;
+      wv.x = aia::pack_bf16x2(o[rt][dt][0] * inv, o[rt][dt][1] * inv);
+      wv.y = aia::pack_bf16x2(o[rt][dt][2] * inv, o[rt][dt][3] * inv);
+      *reinterpret_cast<uint2*>(op + 16 * dt + 4 * g) = wv;
+    }
   }
 }
 
@@ -1343,7 +1767,8 @@ extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens
       head_dim_v, reinterpret_cast<int32_t*>(ws + L.hdr),
       reinterpret_cast<int32_t*>(ws + L.seg), reinterpret_cast<int32_t*>(ws + L.wave),
       reinterpret_cast<int32_t*>(ws + L.cnt), reinterpret_cast<int32_t*>(ws + L.req),
-      reinterpret_cast<int32_t*>(ws + L.mrg));
+      reinterpret_cast<int32_t*>(ws + L.mrg), reinterpret_cast<int2*>(ws + L.pf),
+      (int32_t)L.pf_cap, (int32_t)L.seg_cap);
   return check_hip(hipGetLastError(), "aia_attn_plan launch");
 }
 
@@ -1357,7 +1782,6 @@ extern "C" int aia_paged_attention_gqa(
     int64_t new_value_token_stride, int32_t num_waves, int32_t flags, void* workspace,
     int64_t workspace_bytes, void* stream) {
   using namespace aia;
-  (void)cu_seqlens_q; (void)seqlens_kv;
   if (int rc = check_heads("aia_paged_attention_gqa", num_q_heads, num_kv_heads)) return rc;
   if (head_dim != kHeadDim)
     return fail(AIA_ERR_UNSUPPORTED, "aia_paged_attention_gqa: head_dim %d (only 128)", head_dim);
@@ -1367,7 +1791,8 @@ extern "C" int aia_paged_attention_gqa(
     return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: block_size %d / num_blocks %d",
                 block_size, num_blocks);
   if (num_tokens == 0 || batch == 0) return AIA_OK;    // empty step (zero-size tensors)
-  if (!query || !key_cache || !value_cache || !block_table || !out || !workspace)
+  if (!query || !key_cache || !value_cache || !block_table || !out || !workspace || !cu_seqlens_q ||
+      !seqlens_kv)
     return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: null pointer argument");
   if (q_token_stride % 8 || q_head_stride % 8 || out_token_stride % 4 || out_head_stride % 8 ||
       ((uintptr_t)query & 15) || ((uintptr_t)key_cache & 15) || ((uintptr_t)value_cache & 15) ||
@@ -1426,6 +1851,26 @@ extern "C" int aia_paged_attention_gqa(
   }
 #undef AIA_GQA_LAUNCH
   if (int rc = check_hip(hipGetLastError(), "gqa_attn_kernel launch")) return rc;
+  if (L.pf_cap > 0) {
+    PrefillArgs pa;
+    pa.q = a.q; pa.q_ts = a.q_ts; pa.q_hs = a.q_hs;
+    pa.kc = a.kc; pa.vc = a.vc; pa.kn = a.kn; pa.vn = a.vn; pa.kn_ts = a.kn_ts; pa.vn_ts = a.vn_ts;
+    pa.bt = block_table; pa.bt_stride = block_table_stride;
+    pa.cu_q = cu_seqlens_q; pa.kvlen = seqlens_kv;
+    pa.hkv = g.hkv; pa.group = g.group; pa.bs = block_size; pa.nb = num_blocks;
+    pa.batch = batch; pa.tokens = num_tokens;
+    pa.scale_log2 = a.scale_log2;
+    pa.out = a.out; pa.o_ts = a.o_ts; pa.o_hs = a.o_hs;
+    pa.items = reinterpret_cast<const int2*>(ws + L.pf);
+    pa.hdr = a.hdr;
+    const dim3 grid((unsigned)(L.pf_cap * g.hkv));
+    const bool one_block = block_size % kPfKeys == 0;
+    if (one_block && pa.kn) gqa_prefill_kernel<true, true><<<grid, kPfWaves * 64, 0, s>>>(pa);
+    else if (one_block) gqa_prefill_kernel<true, false><<<grid, kPfWaves * 64, 0, s>>>(pa);
+    else if (pa.kn) gqa_prefill_kernel<false, true><<<grid, kPfWaves * 64, 0, s>>>(pa);
+    else gqa_prefill_kernel<false, false><<<grid, kPfWaves * 64, 0, s>>>(pa);
+    if (int rc = check_hip(hipGetLastError(), "gqa_prefill_kernel launch")) return rc;
+  }
   if (a.fused_merge || (flags & AIA_ATTN_SKIP_MERGE)) return AIA_OK;
   return launch_merge(ws, L, g, g.nw, head_dim, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs, s);
 }

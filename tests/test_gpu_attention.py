@@ -171,6 +171,8 @@ def test_plan_from_another_stream_is_waited_for():
     ([37, 1, 5, 1, 64], [137, 300, 5, 77, 64], 28, 4, 16, 0),   # chunked prefill, many q-blocks
     ([2, 2, 1], [513, 40, 999], 64, 2, 128, 7),        # head blocks (group 32), splits
     ([2] * 4, [1024, 1500, 2, 4096], 32, 8, 128, 3),   # MTP verify shape
+    ([200, 1, 130, 19], [300, 77, 130, 40], 28, 4, 16, 0),   # prefill route, with/without prefix
+    ([256, 3], [256 + 1000, 900], 16, 8, 128, 0),      # prefill route, group 2
 ])
 def test_fused_kv_write(lqs, lks, hq, hkv, bs, waves):
     """The attention kernel performs the KV slot write of the step's new rows:
@@ -280,3 +282,40 @@ def test_empty_step():
     kc = torch.zeros(4, 16, 8, 128, dtype=torch.bfloat16, device=DEV)
     out = ops.paged_attention_gqa(q, kc, kc, plan, 128 ** -0.5)
     assert out.shape == (0, 16, 128)
+
+
+@pytest.mark.parametrize("lqs,lks,hq,hkv,bs", [
+    ([512, 512, 512], [1383, 1164, 1035], 28, 4, 128),    # configs[1] prefill chunks
+    ([19, 18, 1], [19, 50, 300], 28, 4, 16),              # 133 rows routed, 126 stay split-K
+    ([200], [200], 16, 8, 16),                            # group 2, no prefix
+    ([130, 7], [1000, 7], 8, 8, 128),                     # group 1
+    ([64, 9], [100, 700], 64, 4, 16),                     # group 16
+    ([8, 2], [8, 600], 64, 2, 128),                       # group 32: 256 rows from 8 tokens
+    ([300], [300 + 4000], 32, 8, 128),                    # long prefix
+    ([129, 1], [129, 5], 4, 1, 4),                        # block size 4: blocks inside a tile
+    ([100, 70], [700, 70], 28, 4, 64),                    # block size = tile
+    ([300], [1300], 16, 8, 256),                          # tiles inside a block
+])
+def test_prefill_route(lqs, lks, hq, hkv, bs):
+    """Requests whose query rows (tokens x group) fill a 128-row item run on
+    the prefill kernel (K/V tiles staged in LDS once per 128 rows); the rest
+    of the batch stays on split-K.  Both against the oracle."""
+    step = workloads.make_gqa_step(lqs=lqs, lks=lks, num_q_heads=hq, num_kv_heads=hkv,
+                                   block_size=bs, seed=57)
+    check(step)
+
+
+def test_prefill_route_repeated_and_deterministic():
+    """The prefill kernel has no split: repeated calls on one plan are
+    bit-identical, with a decode batch beside it on split-K."""
+    step = workloads.make_gqa_step(lqs=[300, 1, 1, 2], lks=[700, 2000, 30, 90], num_q_heads=28,
+                                   num_kv_heads=4, block_size=16, seed=8)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, 28, 4, 128, 16)
+    q, kc, vc = step.q.to(DEV), step.k_cache.to(DEV), step.v_cache.to(DEV)
+    first = ops.paged_attention_gqa(q, kc, vc, plan, step.scale).clone()
+    for _ in range(3):
+        again = ops.paged_attention_gqa(q, kc, vc, plan, step.scale)
+    torch.cuda.synchronize()
+    assert torch.equal(first, again)
+    assert (first.float().cpu() - oracle(step)).abs().max().item() <= TOL

@@ -75,6 +75,15 @@ constexpr int kPfWaves = AIA_PF_WAVES;       // waves per prefill work-group
 constexpr int kPfRt = AIA_PF_RT;             // 16-row MFMA tiles per wave
 constexpr int kPfRows = 16 * kPfRt * kPfWaves;   // rows per prefill work item
 constexpr int kPfKeys = AIA_PF_KEYS;         // keys per staged K/V tile (32 or 64)
+// Items alone fill the chip when items x kv heads reach kPfTargetWgs (two
+// resident work-groups per CU); below that, each item's key tiles are cut
+// into chunks of at least kPfMinChunk tiles, sized so all units still fit in
+// one round (fp32 partials, merged with the split-K partials' rule).
+#ifndef AIA_PF_TARGET
+#define AIA_PF_TARGET 512
+#endif
+constexpr int kPfTargetWgs = AIA_PF_TARGET;
+constexpr int kPfMinChunk = 8;
 
 // rb: row blocks (of 16 query rows) per segment.  Two when a GQA launch's
 // requests average more query tokens than one block holds (prefill chunks),
@@ -105,8 +114,8 @@ Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_
 
 // Workspace layout (all offsets 256-byte aligned).
 struct Layout {
-  int64_t hdr, seg, wave, part_ml, part_o, cnt, req, mrg, pf, total;
-  int64_t seg_cap, part_cap, mrg_cap, pf_cap;
+  int64_t hdr, seg, wave, part_ml, part_o, cnt, req, mrg, pf, pfm, pf_o, pf_ml, total;
+  int64_t seg_cap, part_cap, mrg_cap, pf_cap, pf_unit_cap, pf_mrg_cap, pf_slots;
 };
 
 constexpr int kMergeDims = 16;   // output dims per merge element
@@ -138,7 +147,16 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
   const int64_t pf_rows = g.pf ? (int64_t)tokens * g.group : 0;
   const int64_t pf_reqs = pf_rows / kPfRows < batch ? pf_rows / kPfRows : batch;
   L.pf_cap = (pf_rows + kPfRows - 1) / kPfRows + pf_reqs;
-  L.pf = off;       off = align256(off + L.pf_cap * 8);
+  // Chunked items exist only when items x kv heads < kPfTargetWgs; then the
+  // units number at most items + total tiles / chunk < 2 kPfTargetWgs / Hkv.
+  const int64_t split_units = g.pf ? 2 * ((kPfTargetWgs + g.hkv - 1) / g.hkv) + 1 : 0;
+  L.pf_unit_cap = L.pf_cap > split_units ? L.pf_cap : split_units;
+  L.pf_mrg_cap = g.pf ? (kPfTargetWgs + g.hkv - 1) / g.hkv : 0;
+  L.pf_slots = split_units * g.hkv;             // partial row blocks
+  L.pf = off;       off = align256(off + L.pf_unit_cap * 16);
+  L.pfm = off;      off = align256(off + L.pf_mrg_cap * 16);
+  L.pf_ml = off;    off = align256(off + L.pf_slots * kPfRows * 8);
+  L.pf_o = off;     off = align256(off + L.pf_slots * kPfRows * (int64_t)kHeadDim * 4);
   L.total = off;
   return L;
 }
@@ -234,7 +252,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     int32_t batch, Geometry g, int32_t waves, int32_t dv,
     int32_t* __restrict__ hdr, int32_t* __restrict__ seg, int32_t* __restrict__ wave_rec,
     int32_t* __restrict__ counters, int32_t* __restrict__ req_scratch,
-    int32_t* __restrict__ mrg, int2* __restrict__ pf_items, int32_t pf_cap, int32_t seg_cap) {
+    int32_t* __restrict__ mrg, int4* __restrict__ pf_units, int4* __restrict__ pf_mrg,
+    int32_t pf_cap, int32_t pf_unit_cap, int32_t pf_mrg_cap, int32_t seg_cap) {
   __shared__ int lds[kPlanLds];
   __shared__ int wave_sums[kPlanThreads / 64];
   __shared__ int2 wave_sums2[kPlanThreads / 64];
@@ -268,10 +287,6 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     int2 tot2;
     const int2 ex2 = block_exclusive_scan2(make_int2(cnt, pcnt), wave_sums2, &tot2);
     if (b < batch) req_off[b] = carry + ex2.x;
-    // (the capacity holds whenever cu_seqlens_q ends at the step's token
-    // count; metadata that does not is cut off here, never written past)
-    for (int i = 0; i < pcnt && pcarry + ex2.y + i < pf_cap; ++i)
-      pf_items[pcarry + ex2.y + i] = make_int2(b, (pcnt - 1 - i) * kPfRows);
     carry += tot2.x;
     pcarry += tot2.y;
   }
@@ -280,6 +295,76 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   // write past it.
   if (carry > seg_cap || pcarry > pf_cap) { carry = 0; pcarry = 0; }
   if (tid == 0) req_off[batch] = carry;
+
+  // 1b) prefill units.  Items are listed per request, last rows first (under
+  // the causal mask they see the most keys).  When items x kv heads leave
+  // the chip underfilled, an item's tiles are cut into k balanced chunks of
+  // about `chunk` tiles; its k units write partials and get a merge record.
+  int units = 0, pmerges = 0;
+  if (pcarry > 0) {
+    const int* cu_p = req_lds ? cuv : cu_q;
+    const int* kv_p = req_lds ? kvv : kvlen;
+    auto item_tiles = [&](int lq, int lk, int row0) {
+      const int last = min(lq * g.group, row0 + kPfRows) - 1;
+      const int kend = max(0, min(lk, lk - lq + last / g.group + 1));
+      return (kend + kPfKeys - 1) / kPfKeys;
+    };
+    int chunk = 0x7fffffff;
+    if ((int64_t)pcarry * g.hkv < kPfTargetWgs) {
+      int mine = 0;
+      for (int base = 0; base < batch; base += kPlanThreads) {
+        const int b = base + tid;
+        if (b < batch) {
+          const int lq = cu_p[b + 1] - cu_p[b], lk = kv_p[b];
+          if ((int64_t)lq * g.group >= kPfRows)
+            for (int r0 = 0; r0 < lq * g.group; r0 += kPfRows) mine += item_tiles(lq, lk, r0);
+        }
+      }
+      int wtot;
+      block_exclusive_scan(mine, wave_sums, &wtot);
+      // sum_i ceil(nt_i / c) <= W / c + P, so c = W Hkv / (target - P Hkv)
+      // keeps units x kv heads within the target: one round of work-groups
+      const int64_t room = kPfTargetWgs - (int64_t)pcarry * g.hkv;
+      chunk = max(kPfMinChunk, (int)(((int64_t)wtot * g.hkv + room - 1) / room));
+    }
+    int ucarry = 0, mcarry2 = 0;
+    for (int base = 0; base < batch; base += kPlanThreads) {
+      const int b = base + tid;
+      int lq = 0, lk = 0, nu = 0, nm = 0;
+      bool routed = false;
+      if (b < batch) {
+        lq = cu_p[b + 1] - cu_p[b];
+        lk = kv_p[b];
+        routed = (int64_t)lq * g.group >= kPfRows;
+      }
+      if (routed)
+        for (int r0 = 0; r0 < lq * g.group; r0 += kPfRows) {
+          const int nt = item_tiles(lq, lk, r0);
+          const int k = nt > chunk ? (nt + chunk - 1) / chunk : 1;
+          nu += k;
+          nm += k > 1 ? 1 : 0;
+        }
+      int2 tot2;
+      const int2 ex2 = block_exclusive_scan2(make_int2(nu, nm), wave_sums2, &tot2);
+      if (routed && ucarry + tot2.x <= pf_unit_cap && mcarry2 + tot2.y <= pf_mrg_cap) {
+        int u = ucarry + ex2.x, mm = mcarry2 + ex2.y;
+        const int nitems = (lq * g.group + kPfRows - 1) / kPfRows;
+        for (int i = nitems - 1; i >= 0; --i) {
+          const int r0 = i * kPfRows;
+          const int nt = item_tiles(lq, lk, r0);
+          const int k = nt > chunk ? (nt + chunk - 1) / chunk : 1;
+          if (k > 1) pf_mrg[mm++] = make_int4(b, r0, u, k);
+          for (int j = 0; j < k; ++j)
+            pf_units[u++] = make_int4(b, r0, (int)((int64_t)j * nt / k), (int)((int64_t)(j + 1) * nt / k));
+        }
+      }
+      ucarry += tot2.x;
+      mcarry2 += tot2.y;
+    }
+    units = ucarry;
+    pmerges = mcarry2;
+    if (units > pf_unit_cap || pmerges > pf_mrg_cap) { units = 0; pmerges = 0; }
+  }
   __syncthreads();
   const int nseg = req_off[batch];
   const int* cu_r = req_lds ? cuv : cu_q;
@@ -465,7 +550,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   }
   if (tid == 0) {
     hdr[0] = nseg; hdr[1] = total_tiles; hdr[2] = tpw; hdr[3] = carry; hdr[4] = waves;
-    hdr[5] = mcarry; hdr[6] = min(pcarry, pf_cap);
+    hdr[5] = mcarry; hdr[6] = units; hdr[7] = pmerges;
     // sentinel record so readers may look one past the end
     int* r = seg + (int64_t)nseg * 8;
     r[0] = 0; r[1] = 0; r[2] = 0; r[3] = 0; r[4] = 0;
@@ -1014,8 +1099,11 @@ struct PrefillArgs {
   float scale_log2;
   uint16_t* out;
   int64_t o_ts, o_hs;
-  const int2* items;
+  const int4* units;         // {request, first row, first tile, end tile}
   const int32_t* hdr;
+  float* part_o;             // partial row blocks of chunked items
+  float2* part_ml;
+  int32_t part_units;        // units the partial buffer holds
 };
 
 // LDS row strides (elements) of the staged K and V tiles: 272 bytes puts the
@@ -1070,9 +1158,9 @@ void gqa_prefill_kernel(PrefillArgs a) {
   const int pairs = count * a.hkv;
   if ((int)blockIdx.x >= pairs) return;
   const int pair = xcd_range(blockIdx.x, pairs);
-  const int kvh = pair / count, item = pair - kvh * count;
-  const int2 it = a.items[item];
-  const int b = it.x, row0 = it.y;
+  const int kvh = pair / count, unit = pair - kvh * count;
+  const int4 it = a.units[unit];
+  const int b = it.x, row0 = it.y, t0 = it.z, t1 = it.w;
   if (b < 0 || b >= a.batch || kvh >= a.hkv) return;
   const int q_begin = a.cu_q[b], lq = a.cu_q[b + 1] - q_begin, lk = a.kvlen[b];
   const int G = a.group;
@@ -1086,8 +1174,9 @@ void gqa_prefill_kernel(PrefillArgs a) {
   const int row_elems = a.hkv * kHeadDim;
   const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
 
-  // new K/V rows of the tokens whose first row lies in this item
-  if (FUSED) {
+  // new K/V rows of the tokens whose first row lies in this item (written by
+  // the item's first chunk)
+  if (FUSED && t0 == 0) {
     const int t_lo = (row0 + G - 1) / G, t_hi = min(lq, (row_end - 1) / G + 1);
     for (int e = tid; e < (t_hi - t_lo) * 16; e += kPfWaves * 64) {
       const int t = t_lo + (e >> 4), c = e & 15;
@@ -1138,6 +1227,11 @@ void gqa_prefill_kernel(PrefillArgs a) {
   // keys the work-group's last row sees
   const int kend = max(0, min(lk, ctx0 + (row_end - 1) / G + 1));
   const int ntiles = (kend + kPfKeys - 1) / kPfKeys;
+  // this unit's tiles [t0, t1) of the item's [0, ntiles); a unit that does
+  // not cover them all writes a partial
+  if (t0 < 0 || t1 < t0 || t1 > ntiles) return;
+  const bool whole = t0 == 0 && t1 == ntiles;
+  if (!whole && unit >= a.part_units) return;
 
   // loader: thread tid moves 16-byte chunk (tid % 16) of keys kLdKeys i + tid / 16.
   // Block ids are fetched one tile ahead (their loads are in flight during a
@@ -1328,34 +1422,42 @@ void gqa_prefill_kernel(PrefillArgs a) {
 #endif
   };
 
-  if (ntiles > 0) {
-    fetch_ids(0);
-    load(0);
-    fetch_ids(1);
+  if (t1 > t0) {
+    fetch_ids(t0);
+    load(t0);
+    fetch_ids(t0 + 1);
     store(0);
     __syncthreads();
     // tiles below the wave's smallest row limit need no mask; the two runs
     // together take every tile, so all waves pass the same barriers
-    const int t_um = min(ntiles, (wlim_lo + 1) / kPfKeys);
+    const int t_um = max(t0, min(t1, (wlim_lo + 1) / kPfKeys));
     auto step = [&](int t, auto mask_tag) {
-      const int buf = t & 1;
-      if (t + 1 < ntiles) {
+      const int buf = (t - t0) & 1;
+      if (t + 1 < t1) {
         load(t + 1);
         fetch_ids(t + 2);
       }
       compute(t, buf, mask_tag);
-      if (t + 1 < ntiles) store(buf ^ 1);
+      if (t + 1 < t1) store(buf ^ 1);
       __syncthreads();
     };
-    int t = 0;
+    int t = t0;
     for (; t < t_um; ++t) step(t, std::false_type{});
-    for (; t < ntiles; ++t) step(t, std::true_type{});
+    for (; t < t1; ++t) step(t, std::true_type{});
   }
 
 #pragma unroll
   for (int rt = 0; rt < kPfRt; ++rt) {
     lsum[rt] = aia::group4_sum(lsum[rt]);
     if (!rv[rt]) continue;
+    if (!whole) {   // partial (O, m, l) of the unit's rows
+      const int64_t prow = ((int64_t)unit * a.hkv + kvh) * kPfRows + (wid * kPfRt + rt) * kRows + n;
+      float* pp = a.part_o + prow * kHeadDim;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * g) = o[rt][dt];
+      if (g == 0) a.part_ml[prow] = make_float2(m[rt], lsum[rt]);
+      continue;
+    }
     const float inv = lsum[rt] > 0.f ? 1.f / lsum[rt] : 0.f;
     uint16_t* op = a.out + (int64_t)(q_begin + tokr[rt]) * a.o_ts + (int64_t)headr[rt] * a.o_hs;
 #pragma unroll
@@ -1378,6 +1480,11 @@ struct MergeArgs {
   int32_t group, hb, dv, nw, hkv, rb;
   const int32_t* mrg;
   int64_t mrg_cap;
+  // prefill chunk merges: records {request, first row, first unit, units}
+  const int4* pf_mrg;
+  const float* pf_o;
+  const float2* pf_ml;
+  const int32_t* cu_q;
 };
 
 // Merge of split partials.  The planner lists the merge work: one record per
@@ -1466,6 +1573,49 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
       }
     }
     __syncthreads();
+  }
+
+  // Prefill chunk merges, one work item per (record, kv head, 16 rows):
+  // thread (row r, 8 dims) folds the record's partials with the same rule.
+  const int npm = a.pf_mrg ? a.hdr[7] : 0;
+  constexpr int kSlices = kPfRows / 16;
+  const int64_t pitems = (int64_t)npm * a.hkv * kSlices;
+  for (int64_t it = blockIdx.x; it < pitems; it += gridDim.x) {
+    const int rec = (int)(it / (a.hkv * kSlices));
+    const int rem = (int)(it - (int64_t)rec * a.hkv * kSlices);
+    const int kvh = rem / kSlices, slice = rem - kvh * kSlices;
+    const int4 r = a.pf_mrg[rec];
+    const int b = r.x, row0 = r.y, u0 = r.z, k = r.w;
+    const int q_begin = a.cu_q[b], lq = a.cu_q[b + 1] - q_begin;
+    const int rl = slice * 16 + (threadIdx.x >> 4), c = (threadIdx.x & 15) * 8;
+    const int row = row0 + rl;
+    if (row >= lq * a.group) continue;
+    float4 acc[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+    float mx = -1e30f, ls = 0.f;
+    for (int j = 0; j < k; ++j) {
+      const int64_t prow = ((int64_t)(u0 + j) * a.hkv + kvh) * kPfRows + rl;
+      const float2 ml = a.pf_ml[prow];
+      const float4* src = reinterpret_cast<const float4*>(a.pf_o + prow * kHeadDim + c);
+      const float4 x0 = src[0], x1 = src[1];
+      const float mn = fmaxf(mx, ml.x);
+      const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
+      ls = ls * sa + ml.y * sb;
+      acc[0].x = acc[0].x * sa + x0.x * sb; acc[0].y = acc[0].y * sa + x0.y * sb;
+      acc[0].z = acc[0].z * sa + x0.z * sb; acc[0].w = acc[0].w * sa + x0.w * sb;
+      acc[1].x = acc[1].x * sa + x1.x * sb; acc[1].y = acc[1].y * sa + x1.y * sb;
+      acc[1].z = acc[1].z * sa + x1.z * sb; acc[1].w = acc[1].w * sa + x1.w * sb;
+      mx = mn;
+    }
+    const float inv = ls > 0.f ? 1.f / ls : 0.f;
+    const int tok = row / a.group, head = kvh * a.group + (row - tok * a.group);
+    uint16_t* op = a.out + (int64_t)(q_begin + tok) * a.o_ts + (int64_t)head * a.o_hs + c;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      uint2 wv;
+      wv.x = aia::pack_bf16x2(acc[i].x * inv, acc[i].y * inv);
+      wv.y = aia::pack_bf16x2(acc[i].z * inv, acc[i].w * inv);
+      *reinterpret_cast<uint2*>(op + 4 * i) = wv;
+    }
   }
 }
 
@@ -1705,14 +1855,20 @@ void mla_attn_kernel(MlaArgs a) {
 int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32_t dv,
                  const float* part_o,
                  const float2* part_ml, const int32_t* seg, uint16_t* out, int64_t o_ts,
-                 int64_t o_hs, hipStream_t s) {
+                 int64_t o_hs, const int32_t* cu_q, hipStream_t s) {
   MergeArgs mg;
   mg.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
   mg.seg = seg; mg.part_o = part_o; mg.part_ml = part_ml;
   mg.out = out; mg.o_ts = o_ts; mg.o_hs = o_hs; mg.group = g.group; mg.hb = g.hb; mg.dv = dv;
   mg.nw = nw; mg.hkv = g.hkv; mg.rb = g.rb;
   mg.mrg = reinterpret_cast<const int32_t*>(ws + L.mrg); mg.mrg_cap = L.mrg_cap;
-  const int64_t items = L.mrg_cap;
+  const bool pf = L.pf_mrg_cap > 0;
+  mg.pf_mrg = pf ? reinterpret_cast<const int4*>(ws + L.pfm) : nullptr;
+  mg.pf_o = reinterpret_cast<const float*>(ws + L.pf_o);
+  mg.pf_ml = reinterpret_cast<const float2*>(ws + L.pf_ml);
+  mg.cu_q = cu_q;
+  const int64_t pitems = pf ? L.pf_mrg_cap * g.hkv * (kPfRows / 16) : 0;
+  const int64_t items = L.mrg_cap > pitems ? L.mrg_cap : pitems;
   int64_t mgrid = items < 2048 ? items : 2048;
   if (mgrid < 1) mgrid = 1;
   merge_kernel<<<(unsigned)mgrid, 256, 0, s>>>(mg);
@@ -1767,8 +1923,9 @@ extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens
       head_dim_v, reinterpret_cast<int32_t*>(ws + L.hdr),
       reinterpret_cast<int32_t*>(ws + L.seg), reinterpret_cast<int32_t*>(ws + L.wave),
       reinterpret_cast<int32_t*>(ws + L.cnt), reinterpret_cast<int32_t*>(ws + L.req),
-      reinterpret_cast<int32_t*>(ws + L.mrg), reinterpret_cast<int2*>(ws + L.pf),
-      (int32_t)L.pf_cap, (int32_t)L.seg_cap);
+      reinterpret_cast<int32_t*>(ws + L.mrg), reinterpret_cast<int4*>(ws + L.pf),
+      reinterpret_cast<int4*>(ws + L.pfm), (int32_t)L.pf_cap, (int32_t)L.pf_unit_cap,
+      (int32_t)L.pf_mrg_cap, (int32_t)L.seg_cap);
   return check_hip(hipGetLastError(), "aia_attn_plan launch");
 }
 
@@ -1861,9 +2018,12 @@ extern "C" int aia_paged_attention_gqa(
     pa.batch = batch; pa.tokens = num_tokens;
     pa.scale_log2 = a.scale_log2;
     pa.out = a.out; pa.o_ts = a.o_ts; pa.o_hs = a.o_hs;
-    pa.items = reinterpret_cast<const int2*>(ws + L.pf);
+    pa.units = reinterpret_cast<const int4*>(ws + L.pf);
     pa.hdr = a.hdr;
-    const dim3 grid((unsigned)(L.pf_cap * g.hkv));
+    pa.part_o = reinterpret_cast<float*>(ws + L.pf_o);
+    pa.part_ml = reinterpret_cast<float2*>(ws + L.pf_ml);
+    pa.part_units = (int32_t)(L.pf_slots / g.hkv);
+    const dim3 grid((unsigned)(L.pf_unit_cap * g.hkv));
     const bool one_block = block_size % kPfKeys == 0;
     if (one_block && pa.kn) gqa_prefill_kernel<true, true><<<grid, kPfWaves * 64, 0, s>>>(pa);
     else if (one_block) gqa_prefill_kernel<true, false><<<grid, kPfWaves * 64, 0, s>>>(pa);
@@ -1872,7 +2032,8 @@ extern "C" int aia_paged_attention_gqa(
     if (int rc = check_hip(hipGetLastError(), "gqa_prefill_kernel launch")) return rc;
   }
   if (a.fused_merge || (flags & AIA_ATTN_SKIP_MERGE)) return AIA_OK;
-  return launch_merge(ws, L, g, g.nw, head_dim, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs, s);
+  return launch_merge(ws, L, g, g.nw, head_dim, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
+                      cu_seqlens_q, s);
 }
 
 extern "C" int aia_paged_attention_mla(
@@ -1925,5 +2086,6 @@ extern "C" int aia_paged_attention_mla(
   mla_attn_kernel<<<waves, 256, 0, s>>>(a);
   if (int rc = check_hip(hipGetLastError(), "mla_attn_kernel launch")) return rc;
   if (flags & AIA_ATTN_SKIP_MERGE) return AIA_OK;
-  return launch_merge(ws, L, g, 1, kMlaV, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs, s);
+  return launch_merge(ws, L, g, 1, kMlaV, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
+                      cu_seqlens_q, s);
 }

@@ -173,6 +173,7 @@ def test_plan_from_another_stream_is_waited_for():
     ([2] * 4, [1024, 1500, 2, 4096], 32, 8, 128, 3),   # MTP verify shape
     ([200, 1, 130, 19], [300, 77, 130, 40], 28, 4, 16, 0),   # prefill route, with/without prefix
     ([256, 3], [256 + 1000, 900], 16, 8, 128, 0),      # prefill route, group 2
+    ([300], [6000], 16, 8, 128, 0),                    # prefill items cut into key chunks
 ])
 def test_fused_kv_write(lqs, lks, hq, hkv, bs, waves):
     """The attention kernel performs the KV slot write of the step's new rows:
@@ -319,3 +320,18 @@ def test_prefill_route_repeated_and_deterministic():
     torch.cuda.synchronize()
     assert torch.equal(first, again)
     assert (first.float().cpu() - oracle(step)).abs().max().item() <= TOL
+
+
+@pytest.mark.parametrize("lqs,lks,hq,hkv,bs", [
+    ([128], [16384], 16, 8, 128),                         # 16 items: 32 chunks each
+    ([512], [8192], 28, 4, 128),                          # 112 items: a few chunks each
+    ([200, 1, 3], [5000, 300, 40], 32, 8, 16),            # chunks + split-K rows, block 16
+    ([64, 64], [64, 3000], 16, 8, 64),                    # one item short, one chunked
+])
+def test_prefill_chunked_items(lqs, lks, hq, hkv, bs):
+    """Too few prefill items to fill the chip: each item's keys are cut into
+    balanced chunks whose partials are merged (log-sum-exp) in the merge
+    pass; the result matches the oracle and does not depend on the cut."""
+    step = workloads.make_gqa_step(lqs=lqs, lks=lks, num_q_heads=hq, num_kv_heads=hkv,
+                                   block_size=bs, seed=61)
+    check(step)

@@ -204,3 +204,31 @@ def test_gqa_fused_pre_attention_matches_torch_path(qwen3):
             assert torch.equal(cf[0].cpu(), cp[0].cpu())
         scale = op.float().abs().max().item()
         assert (of.float() - op.float()).abs().max().item() <= TOL * max(1.0, scale)
+
+
+def test_gqa_backend_long_prefill_on_prefill_kernel():
+    """Prompts long enough to fill 128-row items (tokens x group 4) run on the
+    prefill kernel, with the new K/V rows written by it: caches bit-exact and
+    outputs within tolerance, across a prefill, a chunked continuation beside
+    a decode row, and a decode step."""
+    g = torch.Generator().manual_seed(5)
+    hq, hkv, d, hidden, bs = 8, 2, 128, 256, 16
+    p = "model.layers.0.self_attn."
+    w = {
+        p + "qkv_proj.weight": (torch.randn((hq + 2 * hkv) * d, hidden, generator=g) / 16).bfloat16(),
+        p + "o_proj.weight": (torch.randn(hidden, hq * d, generator=g) / 32).bfloat16(),
+    }
+    w = {k: v.to(DEV) for k, v in w.items()}
+    kw = dict(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, scale=d ** -0.5, num_layers=1,
+              device=DEV, dtype=torch.bfloat16, w=w, rms_eps=1e-6)
+    hip = GqaHipBackend(**kw)
+    twin = oracle_twin(GqaHipBackend)(**kw)
+    caches_h = hip.alloc_kv_caches(24, bs)
+    caches_r = twin.alloc_kv_caches(24, bs)
+    a, b = [3, 9, 4], [7, 1, 11, 2, 5, 13, 17, 6, 19, 20]
+    steps = [
+        [(0, 40, a), (0, 70, b[:5])],              # two prompts: 160 and 280 rows
+        [(40, 1, a), (70, 64, b[:9])],             # decode + 64-token continuation (256 rows)
+        [(41, 1, a), (134, 1, b[:9])],             # decode
+    ]
+    run_pair(hip, twin, steps, caches_h, caches_r, bs, hidden, seed=6)

@@ -43,6 +43,10 @@ SIGNATURES = {
                       c_i32, c_i32, c_vp],
     "aia_qk_norm_rope": [c_vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_i64,
                          c_vp, c_vp, c_f32, c_vp],
+    "aia_mla_kv_latent": [c_vp, c_i64, c_i32, c_vp, c_f32, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64,
+                          c_vp],
+    "aia_mla_q_latent": [c_vp, c_i64, c_i64, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp,
+                         c_i64, c_i64, c_vp],
     "aia_mtp_compact": [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32,
                         c_i32, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp],
 }

@@ -31,7 +31,7 @@ class MlaHipBackend(AttentionBackend):
     def __init__(self, w: dict, *, num_heads: int, qk_nope: int, qk_rope: int,
                  v_head_dim: int, kv_lora_rank: int, q_lora_rank, rms_eps: float,
                  softmax_scale: float, num_layers: int, device, dtype, absorb: bool = True,
-                 layer_prefix=None):
+                 layer_prefix=None, fuse_pre_attention: bool = True):
         if kv_lora_rank != ops.MLA_LATENT or qk_rope != ops.MLA_ROPE:
             raise NotImplementedError(
                 f"mla_hip supports latent 512 + rope 64, got {kv_lora_rank} + {qk_rope}")
@@ -50,6 +50,10 @@ class MlaHipBackend(AttentionBackend):
         self.absorb = True      # the latent cache is the point of this family
         self.layer_prefix = layer_prefix or (lambda i: f"model.layers.{i}.")
         self._absorb_w = {}
+        # With fuse_pre_attention, q_latent and k_latent each come from one
+        # kernel (norm / interleave / RoPE / W_UK product / cat; bf16 rounding
+        # where the torch ops round) when the shapes allow it (nope 128).
+        self.fuse_pre_attention = fuse_pre_attention
 
     def alloc_kv_caches(self, num_blocks: int, block_size: int) -> list:
         kd = self.kv_lora_rank + self.qk_rope
@@ -61,12 +65,27 @@ class MlaHipBackend(AttentionBackend):
         return caches
 
     def _weights(self, layer_idx):
+        """(W_UK, W_UV, W_UK transposed to (H, 512, nope) for the fused query
+        kernel), split once per layer."""
         if layer_idx not in self._absorb_w:
             p = self.layer_prefix(layer_idx)
-            self._absorb_w[layer_idx] = build_absorb_weights(
+            w_uk, w_uv = build_absorb_weights(
                 self.w[p + "self_attn.kv_b_proj.weight"], self.num_heads, self.qk_nope,
                 self.v_head_dim, self.kv_lora_rank)
+            self._absorb_w[layer_idx] = (w_uk, w_uv, w_uk.transpose(1, 2).contiguous())
         return self._absorb_w[layer_idx]
+
+    def _fusable(self, q, ckv_full, ctx):
+        T = q.shape[0]
+
+        def rows(t):             # one 64-wide row per token, 8-byte accesses
+            return (t is not None and t.dtype == torch.bfloat16 and t.is_cuda and t.numel() == T * 64
+                    and t.stride(-1) == 1 and t.stride(0) % 4 == 0 and t.data_ptr() % 8 == 0)
+        return (self.fuse_pre_attention and self.qk_nope == 128 and q.dtype == torch.bfloat16
+                and q.is_cuda and q.stride(-1) == 1 and q.stride(0) % 8 == 0 and q.stride(1) % 8 == 0
+                and q.data_ptr() % 16 == 0 and ckv_full.stride(-1) == 1
+                and ckv_full.stride(0) % 8 == 0 and ckv_full.data_ptr() % 16 == 0
+                and rows(getattr(ctx, "cos", None)) and rows(getattr(ctx, "sin", None)))
 
     def attention(self, layer_idx: int, x: torch.Tensor, ctx) -> torch.Tensor:
         w = self.w
@@ -81,19 +100,24 @@ class MlaHipBackend(AttentionBackend):
                          w[p + "self_attn.q_a_layernorm.weight"], self.rms_eps)
             q = q @ w[p + "self_attn.q_b_proj.weight"].t()
         q = q.view(T, nh, nope + rope)
-        q_nope, q_pe = q.split([nope, rope], dim=-1)
         ckv_full = x @ w[p + "self_attn.kv_a_proj_with_mqa.weight"].t()
-        ckv, k_pe = ckv_full.split([kvl, rope], dim=-1)
-        ckv = rms_norm(ckv, w[p + "self_attn.kv_a_layernorm.weight"], self.rms_eps)
-        k_pe = k_pe.reshape(T, 1, rope)
-        q_pe = ds_rope_interleave(q_pe)
-        k_pe = ds_rope_interleave(k_pe)
-        q_pe = q_pe * ctx.cos + rotate_half(q_pe) * ctx.sin
-        k_pe = k_pe * ctx.cos + rotate_half(k_pe) * ctx.sin
-        w_uk, w_uv = self._weights(layer_idx)
-        q_latent = torch.cat([torch.einsum("tnp,npl->tnl", q_nope, w_uk), q_pe],
-                             dim=-1).contiguous()
-        k_latent = torch.cat([ckv.unsqueeze(1), k_pe], dim=-1).contiguous()
+        w_uk, w_uv, w_uk_t = self._weights(layer_idx)
+        if self._fusable(q, ckv_full, ctx):
+            q_latent = ops.mla_q_latent(q, w_uk_t, ctx.cos, ctx.sin)
+            k_latent = ops.mla_kv_latent(ckv_full, w[p + "self_attn.kv_a_layernorm.weight"],
+                                         self.rms_eps, ctx.cos, ctx.sin)
+        else:
+            q_nope, q_pe = q.split([nope, rope], dim=-1)
+            ckv, k_pe = ckv_full.split([kvl, rope], dim=-1)
+            ckv = rms_norm(ckv, w[p + "self_attn.kv_a_layernorm.weight"], self.rms_eps)
+            k_pe = k_pe.reshape(T, 1, rope)
+            q_pe = ds_rope_interleave(q_pe)
+            k_pe = ds_rope_interleave(k_pe)
+            q_pe = q_pe * ctx.cos + rotate_half(q_pe) * ctx.sin
+            k_pe = k_pe * ctx.cos + rotate_half(k_pe) * ctx.sin
+            q_latent = torch.cat([torch.einsum("tnp,npl->tnl", q_nope, w_uk), q_pe],
+                                 dim=-1).contiguous()
+            k_latent = torch.cat([ckv.unsqueeze(1), k_pe], dim=-1).contiguous()
         self._write_kv(layer_idx, k_latent, None, ctx)
         o_latent = self._attn(layer_idx, q_latent, k_latent, None, ctx)
         o = torch.einsum("tnl,nvl->tnv", o_latent, w_uv)

@@ -78,6 +78,60 @@ def qk_norm_rope(qkv, num_q_heads, num_kv_heads, cos, sin, q_norm_weight=None,
     return q.view(T, num_q_heads, D), k.view(T, num_kv_heads, D), v.view(T, num_kv_heads, D)
 
 
+def _rope_rows(t, name, T, width):
+    _check_device_tensor(t, name, _BF16)
+    _require(t.shape[0] == T and t.shape[-1] == width and t.numel() == T * width and
+             t.stride(-1) == 1, f"{name} must hold one {width}-wide row per token")
+    return t.stride(0)
+
+
+def mla_kv_latent(ckv_full, norm_weight, eps, cos, sin, out=None):
+    """Absorbed-MLA latent KV rows, one launch: ``[rms_norm(ckv), rope(
+    interleave(k_pe))]`` of the kv_a_proj_with_mqa output ``ckv_full`` (T,
+    576) with ``cos``/``sin`` (T, 1, 64).  Returns ``out`` (T, 1, 576), the
+    reference's ``k_latent`` (auto_infer/layers/attention/mla.py:97-111)."""
+    _check_device_tensor(ckv_full, "ckv_full", _BF16)
+    _require(ckv_full.dim() == 2 and ckv_full.shape[1] == MLA_LATENT + MLA_ROPE and
+             ckv_full.stride(1) == 1, "ckv_full must be (T, 576) with unit inner stride")
+    T = ckv_full.shape[0]
+    cts, sts = _rope_rows(cos, "cos", T, MLA_ROPE), _rope_rows(sin, "sin", T, MLA_ROPE)
+    _check_device_tensor(norm_weight, "norm_weight", _BF16)
+    _require(norm_weight.numel() == MLA_LATENT and norm_weight.is_contiguous(),
+             "norm_weight must be 512 contiguous values")
+    if out is None:
+        out = torch.empty(T, 1, MLA_LATENT + MLA_ROPE, dtype=_BF16, device=ckv_full.device)
+    _require(out.is_contiguous() and out.numel() == T * (MLA_LATENT + MLA_ROPE),
+             "out must be a contiguous (T, 1, 576) tensor")
+    _native.call("aia_mla_kv_latent", _ptr(ckv_full), ckv_full.stride(0), T, _ptr(norm_weight),
+                 float(eps), _ptr(cos), cts, _ptr(sin), sts, _ptr(out), MLA_LATENT + MLA_ROPE,
+                 _stream(ckv_full.device))
+    return out
+
+
+def mla_q_latent(q, w_uk_t, cos, sin, out=None):
+    """Absorbed-MLA latent query, one launch: ``[q_nope . W_UK, rope(
+    interleave(q_pe))]`` for ``q`` (T, H, 192) = [nope 128, pe 64], with
+    ``w_uk_t`` = W_UK transposed, (H, 512, 128) contiguous, and ``cos``/``sin``
+    (T, 1, 64).  Returns ``out`` (T, H, 576), the reference's ``q_latent``
+    (auto_infer/layers/attention/mla.py:93-107)."""
+    _check_device_tensor(q, "q", _BF16)
+    _require(q.dim() == 3 and q.shape[2] == 128 + MLA_ROPE and q.stride(2) == 1,
+             "q must be (T, H, 192) with unit inner stride")
+    T, H, _ = q.shape
+    _check_device_tensor(w_uk_t, "w_uk_t", _BF16)
+    _require(tuple(w_uk_t.shape) == (H, MLA_LATENT, 128) and w_uk_t.is_contiguous(),
+             "w_uk_t must be a contiguous (H, 512, 128) tensor")
+    cts, sts = _rope_rows(cos, "cos", T, MLA_ROPE), _rope_rows(sin, "sin", T, MLA_ROPE)
+    if out is None:
+        out = torch.empty(T, H, MLA_LATENT + MLA_ROPE, dtype=_BF16, device=q.device)
+    _require(tuple(out.shape) == (T, H, MLA_LATENT + MLA_ROPE) and out.stride(2) == 1,
+             "out must be (T, H, 576) with unit inner stride")
+    _native.call("aia_mla_q_latent", _ptr(q), q.stride(0), q.stride(1), T, H, _ptr(w_uk_t),
+                 _ptr(cos), cts, _ptr(sin), sts, _ptr(out), out.stride(0), out.stride(1),
+                 _stream(q.device))
+    return out
+
+
 def mtp_compact(preds, drafts, active_mask, hidden, positions, slots, scratch_positions,
                 scratch_slots, *, accepted=None, out_hidden=None, out_tokens=None,
                 out_positions=None, out_slots=None):

@@ -148,7 +148,7 @@ def other_configs(stream, only=None):
     with enough rotating caches to exceed the Infinity Cache, and the fused
     kernels either side of the path.  `only` selects one entry (its key:
     configs[1] .. configs[4], configs[1]_prefill, configs[1]_decode,
-    pre_attention, mtp_compaction)."""
+    pre_attention, mla_pre_attention, mtp_compaction)."""
     import time as _time
     import numpy as np
     from auto_infer_amd import ops, packing, workloads
@@ -259,6 +259,47 @@ def other_configs(stream, only=None):
             "GBps": round(by / fused_us / 1e3, 1),
             "frac_of_peak": round(by / fused_us / 1e3 / HBM_PEAK_GBS, 4)}
         del qkv, qkv0
+
+    if want("mla_pre_attention"):
+        note("absorbed-MLA pre-attention: latent query + latent KV rows at the configs[2] batch")
+        from auto_infer_amd.attention.layers import ds_rope_interleave, rms_norm, rotate_half
+        T, H, kvl, rope = 64, 16, 512, 64
+        g = torch.Generator(device=dev).manual_seed(6)
+        q = torch.randn(T, H, 128 + rope, device=dev, generator=g).bfloat16()
+        ckv_full = torch.randn(T, kvl + rope, device=dev, generator=g).bfloat16()
+        w_uk = (torch.randn(H, 128, kvl, device=dev, generator=g) / 11).bfloat16()
+        w_uk_t = w_uk.transpose(1, 2).contiguous()
+        nw = torch.ones(kvl, device=dev, dtype=torch.bfloat16)
+        pos = torch.arange(T, device=dev) + 1000
+        inv = 1.0 / (10000.0 ** (torch.arange(0, rope, 2, device=dev).float() / rope))
+        emb = torch.cat([torch.outer(pos.float(), inv)] * 2, dim=-1)
+        cos, sin = emb.cos().bfloat16()[:, None], emb.sin().bfloat16()[:, None]
+        ql_buf = torch.empty(T, H, kvl + rope, device=dev, dtype=torch.bfloat16)
+        kl_buf = torch.empty(T, 1, kvl + rope, device=dev, dtype=torch.bfloat16)
+
+        def fused(i):
+            ops.mla_q_latent(q, w_uk_t, cos, sin, out=ql_buf)
+            ops.mla_kv_latent(ckv_full, nw, 1e-6, cos, sin, out=kl_buf)
+
+        def torch_ops(i):      # mla.py:93-111 as torch ops
+            q_nope, q_pe = q.split([128, rope], dim=-1)
+            ckv, k_pe = ckv_full.split([kvl, rope], dim=-1)
+            ckv = rms_norm(ckv, nw, 1e-6)
+            k_pe = ds_rope_interleave(k_pe.reshape(T, 1, rope))
+            q_pe = ds_rope_interleave(q_pe)
+            q_pe = q_pe * cos + rotate_half(q_pe) * sin
+            k_pe = k_pe * cos + rotate_half(k_pe) * sin
+            ql = torch.cat([torch.einsum("tnp,npl->tnl", q_nope, w_uk), q_pe], dim=-1)
+            kl = torch.cat([ckv.unsqueeze(1), k_pe], dim=-1)
+            return ql, kl
+
+        fused_us = _time_graph(fused, stream, 5, 20)
+        torch_us = _time_graph(torch_ops, stream, 5, 20)
+        by = (q.numel() + ckv_full.numel() + w_uk.numel() + ql_buf.numel() + kl_buf.numel()) * 2
+        res["mla_pre_attention_latents"] = {
+            "shape": f"T {T}, H {H}, nope 128, rope {rope}, latent {kvl} (W_UK product on MFMA)",
+            "fused_us": round(fused_us, 2), "torch_ops_us": round(torch_us, 2),
+            "GBps": round(by / fused_us / 1e3, 1)}
 
     if want("mtp_compaction"):
         note("MTP verify compaction at the configs[3] gear")

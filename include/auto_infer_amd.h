@@ -187,6 +187,30 @@ int aia_qk_norm_rope(void* qkv, int64_t qkv_token_stride, int32_t num_tokens,
                      int64_t sin_token_stride, const void* q_norm_weight,
                      const void* k_norm_weight, float eps, void* stream);
 
+/* Absorbed-MLA latent KV row, one launch.  Replaces the ckv RMSNorm, the
+ * k_pe ds_rope_interleave + NeoX RoPE and the cat of mla_paged_absorbed
+ * (auto_infer/layers/attention/mla.py:97-111; rotary_embedding/__init__.py:
+ * 10-23): out[t] = [rms_norm(ckv_full[t][:512], norm_weight, eps) (512),
+ * rope(interleave(ckv_full[t][512:576])) (64)], rounding to bf16 where those
+ * bf16 ops round.  ckv_full rows of 576 bf16 (the kv_a_proj_with_mqa output),
+ * cos/sin one 64-wide row per token; out rows of 576 (the k_latent that
+ * aia_kv_write stores). */
+int aia_mla_kv_latent(const void* ckv_full, int64_t ckv_token_stride, int32_t num_tokens,
+                      const void* norm_weight, float eps, const void* cos,
+                      int64_t cos_token_stride, const void* sin, int64_t sin_token_stride,
+                      void* out, int64_t out_token_stride, void* stream);
+
+/* Absorbed-MLA latent query, one launch.  Replaces the q_pe interleave +
+ * RoPE, the einsum("tnp,npl->tnl", q_nope, W_UK) and the cat of
+ * mla_paged_absorbed (mla.py:93-107): out[t][h] = [q_nope[t][h] . W_UK[h]
+ * (512, fp32 accumulation on MFMA, one bf16 rounding), rope(interleave(
+ * q_pe[t][h])) (64)].  q (T, H, 192) = [nope 128, pe 64]; w_uk_t is W_UK
+ * transposed, (H, 512, 128) contiguous; out (T, H, 576). */
+int aia_mla_q_latent(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                     int32_t num_tokens, int32_t num_heads, const void* w_uk_t, const void* cos,
+                     int64_t cos_token_stride, const void* sin, int64_t sin_token_stride,
+                     void* out, int64_t out_token_stride, int64_t out_head_stride, void* stream);
+
 /* On-device MTP verify compaction, one launch.  Replaces the accept/compact
  * block of GraphMtpRunner._target_body (auto_infer/worker/
  * graph_mtp_runner.py:224-248): for a gear of `gear` (<= 64) requests of

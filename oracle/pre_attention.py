@@ -83,3 +83,66 @@ def qk_norm_rope_f64(qkv, num_q_heads, num_kv_heads, positions, q_norm_weight=No
     q = q * emb.cos() + rotate_half(q) * emb.sin()
     k = k * emb.cos() + rotate_half(k) * emb.sin()
     return q, k, v
+
+
+# ------------------------------------------------------------- absorbed MLA
+
+def ds_rope_interleave(x):
+    """rotary_embedding/__init__.py:15-23: the DeepSeek pe dims are stored
+    interleaved; view (d/2, 2), transpose, flatten: out[j] = in[2j],
+    out[d/2 + j] = in[2j + 1]."""
+    d = x.shape[-1]
+    return x.reshape(*x.shape[:-1], d // 2, 2).transpose(-1, -2).reshape(*x.shape[:-1], d)
+
+
+def mla_kv_latent(ckv_full, norm_weight, eps, cos, sin, kv_lora_rank=512):
+    """mla.py:97-111 on the kv_a_proj_with_mqa output (T, kvl + rope):
+    k_latent = cat(rms_norm(ckv), rope(ds_rope_interleave(k_pe))), (T, 1,
+    kvl + rope), every op rounding to bf16 as the reference's bf16 ops do."""
+    T = ckv_full.shape[0]
+    ckv, k_pe = ckv_full.split([kv_lora_rank, ckv_full.shape[1] - kv_lora_rank], dim=-1)
+    ckv = rms_norm(ckv, norm_weight, eps)
+    k_pe = ds_rope_interleave(k_pe.reshape(T, 1, -1))
+    cos = cos.reshape(T, 1, -1)
+    sin = sin.reshape(T, 1, -1)
+    k_pe = k_pe * cos + rotate_half(k_pe) * sin
+    return torch.cat([ckv.unsqueeze(1), k_pe], dim=-1)
+
+
+def mla_q_latent(q, w_uk, cos, sin):
+    """mla.py:93-107 on q (T, H, nope + rope): q_latent = cat(einsum(
+    "tnp,npl->tnl", q_nope, W_UK), rope(ds_rope_interleave(q_pe))), (T, H,
+    kvl + rope).  The einsum is a bf16 GEMM: fp32 products and sums, one
+    rounding to bf16 (as the library GEMM it runs on)."""
+    T, H, _ = q.shape
+    nope = w_uk.shape[1]
+    q_nope, q_pe = q.split([nope, q.shape[2] - nope], dim=-1)
+    absorbed = torch.einsum("tnp,npl->tnl", q_nope.float(), w_uk.float()).to(q.dtype)
+    q_pe = ds_rope_interleave(q_pe)
+    cos = cos.reshape(T, 1, -1)
+    sin = sin.reshape(T, 1, -1)
+    q_pe = q_pe * cos + rotate_half(q_pe) * sin
+    return torch.cat([absorbed, q_pe], dim=-1)
+
+
+def mla_latents_f64(q, w_uk, ckv_full, norm_weight, eps, positions, kv_lora_rank=512,
+                    base=10000.0):
+    """q_latent and k_latent in float64 with exact angles (no rounding)."""
+    T, H, _ = q.shape
+    nope = w_uk.shape[1]
+    x = q.double()
+    q_nope, q_pe = x.split([nope, x.shape[2] - nope], dim=-1)
+    rope = q_pe.shape[-1]
+    inv = 1.0 / (base ** (torch.arange(0, rope, 2, dtype=torch.float64) / rope))
+    f = torch.outer(torch.as_tensor(positions).double(), inv)
+    emb = torch.cat((f, f), dim=-1)[:, None]
+
+    def rot(t):
+        t = ds_rope_interleave(t)
+        return t * emb.cos() + rotate_half(t) * emb.sin()
+    ql = torch.cat([torch.einsum("tnp,npl->tnl", q_nope, w_uk.double()), rot(q_pe)], dim=-1)
+    c = ckv_full.double()
+    ckv, k_pe = c.split([kv_lora_rank, c.shape[1] - kv_lora_rank], dim=-1)
+    ckv = ckv * torch.rsqrt(ckv.pow(2).mean(dim=-1, keepdim=True) + eps) * norm_weight.double()
+    kl = torch.cat([ckv.unsqueeze(1), rot(k_pe.reshape(T, 1, -1))], dim=-1)
+    return ql, kl

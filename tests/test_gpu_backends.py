@@ -232,3 +232,47 @@ def test_gqa_backend_long_prefill_on_prefill_kernel():
         [(41, 1, a), (134, 1, b[:9])],             # decode
     ]
     run_pair(hip, twin, steps, caches_h, caches_r, bs, hidden, seed=6)
+
+
+def test_mla_fused_pre_attention_matches_torch_path():
+    """The latent-query and latent-KV kernels against the torch ops they
+    replace (split, rms_norm, ds_rope_interleave, RoPE, einsum with W_UK,
+    cat), end to end through attention() with DeepSeek-V2-Lite head shapes
+    (nope 128, rope 64, latent 512): the latent caches within one bf16 ulp of
+    each row's largest value (the norm's sum order), outputs within 2e-2."""
+    g = torch.Generator().manual_seed(9)
+    nh, nope, rope, vd, kvl, hidden, bs = 16, 128, 64, 128, 512, 512, 16
+    p = "model.layers.0."
+    w = {
+        p + "self_attn.q_proj.weight": torch.randn(nh * (nope + rope), hidden, generator=g) / 22,
+        p + "self_attn.kv_a_proj_with_mqa.weight": torch.randn(kvl + rope, hidden, generator=g) / 22,
+        p + "self_attn.kv_a_layernorm.weight": 1 + 0.1 * torch.randn(kvl, generator=g),
+        p + "self_attn.kv_b_proj.weight": torch.randn(nh * (nope + vd), kvl, generator=g) / 22,
+        p + "self_attn.o_proj.weight": torch.randn(hidden, nh * vd, generator=g) / 45,
+    }
+    w = {k: v.bfloat16().to(DEV) for k, v in w.items()}
+    kw = dict(num_heads=nh, qk_nope=nope, qk_rope=rope, v_head_dim=vd, kv_lora_rank=kvl,
+              q_lora_rank=None, rms_eps=1e-6, softmax_scale=(nope + rope) ** -0.5,
+              num_layers=1, device=DEV, dtype=torch.bfloat16)
+    fused = MlaHipBackend(w, **kw)
+    plain = MlaHipBackend(w, fuse_pre_attention=False, **kw)
+    cf, cp = fused.alloc_kv_caches(12, bs), plain.alloc_kv_caches(12, bs)
+    for rows in ([(0, 11, [4]), (0, 40, [1, 6, 7])], [(11, 1, [4]), (40, 1, [1, 6, 7])]):
+        T = sum(n for _, n, _ in rows)
+        x = (torch.randn(T, hidden, generator=g) * 0.5).bfloat16().to(DEV)
+        ctx_f, positions = make_ctx(fused, cf, rows, bs)
+        ctx_p, _ = make_ctx(plain, cp, rows, bs)
+        cos, sin = rope_tables(positions * 53, rope)
+        ctx_f.cos = ctx_p.cos = cos.to(DEV)
+        ctx_f.sin = ctx_p.sin = sin.to(DEV)
+        assert fused._fusable(torch.zeros(T, nh, 192, dtype=torch.bfloat16, device=DEV),
+                              torch.zeros(T, 576, dtype=torch.bfloat16, device=DEV), ctx_f)
+        of = fused.attention(0, x, ctx_f)
+        op = plain.attention(0, x, ctx_p)
+        torch.cuda.synchronize()
+        a, b = cf[0][0].float(), cp[0][0].float()
+        assert bool(((a - b).abs() <= b.abs().amax(-1, keepdim=True) * 2.0 ** -7).all())
+        scale = op.float().abs().max().item()
+        err = (of.float() - op.float()).abs().max().item()
+        print(f"output max-abs diff {err:.3e} (scale {scale:.2f})", flush=True)
+        assert err <= TOL * max(1.0, scale)

@@ -74,3 +74,18 @@ def test_argument_validation_of_the_fused_kernels_without_gpu():
                                      vp(16), 2048, 128, None, None, 0, 0, 0, 0, vp(16), 1 << 20,
                                      None)
     assert rc == _native.AIA_ERR_INVALID and "scale" in _native.last_error()
+    # absorbed-MLA latents: rows of 576 with 16-byte alignment
+    rc = lib.aia_mla_kv_latent(vp(16), 500, 4, vp(16), ctypes.c_float(1e-6), vp(16), 64, vp(16),
+                               64, vp(16), 576, None)
+    assert rc == _native.AIA_ERR_INVALID and "576" in _native.last_error()
+    rc = lib.aia_mla_kv_latent(vp(8), 576, 4, vp(16), ctypes.c_float(1e-6), vp(16), 64, vp(16),
+                               64, vp(16), 576, None)
+    assert rc == _native.AIA_ERR_INVALID
+    rc = lib.aia_mla_q_latent(vp(16), 16 * 192, 192, 4, 0, vp(16), vp(16), 64, vp(16), 64,
+                              vp(16), 16 * 576, 576, None)
+    assert rc == _native.AIA_ERR_INVALID and "sizes" in _native.last_error()
+    rc = lib.aia_mla_q_latent(vp(16), 16 * 192, 100, 4, 16, vp(16), vp(16), 64, vp(16), 64,
+                              vp(16), 16 * 576, 576, None)
+    assert rc == _native.AIA_ERR_INVALID and "alignment" in _native.last_error()
+    # no tokens: nothing to do, whatever the pointers
+    assert lib.aia_mla_q_latent(None, 0, 0, 0, 16, None, None, 0, None, 0, None, 0, 0, None) == 0

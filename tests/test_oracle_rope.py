@@ -90,3 +90,68 @@ def test_bf16_restatement_tracks_float64(norm):
         assert err < 0.05, err
         assert (a.double() - b).abs().mean().item() < 0.01
     assert torch.equal(v.double(), v64)
+
+
+# ------------------------------------------------------------- absorbed MLA
+
+from oracle.pre_attention import ds_rope_interleave, mla_kv_latent, mla_latents_f64, mla_q_latent
+
+
+def test_ds_rope_interleave_closed_form():
+    x = torch.arange(64).float().reshape(1, 64)
+    y = ds_rope_interleave(x)[0]
+    assert y[:32].tolist() == list(range(0, 64, 2))
+    assert y[32:].tolist() == list(range(1, 64, 2))
+
+
+def _mla_case(T, H, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(T, H, 192, generator=g) * 2).bfloat16()
+    w_uk = (torch.randn(H, 128, 512, generator=g) / 11).bfloat16()
+    ckv = (torch.randn(T, 576, generator=g) * 3).bfloat16()
+    w = (1 + 0.2 * torch.randn(512, generator=g)).bfloat16()
+    return q, w_uk, ckv, w
+
+
+def test_mla_position_zero_leaves_pe_interleaved_only():
+    q, w_uk, ckv, w = _mla_case(3, 2, 1)
+    cos, sin = rope_tables([0, 0, 0], 64)
+    ql = mla_q_latent(q, w_uk, cos, sin)
+    kl = mla_kv_latent(ckv, w, 1e-6, cos, sin)
+    assert torch.equal(ql[..., 512:], ds_rope_interleave(q[..., 128:]))
+    assert torch.equal(kl[:, 0, 512:], ds_rope_interleave(ckv[:, 512:]))
+
+
+def test_mla_rope_pairs_keep_norm_and_relative_scores():
+    """In float64: each rotated pair (j, 32 + j) of the interleaved pe keeps
+    its norm, and the pe score q . k depends on the position difference."""
+    q, w_uk, ckv, w = _mla_case(1, 1, 2)
+    for p in (0, 5, 1000):
+        ql, kl = mla_latents_f64(q, w_uk, ckv, w, 1e-6, [p])
+        x = ds_rope_interleave(q[..., 128:].double())
+        got = ql[..., 512:]
+        assert torch.allclose(got[..., :32] ** 2 + got[..., 32:] ** 2, x[..., :32] ** 2 + x[..., 32:] ** 2)
+    s = []
+    for pq, pk in ((10, 3), (107, 100), (5007, 5000)):
+        ql, _ = mla_latents_f64(q, w_uk, ckv, w, 1e-6, [pq])
+        _, kl = mla_latents_f64(q, w_uk, ckv, w, 1e-6, [pk])
+        s.append(float((ql[0, 0, 512:] * kl[0, 0, 512:]).sum()))
+    assert max(s) - min(s) < 1e-9 * max(1.0, abs(s[0]))
+
+
+def test_mla_bf16_restatement_tracks_float64():
+    """The bf16 restatement is the float64 mathematics up to bf16 rounding:
+    the W_UK product within one bf16 ulp (fp32 accumulation, one rounding),
+    the norm and RoPE within a few ulps of each row's largest value."""
+    T, H = 6, 4
+    q, w_uk, ckv, w = _mla_case(T, H, 3)
+    pos = [0, 1, 17, 300, 4095, 65000]
+    cos, sin = rope_tables(pos, 64)
+    ql = mla_q_latent(q, w_uk, cos, sin).double()
+    kl = mla_kv_latent(ckv, w, 1e-6, cos, sin).double()
+    el, ek = mla_latents_f64(q, w_uk, ckv, w, 1e-6, pos)
+    absd = (ql[..., :512] - el[..., :512]).abs()
+    assert bool((absd <= el[..., :512].abs() * 2.0 ** -8 + 1e-6).all())
+    for got, exp in ((ql[..., 512:], el[..., 512:]), (kl, ek)):
+        row = exp.abs().amax(dim=-1, keepdim=True)
+        assert bool(((got - exp).abs() <= row * 2.0 ** -6).all())

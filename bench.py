@@ -14,7 +14,12 @@ Infinity Cache) so KV reads come from HBM.  Steps are replayed from a HIP
 graph captured on the timed stream (the reference replays ACL graphs for
 decode too).
 
-Prints ONE JSON line (see the field notes in DESIGN.md).
+Prints ONE JSON line: the metric (tok/s of the step), the timing, the
+roofline of the attention kernel (algorithmic bytes per launch / kernel
+time against 8 TB/s, with the HBM traffic per launch measured by rocprofv3
+FETCH_SIZE + WRITE_SIZE), the CPU baseline (the oracle on this host's
+cores, a bounded sample) and the other BASELINE configs plus the fused
+kernels either side of the path (``other_configs``).
 """
 import argparse
 import json

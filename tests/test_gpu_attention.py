@@ -335,3 +335,50 @@ def test_prefill_chunked_items(lqs, lks, hq, hkv, bs):
     step = workloads.make_gqa_step(lqs=lqs, lks=lks, num_q_heads=hq, num_kv_heads=hkv,
                                    block_size=bs, seed=61)
     check(step)
+
+
+def test_prefill_route_in_a_hip_graph():
+    """The planner, the split-K kernel, the prefill kernel (with chunked
+    items) and the merge captured in one HIP graph: every replay, with eager
+    work and synchronisation between replays, equals the eager result, and
+    the metadata updated in place between replays is picked up."""
+    step = workloads.make_gqa_step(lqs=[128, 1, 2], lks=[6000, 700, 90], num_q_heads=16,
+                                   num_kv_heads=8, block_size=64, seed=71)
+    q, kc, vc = step.q.to(DEV), step.k_cache.to(DEV), step.v_cache.to(DEV)
+    bt = step.block_table.to(DEV)
+    cu = torch.tensor([0, *step.cu_seqlens_q], dtype=torch.int32, device=DEV)
+    kv = torch.tensor(step.seqlens_kv, dtype=torch.int32, device=DEV)
+    T = step.cu_seqlens_q[-1]
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        plan = ops.AttentionPlan(bt, cu, kv, T, 16, 8, 128, 64)
+        eager = ops.paged_attention_gqa(q, kc, vc, plan, step.scale).clone()
+        out = torch.empty_like(eager)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            plan.replan()
+            ops.paged_attention_gqa(q, kc, vc, plan, step.scale, out=out)
+    torch.cuda.synchronize()
+    assert (eager.float().cpu() - oracle(step)).abs().max().item() <= TOL
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        _ = (q.float() * 2).sum()            # unrelated eager work between replays
+    # shorter contexts written into the same metadata tensors: the replayed
+    # plan follows them
+    kv.copy_(torch.tensor([5000, 600, 80], dtype=torch.int32))
+    step.seqlens_kv = [5000, 600, 80]
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert (out.float().cpu() - oracle(step)).abs().max().item() <= TOL
+
+
+def test_prefill_chunk_at_32k_keys():
+    """One 512-token chunk behind a 32K-key context (group 7): chunked items,
+    many 64-block windows, against the oracle."""
+    check(workloads.make_gqa_step(lqs=[512], lks=[32768], num_q_heads=28, num_kv_heads=4,
+                                  block_size=128, seed=73))

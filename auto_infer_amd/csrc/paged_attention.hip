@@ -1911,6 +1911,8 @@ extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens
     return fail(AIA_ERR_INVALID, "aia_attn_plan: null metadata");
   if (block_size <= 0) return fail(AIA_ERR_INVALID, "aia_attn_plan: block_size %d", block_size);
   if (!workspace) return fail(AIA_ERR_INVALID, "aia_attn_plan: null workspace");
+  if ((uintptr_t)workspace & 255)
+    return fail(AIA_ERR_INVALID, "aia_attn_plan: workspace must be 256-byte aligned");
   const Geometry g = geometry(num_q_heads, num_kv_heads, batch, num_tokens, head_dim_v);
   const int32_t waves = resolve_waves(num_waves, g, head_dim_v);
   const Layout L = layout(batch, num_tokens, g, head_dim_v, waves);
@@ -1951,6 +1953,8 @@ extern "C" int aia_paged_attention_gqa(
   if (!query || !key_cache || !value_cache || !block_table || !out || !workspace || !cu_seqlens_q ||
       !seqlens_kv)
     return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: null pointer argument");
+  if ((uintptr_t)workspace & 255)
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: workspace must be 256-byte aligned");
   if (q_token_stride % 8 || q_head_stride % 8 || out_token_stride % 4 || out_head_stride % 8 ||
       ((uintptr_t)query & 15) || ((uintptr_t)key_cache & 15) || ((uintptr_t)value_cache & 15) ||
       ((uintptr_t)out & 15))
@@ -2055,6 +2059,8 @@ extern "C" int aia_paged_attention_mla(
   if (num_tokens == 0 || batch == 0) return AIA_OK;    // empty step (zero-size tensors)
   if (!q_latent || !latent_cache || !block_table || !out || !workspace)
     return fail(AIA_ERR_INVALID, "aia_paged_attention_mla: null pointer argument");
+  if ((uintptr_t)workspace & 255)
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_mla: workspace must be 256-byte aligned");
   if (q_token_stride % 8 || q_head_stride % 8 || out_token_stride % 8 || out_head_stride % 8 ||
       ((uintptr_t)q_latent & 15) || ((uintptr_t)latent_cache & 15) || ((uintptr_t)out & 15))
     return fail(AIA_ERR_INVALID, "aia_paged_attention_mla: tensors must be 16-byte aligned with "

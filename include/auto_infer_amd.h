@@ -63,10 +63,13 @@ int aia_attn_workspace_bytes(int32_t batch, int32_t num_tokens,
  * .cu_seqlens_q), seqlens_kv (batch entries, forward_context.py:15) and the
  * block table (batch rows, block_table_stride apart) and writes a flat list
  * of (request, kv-head group, query block, key range) work items into
- * `workspace`, each carrying the first block ids it reads.  The plan
- * depends only on step metadata, so one plan serves every layer of the
- * step.  num_waves: number of key ranges (work-groups); 0 picks the default
- * (about 2048 waves in flight for GQA, 512 groups for MLA). */
+ * `workspace` (256-byte aligned, aia_attn_workspace_bytes long), each
+ * carrying the first block ids it reads.  GQA requests whose query rows
+ * (tokens x group) fill a 128-row item become prefill items instead (cut
+ * into key chunks when they are too few to fill the chip).  The plan depends
+ * only on step metadata, so one plan serves every layer of the step.
+ * num_waves: number of key ranges (work-groups); 0 picks the default (about
+ * 2048 waves in flight for GQA, 768 four-wave groups for MLA). */
 int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
                   const int32_t* block_table, int32_t block_table_stride,
                   int32_t block_size, int32_t batch, int32_t num_tokens,

@@ -74,6 +74,10 @@ def test_argument_validation_of_the_fused_kernels_without_gpu():
                                      vp(16), 2048, 128, None, None, 0, 0, 0, 0, vp(16), 1 << 20,
                                      None)
     assert rc == _native.AIA_ERR_INVALID and "scale" in _native.last_error()
+    # the workspace must be 256-byte aligned
+    rc = lib.aia_attn_plan(vp(256), vp(256), vp(256), 16, 16, 1, 1, 16, 8, 128, 0, vp(256 + 16),
+                           1 << 30, None)
+    assert rc == _native.AIA_ERR_INVALID and "256-byte" in _native.last_error()
     # absorbed-MLA latents: rows of 576 with 16-byte alignment
     rc = lib.aia_mla_kv_latent(vp(16), 500, 4, vp(16), ctypes.c_float(1e-6), vp(16), 64, vp(16),
                                64, vp(16), 576, None)

@@ -1,0 +1,74 @@
+"""Seeded random steps through the whole GQA path (planner routing, split-K
+segments and their padding, row blocks, prefill items and their key chunks,
+merge) against the oracle, plus the fused KV write against the oracle write.
+
+Each case draws: heads (group 1..32), block size, a batch mixing decode,
+verify (2-4 tokens) and prefill chunks (with and without a prefix), and
+optionally a forced range count.  Sizes keep the float32 oracle to well
+under a second per case.
+"""
+import random
+
+import pytest
+import torch
+
+from auto_infer_amd import ops, workloads
+from oracle.paged_attn import kv_write, paged_attention
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+TOL = 2e-2
+
+HEADS = [(8, 8), (16, 8), (16, 4), (28, 4), (32, 8), (64, 4), (32, 1), (64, 2)]
+BLOCKS = [4, 16, 32, 64, 128, 256]
+
+
+def draw(seed):
+    r = random.Random(seed)
+    hq, hkv = r.choice(HEADS)
+    bs = r.choice(BLOCKS)
+    B = r.randint(1, 12)
+    lqs, lks = [], []
+    for _ in range(B):
+        kind = r.random()
+        if kind < 0.45:
+            lq = 1
+        elif kind < 0.65:
+            lq = r.randint(2, 4)
+        else:
+            lq = r.randint(5, 300)
+        prefix = 0 if r.random() < 0.2 else r.randint(0, 3000)
+        lqs.append(lq)
+        lks.append(lq + prefix)
+    waves = r.choice([0, 0, 0, 1, 3, 64, 700])
+    fused = r.random() < 0.5
+    return dict(hq=hq, hkv=hkv, bs=bs, lqs=lqs, lks=lks, waves=waves, fused=fused)
+
+
+@pytest.mark.parametrize("seed", range(120))
+def test_random_steps_match_the_oracle(seed):
+    c = draw(1000 + seed)
+    print(f"case {seed}: {c}", flush=True)
+    step = workloads.make_gqa_step(lqs=c["lqs"], lks=c["lks"], num_q_heads=c["hq"],
+                                   num_kv_heads=c["hkv"], block_size=c["bs"], seed=seed,
+                                   extra_blocks=3)
+    kc, vc = step.k_cache.to(DEV), step.v_cache.to(DEV)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, c["hq"], c["hkv"], 128, c["bs"],
+                                        num_waves=c["waves"])
+    ek, ev = step.k_cache, step.v_cache
+    if c["fused"]:
+        ek, ev = ek.clone(), ev.clone()
+        kv_write(step.k_new, step.v_new, ek, ev, step.slot_mapping)
+        out = ops.paged_attention_gqa(step.q.to(DEV), kc, vc, plan, step.scale,
+                                      key_new=step.k_new.to(DEV), value_new=step.v_new.to(DEV))
+    else:
+        out = ops.paged_attention_gqa(step.q.to(DEV), kc, vc, plan, step.scale)
+    torch.cuda.synchronize()
+    if c["fused"]:
+        assert torch.equal(kc.cpu(), ek) and torch.equal(vc.cpu(), ev)
+    exp = paged_attention(step.q, ek, ev, step.block_table, step.cu_seqlens_q, step.seqlens_kv,
+                          step.scale)
+    err = (out.float().cpu() - exp).abs().max().item()
+    print(f"max-abs err {err:.3e}", flush=True)
+    assert err <= TOL

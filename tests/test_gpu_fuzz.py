@@ -72,3 +72,33 @@ def test_random_steps_match_the_oracle(seed):
     err = (out.float().cpu() - exp).abs().max().item()
     print(f"max-abs err {err:.3e}", flush=True)
     assert err <= TOL
+
+
+def draw_mla(seed):
+    r = random.Random(seed)
+    bs = r.choice(BLOCKS)
+    B = r.randint(1, 10)
+    lqs, lks = [], []
+    for _ in range(B):
+        lq = 1 if r.random() < 0.6 else r.randint(2, 40)
+        lqs.append(lq)
+        lks.append(lq + (0 if r.random() < 0.15 else r.randint(0, 2500)))
+    return dict(bs=bs, lqs=lqs, lks=lks, waves=r.choice([0, 0, 1, 5, 100]))
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_mla_steps_match_the_oracle(seed):
+    from oracle.paged_attn import mla_absorbed_attention
+    c = draw_mla(2000 + seed)
+    print(f"case {seed}: {c}", flush=True)
+    step = workloads.make_mla_step(lqs=c["lqs"], lks=c["lks"], block_size=c["bs"], seed=seed)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, step.q_latent.shape[1], 1, 512,
+                                        c["bs"], num_waves=c["waves"])
+    out = ops.paged_attention_mla(step.q_latent.to(DEV), step.cache.to(DEV), plan, step.scale)
+    torch.cuda.synchronize()
+    exp = mla_absorbed_attention(step.q_latent, step.cache, step.block_table, step.cu_seqlens_q,
+                                 step.seqlens_kv, step.scale, 512)
+    err = (out.float().cpu() - exp).abs().max().item()
+    print(f"max-abs err {err:.3e}", flush=True)
+    assert err <= TOL

@@ -114,7 +114,7 @@ Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_
 
 // Workspace layout (all offsets 256-byte aligned).
 struct Layout {
-  int64_t hdr, seg, wave, part_ml, part_o, cnt, req, mrg, pf, pfm, pf_o, pf_ml, total;
+  int64_t hdr, seg, wave, part_ml, part_o, part_sc, cnt, req, mrg, pf, pfm, pf_o, pf_ml, total;
   int64_t seg_cap, part_cap, mrg_cap, pf_cap, pf_unit_cap, pf_mrg_cap, pf_slots;
 };
 
@@ -138,6 +138,7 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
   L.wave = off;     off = align256(off + (int64_t)waves * kRecInts * 4);
   L.part_ml = off;  off = align256(off + L.part_cap * g.nw * kRows * g.rb * 8);
   L.part_o = off;   off = align256(off + L.part_cap * g.nw * kRows * g.rb * (int64_t)dv * 4);
+  L.part_sc = off;  off = align256(off + L.part_cap * g.nw * kRows * g.rb * 4);
   L.mrg_cap = L.seg_cap * g.nw * merge_slices(g, dv);
   L.mrg = off;      off = align256(off + L.mrg_cap * kMrgInts * 4);
   L.cnt = off;      off = align256(off + L.seg_cap * g.nw * 4);
@@ -659,6 +660,12 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  const half2_t v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 
 __device__ __forceinline__ u32x4_t as_u4(uint4 v) { return u32x4_t{v.x, v.y, v.z, v.w}; }
 __device__ __forceinline__ bf16x8_t as_b8(uint4 v) { return __builtin_bit_cast(bf16x8_t, as_u4(v)); }
@@ -1480,6 +1487,8 @@ struct MergeArgs {
   int32_t group, hb, dv, nw, hkv, rb;
   const int32_t* mrg;
   int64_t mrg_cap;
+  int32_t part_f16;          // split-K partials stored as fp16 scaled by part_sc
+  const float* part_sc;
   // prefill chunk merges: records {request, first row, first unit, units}
   const int4* pf_mrg;
   const float* pf_o;
@@ -1533,7 +1542,26 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
       }
       mx = mn;
     };
-    if (live) {
+    if (live && a.part_f16) {    // scaled fp16 partials: x = y * c
+#pragma unroll 2
+      for (int k = kg; k < np; k += kMergeGroups) {
+        const int64_t pr = row0 + k * pstride;
+        const float2 ml = a.part_ml[pr];
+        const float sc = a.part_sc[pr];
+        const uint4* src = reinterpret_cast<const uint4*>(
+            reinterpret_cast<const uint16_t*>(a.part_o) + pr * a.dv + c);
+        const uint4 h0 = src[0], h1 = src[1];
+        const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        float4 x[kMergeDims / 4];
+#pragma unroll
+        for (int i = 0; i < kMergeDims / 4; ++i) {
+          const half2_t a2 = __builtin_bit_cast(half2_t, hw[2 * i]);
+          const half2_t b2 = __builtin_bit_cast(half2_t, hw[2 * i + 1]);
+          x[i] = make_float4((float)a2[0] * sc, (float)a2[1] * sc, (float)b2[0] * sc, (float)b2[1] * sc);
+        }
+        fold(ml, x);
+      }
+    } else if (live) {
 #pragma unroll 2
       for (int k = kg; k < np; k += kMergeGroups) {
         const int64_t pr = row0 + k * pstride;
@@ -1649,6 +1677,7 @@ struct MlaArgs {
   const int32_t* wave_rec;
   float* part_o;
   float2* part_ml;
+  float* part_sc;
   uint16_t* out;
   int64_t o_ts, o_hs;
   int32_t waves;
@@ -1657,8 +1686,8 @@ struct MlaArgs {
 };
 
 __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, int lt0, int lt1,
-                                            int w, int tpw, uint16_t* vt, float* sx, int lane,
-                                            int wid, bool use_pre, int pre) {
+                                            int w, int tpw, uint16_t* vt, float* sx, float* smax,
+                                            int lane, int wid, bool use_pre, int pre) {
   const int n = lane & 15, g = lane >> 4;
   const int b = rec[0], hbi = (rec[1] >> 16) & 0x3fff;
   const int qtok0 = rec[2], nq = rec[3] & 0xff, q0 = rec[3] >> 8, lim_base = rec[4];
@@ -1797,13 +1826,34 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
       }
     }
   } else {
+    // Partials in fp16 with a per-row scale: y = O / c, c = max |O| over the
+    // row's 512 dims (all 4 waves), so y is in [-1, 1] with 11 mantissa bits
+    // relative to the row's largest value -- finer than the bf16 output --
+    // and half the bytes of fp32 partials.  The merge multiplies back by c.
+    float mx = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) mx = fmaxf(mx, fabsf(o[dt][v]));
+    mx = aia::group4_max(mx);
+    if (g == 0) smax[wid * kRows + n] = mx;
+    __syncthreads();
+    const float c = fmaxf(fmaxf(smax[n], smax[kRows + n]), fmaxf(smax[2 * kRows + n], smax[3 * kRows + n]));
     const int part = part_base + (w - first_wave);
     if (rv) {
-      float* pp = a.part_o + ((int64_t)part * kRows + n) * kMlaV + d0;
+      const float inv = c > 0.f ? 1.f / c : 0.f;
+      uint16_t* pp = reinterpret_cast<uint16_t*>(a.part_o) + ((int64_t)part * kRows + n) * kMlaV + d0;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-        *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * g) = o[dt];
-      if (g == 0 && wid == 0) a.part_ml[(int64_t)part * kRows + n] = make_float2(m, lsum);
+      for (int dt = 0; dt < 8; ++dt) {
+        uint2 wv;
+        wv.x = pack_f16x2(o[dt][0] * inv, o[dt][1] * inv);
+        wv.y = pack_f16x2(o[dt][2] * inv, o[dt][3] * inv);
+        *reinterpret_cast<uint2*>(pp + 16 * dt + 4 * g) = wv;
+      }
+      if (g == 0 && wid == 0) {
+        a.part_ml[(int64_t)part * kRows + n] = make_float2(m, lsum);
+        a.part_sc[(int64_t)part * kRows + n] = c;
+      }
     }
   }
 }
@@ -1817,6 +1867,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AIA_MLA_WAV
 void mla_attn_kernel(MlaArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vt_all[4][kTile * kVStride];
   __shared__ __attribute__((aligned(16))) float sx[2 * 4 * 256];
+  __shared__ float smax[4 * kRows];
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int w = blockIdx.x;   // one tile range per work-group
@@ -1839,7 +1890,7 @@ void mla_attn_kernel(MlaArgs a) {
     if (!rec_ok(rec, total_tiles, a.batch, a.tokens, 1, nhb)) return;
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
-      mla_segment(a, rec, t - rec[5], chunk_end - rec[5], w, tpw, vt_all[wid], sx, lane, wid,
+      mla_segment(a, rec, t - rec[5], chunk_end - rec[5], w, tpw, vt_all[wid], sx, smax, lane, wid,
                   first, pre);
       first = false;
       t = chunk_end;
@@ -1862,6 +1913,8 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
   mg.out = out; mg.o_ts = o_ts; mg.o_hs = o_hs; mg.group = g.group; mg.hb = g.hb; mg.dv = dv;
   mg.nw = nw; mg.hkv = g.hkv; mg.rb = g.rb;
   mg.mrg = reinterpret_cast<const int32_t*>(ws + L.mrg); mg.mrg_cap = L.mrg_cap;
+  mg.part_f16 = dv == kMlaV ? 1 : 0;
+  mg.part_sc = reinterpret_cast<const float*>(ws + L.part_sc);
   const bool pf = L.pf_mrg_cap > 0;
   mg.pf_mrg = pf ? reinterpret_cast<const int4*>(ws + L.pfm) : nullptr;
   mg.pf_o = reinterpret_cast<const float*>(ws + L.pf_o);
@@ -2083,6 +2136,7 @@ extern "C" int aia_paged_attention_mla(
   a.wave_rec = reinterpret_cast<const int32_t*>(ws + L.wave);
   a.part_o = reinterpret_cast<float*>(ws + L.part_o);
   a.part_ml = reinterpret_cast<float2*>(ws + L.part_ml);
+  a.part_sc = reinterpret_cast<float*>(ws + L.part_sc);
   a.out = static_cast<uint16_t*>(out);
   a.o_ts = out_token_stride; a.o_hs = out_head_stride;
   a.waves = waves;

@@ -85,11 +85,14 @@ constexpr int kPfKeys = AIA_PF_KEYS;         // keys per staged K/V tile (32 or 
 constexpr int kPfTargetWgs = AIA_PF_TARGET;
 constexpr int kPfMinChunk = 8;
 
+constexpr int64_t kMlaRb2Rows = 2048;
+
 // rb: row blocks (of 16 query rows) per segment.  Two when a GQA launch's
 // requests average more query tokens than one block holds (prefill chunks),
-// so each K/V tile feeds 32 rows; one for decode, short verify steps and
-// MLA, whose segments fit one block.  Planner and kernels derive it from the
-// same (batch, tokens, head_dim_v), so they always agree.
+// so each K/V tile feeds 32 rows; one for decode and short verify steps.
+// MLA gets two on steps with more tokens than requests and at least
+// kMlaRb2Rows query rows.  Planner and kernels derive it from the same
+// (heads, batch, tokens, head_dim_v), so they always agree.
 Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_t dv) {
   Geometry g;
   g.hkv = hkv;
@@ -107,7 +110,12 @@ Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_
           ((int64_t)tokens - batch + 1) * g.group >= kPfRows) ? 1 : 0;
   // with prefill routing, requests with many query rows leave the split-K
   // kernel, whose segments are then decode / short-verify sized
-  g.rb = (!g.pf && dv == kHeadDim && tokens > (int64_t)batch * g.qb) ? 2 : 1;
+  // (MLA, dv 512: a token's heads fill a block.  Two blocks halve the
+  // latent reads per row but run two waves per SIMD instead of three, which
+  // only pays once the step has kMlaRb2Rows query rows to fill the chip;
+  // short verify steps of a few dozen requests stay at one block.)
+  const bool mla_rb2 = dv == 512 && (int64_t)tokens * hq >= kMlaRb2Rows;
+  g.rb = ((!g.pf && dv == kHeadDim) || mla_rb2) && tokens > (int64_t)batch * g.qb ? 2 : 1;
   g.qs = g.qb * g.rb;                                   // query tokens per segment
   return g;
 }
@@ -1685,6 +1693,11 @@ struct MlaArgs {
   int32_t batch, tokens;
 };
 
+// Processes key tiles [lt0, lt1) of one segment.  A segment holds RB blocks
+// of 16 rows; block r is the segment's query token r (qb = 1: a token's 16
+// heads fill a block), and every K tile (= V tile) feeds all blocks, so a
+// verify or prefill step reads its keys 1/RB as often.
+template <int RB>
 __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, int lt0, int lt1,
                                             int w, int tpw, uint16_t* vt, float* sx, float* smax,
                                             int lane, int wid, bool use_pre, int pre) {
@@ -1692,10 +1705,18 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
   const int b = rec[0], hbi = (rec[1] >> 16) & 0x3fff;
   const int qtok0 = rec[2], nq = rec[3] & 0xff, q0 = rec[3] >> 8, lim_base = rec[4];
   const int tile_begin = rec[5], tile_end = rec[6], part_base = rec[7];
-  const int qi = n / a.hb, hh = n - qi * a.hb;
-  const bool rv = qi < nq && hbi * a.hb + hh < a.group;
+  const int qb = kRows / a.hb;
+  const int nt = n / a.hb, hh = n - nt * a.hb;
   const int head = hbi * a.hb + hh;
-  const int lim = rv ? lim_base + qi : -1;
+  int qi[RB], lim[RB];
+  bool rv[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    qi[r] = r * qb + nt;
+    rv[r] = nt < qb && qi[r] < nq && head < a.group;
+    lim[r] = rv[r] ? lim_base + qi[r] : -1;
+  }
+  const int nblk = (nq + qb - 1) / qb;                // row blocks holding tokens
   const int visible = max(0, lim_base + nq);
   const bool has_rope = wid < 2;
   // 16-byte chunk index (within a 576-element row) of this lane's pieces
@@ -1708,21 +1729,29 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
   const int nblk_vis = (visible + a.bs - 1) / a.bs;
   int blk_base = 0, btv = 0, w1 = 0;
 
-  uint4 qf[5];
-  if (rv) {
-    const uint4* qp = reinterpret_cast<const uint4*>(
-        a.q + (int64_t)(qtok0 + qi) * a.q_ts + (int64_t)head * a.q_hs);
+  uint4 qf[RB][5];
 #pragma unroll
-    for (int j = 0; j < 5; ++j) qf[j] = (j < 4 || has_rope) ? qp[cidx[j]] : make_uint4(0, 0, 0, 0);
-  } else {
+  for (int r = 0; r < RB; ++r) {
+    if (rv[r]) {
+      const uint4* qp = reinterpret_cast<const uint4*>(
+          a.q + (int64_t)(qtok0 + qi[r]) * a.q_ts + (int64_t)head * a.q_hs);
 #pragma unroll
-    for (int j = 0; j < 5; ++j) qf[j] = make_uint4(0, 0, 0, 0);
+      for (int j = 0; j < 5; ++j) qf[r][j] = (j < 4 || has_rope) ? qp[cidx[j]] : make_uint4(0, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 5; ++j) qf[r][j] = make_uint4(0, 0, 0, 0);
+    }
   }
 
-  float4_t o[8];
+  float4_t o[RB][8];
+  float m[RB], lsum[RB];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m = -1e30f, lsum = 0.f;
+  for (int r = 0; r < RB; ++r) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[r][dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    m[r] = -1e30f;
+    lsum[r] = 0.f;
+  }
 
   auto load = [&](int lt, uint4 (&kk)[5]) {
     const bool live = lt < w1;
@@ -1743,48 +1772,66 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
       uint32_t x = 0;
 #pragma unroll
       for (int j = 0; j < 5; ++j) x ^= kk[j].x ^ kk[j].y ^ kk[j].z ^ kk[j].w;
-      o[0][0] += __uint_as_float(x & 0x3fffffu);
+      o[0][0][0] += __uint_as_float(x & 0x3fffffu);
       return;
     }
 #endif
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    // partial S^T over this wave's dims, one per row block; the 4 waves'
+    // partials are summed through LDS (double-buffered by tile parity)
+    float* xb = sx + parity * (4 * RB * 256);
 #pragma unroll
-    for (int j = 0; j < 5; ++j) {
-      if (j == 4 && !has_rope) break;
-      acc = qk_step(kk[j], qf[j], acc);
+    for (int r = 0; r < RB; ++r) {
+      float4_t acc = {0.f, 0.f, 0.f, 0.f};
+      if (r == 0 || r < nblk) {
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+          if (j == 4 && !has_rope) break;
+          acc = qk_step(kk[j], qf[r][j], acc);
+        }
+      }
+      *reinterpret_cast<float4_t*>(xb + (wid * RB + r) * 256 + lane * 4) = acc;
     }
-    float* xb = sx + parity * (4 * 256);
-    *reinterpret_cast<float4_t*>(xb + wid * 256 + lane * 4) = acc;
     // this wave's V slice (latent dims [128 w, +128)) is the K it holds
     stage_v(vt, n, g, reinterpret_cast<const uint4 (&)[4]>(kk));
     __syncthreads();
-    float4_t tot = *reinterpret_cast<const float4_t*>(xb + lane * 4);
-#pragma unroll
-    for (int ww = 1; ww < 4; ++ww) tot += *reinterpret_cast<const float4_t*>(xb + ww * 256 + lane * 4);
     parity ^= 1;
     const int tb = lt * kTile + 4 * g;
-    float sv[4];
+    short4_t pb[RB];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) sv[v] = (tb + v <= lim) ? tot[v] * a.scale_log2 : -INFINITY;
-    float tmax = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    tmax = aia::group4_max(tmax);
-    const float mnew = fmaxf(m, tmax);
-    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-    float p[4];
+    for (int r = 0; r < RB; ++r) {
+      float4_t tot = *reinterpret_cast<const float4_t*>(xb + r * 256 + lane * 4);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) p[v] = __builtin_amdgcn_exp2f(sv[v] - mnew);
-    lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    m = mnew;
+      for (int ww = 1; ww < 4; ++ww)
+        tot += *reinterpret_cast<const float4_t*>(xb + (ww * RB + r) * 256 + lane * 4);
+      float sv[4];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
-    const short4_t pb = as_s4(aia::pack_bf16x2(p[0], p[1]), aia::pack_bf16x2(p[2], p[3]));
+      for (int v = 0; v < 4; ++v) sv[v] = (tb + v <= lim[r]) ? tot[v] * a.scale_log2 : -INFINITY;
+      float tmax = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+      tmax = aia::group4_max(tmax);
+      const float mnew = fmaxf(m[r], tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m[r] - mnew);
+      float p[4];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt_frag(vt, n, g, dt), pb, o[dt], 0, 0, 0);
+      for (int v = 0; v < 4; ++v) p[v] = __builtin_amdgcn_exp2f(sv[v] - mnew);
+      lsum[r] = lsum[r] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+      m[r] = mnew;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[r][dt] *= alpha;
+      pb[r] = as_s4(aia::pack_bf16x2(p[0], p[1]), aia::pack_bf16x2(p[2], p[3]));
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const short4_t va = vt_frag(vt, n, g, dt);
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+        if (r == 0 || r < nblk)
+          o[r][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb[r], o[r][dt], 0, 0, 0);
+    }
     __builtin_amdgcn_wave_barrier();
   };
 
-  uint4 kbuf[kMlaPipe][5];
+  constexpr int kP = kMlaPipe;
+  uint4 kbuf[kP][5];
   for (int w0 = lt0; w0 < lt1;) {
     blk_base = (w0 * kTile) / a.bs;
     const int win = use_pre ? kRecBlocks : 64;
@@ -1793,35 +1840,39 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
     else btv = blk_base + lane < nblk_vis ? btrow[blk_base + lane] : 0;
     use_pre = false;
 #pragma unroll
-    for (int i = 0; i < kMlaPipe; ++i) {
+    for (int i = 0; i < kP; ++i) {
       load(w0 + i, kbuf[i]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    for (int base = w0; base < w1; base += kMlaPipe) {
+    for (int base = w0; base < w1; base += kP) {
 #pragma unroll
-      for (int i = 0; i < kMlaPipe; ++i) {
+      for (int i = 0; i < kP; ++i) {
         const int lt = base + i;
         if (lt < w1) compute(lt, kbuf[i]);
-        load(lt + kMlaPipe, kbuf[i]);
+        load(lt + kP, kbuf[i]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
     w0 = w1;
   }
 
-  lsum = aia::group4_sum(lsum);
+#pragma unroll
+  for (int r = 0; r < RB; ++r) lsum[r] = aia::group4_sum(lsum[r]);
   const int first_wave = tile_begin / tpw;
   const int nparts = (tile_end - 1) / tpw - first_wave + 1;
   const int d0 = 128 * wid;
+  constexpr int seg_rows = RB * kRows;
   if (nparts == 1) {
-    if (rv) {
-      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-      uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs + d0;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      if (!rv[r]) continue;
+      const float inv = lsum[r] > 0.f ? 1.f / lsum[r] : 0.f;
+      uint16_t* op = a.out + (int64_t)(qtok0 + qi[r]) * a.o_ts + (int64_t)head * a.o_hs + d0;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         uint2 wv;
-        wv.x = aia::pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
-        wv.y = aia::pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
+        wv.x = aia::pack_bf16x2(o[r][dt][0] * inv, o[r][dt][1] * inv);
+        wv.y = aia::pack_bf16x2(o[r][dt][2] * inv, o[r][dt][3] * inv);
         *reinterpret_cast<uint2*>(op + 16 * dt + 4 * g) = wv;
       }
     }
@@ -1830,29 +1881,36 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
     // row's 512 dims (all 4 waves), so y is in [-1, 1] with 11 mantissa bits
     // relative to the row's largest value -- finer than the bf16 output --
     // and half the bytes of fp32 partials.  The merge multiplies back by c.
-    float mx = 0.f;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
+    for (int r = 0; r < RB; ++r) {
+      float mx = 0.f;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) mx = fmaxf(mx, fabsf(o[dt][v]));
-    mx = aia::group4_max(mx);
-    if (g == 0) smax[wid * kRows + n] = mx;
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) mx = fmaxf(mx, fabsf(o[r][dt][v]));
+      mx = aia::group4_max(mx);
+      if (g == 0) smax[(wid * RB + r) * kRows + n] = mx;
+    }
     __syncthreads();
-    const float c = fmaxf(fmaxf(smax[n], smax[kRows + n]), fmaxf(smax[2 * kRows + n], smax[3 * kRows + n]));
     const int part = part_base + (w - first_wave);
-    if (rv) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const float c = fmaxf(fmaxf(smax[r * kRows + n], smax[(RB + r) * kRows + n]),
+                            fmaxf(smax[(2 * RB + r) * kRows + n], smax[(3 * RB + r) * kRows + n]));
+      if (!rv[r]) continue;
       const float inv = c > 0.f ? 1.f / c : 0.f;
-      uint16_t* pp = reinterpret_cast<uint16_t*>(a.part_o) + ((int64_t)part * kRows + n) * kMlaV + d0;
+      const int64_t prow = (int64_t)part * seg_rows + r * kRows + n;
+      uint16_t* pp = reinterpret_cast<uint16_t*>(a.part_o) + prow * kMlaV + d0;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         uint2 wv;
-        wv.x = pack_f16x2(o[dt][0] * inv, o[dt][1] * inv);
-        wv.y = pack_f16x2(o[dt][2] * inv, o[dt][3] * inv);
+        wv.x = pack_f16x2(o[r][dt][0] * inv, o[r][dt][1] * inv);
+        wv.y = pack_f16x2(o[r][dt][2] * inv, o[r][dt][3] * inv);
         *reinterpret_cast<uint2*>(pp + 16 * dt + 4 * g) = wv;
       }
       if (g == 0 && wid == 0) {
-        a.part_ml[(int64_t)part * kRows + n] = make_float2(m, lsum);
-        a.part_sc[(int64_t)part * kRows + n] = c;
+        a.part_ml[prow] = make_float2(m[r], lsum[r]);
+        a.part_sc[prow] = c;
       }
     }
   }
@@ -1863,11 +1921,14 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
 #ifndef AIA_MLA_WAVES_PER_EU
 #define AIA_MLA_WAVES_PER_EU 3
 #endif
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AIA_MLA_WAVES_PER_EU)))
+// The two-row-block instantiation (verify / prefill steps) needs more
+// registers: two waves per SIMD.
+template <int RB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RB == 1 ? AIA_MLA_WAVES_PER_EU : 2)))
 void mla_attn_kernel(MlaArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vt_all[4][kTile * kVStride];
-  __shared__ __attribute__((aligned(16))) float sx[2 * 4 * 256];
-  __shared__ float smax[4 * kRows];
+  __shared__ __attribute__((aligned(16))) float sx[2 * 4 * RB * 256];
+  __shared__ float smax[4 * RB * kRows];
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int w = blockIdx.x;   // one tile range per work-group
@@ -1890,8 +1951,8 @@ void mla_attn_kernel(MlaArgs a) {
     if (!rec_ok(rec, total_tiles, a.batch, a.tokens, 1, nhb)) return;
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
-      mla_segment(a, rec, t - rec[5], chunk_end - rec[5], w, tpw, vt_all[wid], sx, smax, lane, wid,
-                  first, pre);
+      mla_segment<RB>(a, rec, t - rec[5], chunk_end - rec[5], w, tpw, vt_all[wid], sx, smax, lane,
+                      wid, first, pre);
       first = false;
       t = chunk_end;
       if (t >= t_end) break;
@@ -2143,7 +2204,8 @@ extern "C" int aia_paged_attention_mla(
   a.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
   a.batch = batch; a.tokens = num_tokens;
   hipStream_t s = (hipStream_t)stream;
-  mla_attn_kernel<<<waves, 256, 0, s>>>(a);
+  if (g.rb == 2) mla_attn_kernel<2><<<waves, 256, 0, s>>>(a);
+  else mla_attn_kernel<1><<<waves, 256, 0, s>>>(a);
   if (int rc = check_hip(hipGetLastError(), "mla_attn_kernel launch")) return rc;
   if (flags & AIA_ATTN_SKIP_MERGE) return AIA_OK;
   return launch_merge(ws, L, g, 1, kMlaV, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,

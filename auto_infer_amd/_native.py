@@ -47,6 +47,7 @@ SIGNATURES = {
                           c_vp],
     "aia_mla_q_latent": [c_vp, c_i64, c_i64, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp,
                          c_i64, c_i64, c_vp],
+    "aia_mla_v_up": [c_vp, c_i64, c_i64, c_i32, c_i32, c_vp, c_vp, c_i64, c_i64, c_vp],
     "aia_mtp_compact": [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32,
                         c_i32, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp],
 }

@@ -52,7 +52,9 @@ class MlaHipBackend(AttentionBackend):
         self._absorb_w = {}
         # With fuse_pre_attention, q_latent and k_latent each come from one
         # kernel (norm / interleave / RoPE / W_UK product / cat; bf16 rounding
-        # where the torch ops round) when the shapes allow it (nope 128).
+        # where the torch ops round) when the shapes allow it (nope 128), and
+        # the W_UV product after attention from a third (v_head_dim 128, up to
+        # ops.MLA_V_UP_MAX_ROWS query rows; longer steps use the library GEMM).
         self.fuse_pre_attention = fuse_pre_attention
 
     def alloc_kv_caches(self, num_blocks: int, block_size: int) -> list:
@@ -102,7 +104,8 @@ class MlaHipBackend(AttentionBackend):
         q = q.view(T, nh, nope + rope)
         ckv_full = x @ w[p + "self_attn.kv_a_proj_with_mqa.weight"].t()
         w_uk, w_uv, w_uk_t = self._weights(layer_idx)
-        if self._fusable(q, ckv_full, ctx):
+        fused = self._fusable(q, ckv_full, ctx)
+        if fused:
             q_latent = ops.mla_q_latent(q, w_uk_t, ctx.cos, ctx.sin)
             k_latent = ops.mla_kv_latent(ckv_full, w[p + "self_attn.kv_a_layernorm.weight"],
                                          self.rms_eps, ctx.cos, ctx.sin)
@@ -120,7 +123,10 @@ class MlaHipBackend(AttentionBackend):
             k_latent = torch.cat([ckv.unsqueeze(1), k_pe], dim=-1).contiguous()
         self._write_kv(layer_idx, k_latent, None, ctx)
         o_latent = self._attn(layer_idx, q_latent, k_latent, None, ctx)
-        o = torch.einsum("tnl,nvl->tnv", o_latent, w_uv)
+        if fused and vd == 128 and T * nh <= ops.MLA_V_UP_MAX_ROWS:
+            o = ops.mla_v_up(o_latent, w_uv)
+        else:
+            o = torch.einsum("tnl,nvl->tnv", o_latent, w_uv)
         return o.reshape(T, nh * vd) @ w[p + "self_attn.o_proj.weight"].t()
 
     def _write_kv(self, layer_idx, k, v, ctx) -> None:

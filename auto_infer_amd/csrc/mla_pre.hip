@@ -1,5 +1,6 @@
-// Absorbed-MLA pre-attention: the latent query and the latent KV row of each
-// token, each in one launch.
+// Absorbed-MLA pre- and post-attention: the latent query and the latent KV
+// row of each token, each in one launch, and the W_UV value up-projection of
+// the attention output (mla.py:120-121).
 //
 // Reference (auto_infer/layers/attention/mla.py:86-113, mla_paged_absorbed):
 //   q_nope, q_pe = q.split([nope, rope])            q (T, H, nope + rope)
@@ -172,6 +173,75 @@ __global__ __launch_bounds__(256) void mla_q_latent_kernel(QArgs a) {
               a.out + (int64_t)tt * a.out_ts + (int64_t)h * a.out_hs + kLatent, k);
 }
 
+struct UvArgs {
+  const uint16_t* o;        // o_latent rows (T, H, >= 512), strides o_ts / o_hs
+  int64_t o_ts, o_hs;
+  const uint16_t* w;        // W_UV (H, 128, 512) contiguous
+  uint16_t* out;            // (T, H, 128) rows, strides out_ts / out_hs
+  int64_t out_ts, out_hs;
+  int32_t tokens;
+};
+
+// Value up-projection after absorbed attention, per head h:
+// out[t][h][v] = sum_l o_latent[t][h][l] W_UV[h][v][l].  Computed as
+// out^T (v x tokens) = W_UV[h] (v x 512) . o_latent^T (512 x tokens) on
+// v_mfma_f32_16x16x32_bf16, both operands 16-byte contiguous along l:
+// lane (v m, group g) loads W_UV[h][v0 + m][32 j + 8 g, +8) (A) and lane
+// (token n, g) loads o_latent[t][h][32 j + 8 g, +8) (B).  A work-group owns
+// 16 tokens x 32 v columns (grid z: quarter of 128) of one head; wave w sums
+// latent dims 128 w .. 128 w + 127 and wave 0 adds the four slices through
+// LDS, so every wave is short and a 64-token decode batch spreads over 256
+// work-groups.  Each work-group reads its 32 KB of W_UV, so the W_UV reads
+// grow with the token count: the kernel is for decode and verify batches.
+__global__ __launch_bounds__(256) void mla_v_up_kernel(UvArgs a) {
+  constexpr int KS = 4, kSteps = kLatent / 32 / KS;
+  __shared__ aia::float4_t red[KS - 1][2][64];
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int h = blockIdx.y, v0 = 32 * blockIdx.z;
+  const int t0 = blockIdx.x * 16;
+  const int tb = min(t0 + n, a.tokens - 1);           // rows past the end are not stored
+  const int l0 = ks * (kLatent / KS) + 8 * g;
+  const uint16_t* orow = a.o + (int64_t)tb * a.o_ts + (int64_t)h * a.o_hs + l0;
+  const uint16_t* w0 = a.w + ((int64_t)h * kNope + v0 + n) * kLatent + l0;
+  const uint16_t* w1 = w0 + 16 * kLatent;
+  // every operand load is issued before the first MFMA: one memory round
+  // trip per wave instead of one per 32-dim step
+  uint4 b[kSteps], x0[kSteps], x1[kSteps];
+#pragma unroll
+  for (int j = 0; j < kSteps; ++j) {
+    b[j] = *reinterpret_cast<const uint4*>(orow + 32 * j);
+    x0[j] = *reinterpret_cast<const uint4*>(w0 + 32 * j);
+    x1[j] = *reinterpret_cast<const uint4*>(w1 + 32 * j);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  aia::float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < kSteps; ++j) {
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(x0[j]), as_b8(b[j]), acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(x1[j]), as_b8(b[j]), acc1, 0, 0, 0);
+  }
+  if (ks > 0) {
+    red[ks - 1][0][lane] = acc0;
+    red[ks - 1][1][lane] = acc1;
+  }
+  __syncthreads();
+  if (ks > 0) return;
+#pragma unroll
+  for (int k = 0; k < KS - 1; ++k) {
+    const aia::float4_t r0 = red[k][0][lane], r1 = red[k][1][lane];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { acc0[i] += r0[i]; acc1[i] += r1[i]; }
+  }
+  if (t0 + n < a.tokens) {
+    uint16_t* dst = a.out + (int64_t)(t0 + n) * a.out_ts + (int64_t)h * a.out_hs + v0 + 4 * g;
+    *reinterpret_cast<uint2*>(dst) =
+        make_uint2(aia::pack_bf16x2(acc0[0], acc0[1]), aia::pack_bf16x2(acc0[2], acc0[3]));
+    *reinterpret_cast<uint2*>(dst + 16) =
+        make_uint2(aia::pack_bf16x2(acc1[0], acc1[1]), aia::pack_bf16x2(acc1[2], acc1[3]));
+  }
+}
+
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
@@ -229,4 +299,28 @@ extern "C" int aia_mla_q_latent(const void* q, int64_t q_token_stride, int64_t q
   const dim3 grid((unsigned)((num_tokens + 15) / 16), (unsigned)num_heads, kLatent / 128);
   mla_q_latent_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(a);
   return check_hip(hipGetLastError(), "mla_q_latent launch");
+}
+
+extern "C" int aia_mla_v_up(const void* o_latent, int64_t o_token_stride, int64_t o_head_stride,
+                            int32_t num_tokens, int32_t num_heads, const void* w_uv, void* out,
+                            int64_t out_token_stride, int64_t out_head_stride, void* stream) {
+  using namespace aia;
+  if (num_tokens < 0 || num_heads <= 0 || num_heads > 65535)
+    return fail(AIA_ERR_INVALID, "aia_mla_v_up: bad sizes");
+  if (num_tokens == 0) return AIA_OK;
+  if (!o_latent || !w_uv || !out) return fail(AIA_ERR_INVALID, "aia_mla_v_up: null pointer argument");
+  if (o_head_stride < kLatent || o_token_stride < (int64_t)num_heads * o_head_stride ||
+      o_token_stride % 8 || o_head_stride % 8 || out_head_stride < kNope ||
+      out_token_stride < (int64_t)num_heads * out_head_stride || out_token_stride % 4 ||
+      out_head_stride % 4 || !al16(o_latent) || !al16(w_uv) || ((uintptr_t)out & 7))
+    return fail(AIA_ERR_INVALID, "aia_mla_v_up: o_latent rows need 16-byte alignment with "
+                "strides a multiple of 8; out 8-byte alignment with strides a multiple of 4");
+  UvArgs a;
+  a.o = static_cast<const uint16_t*>(o_latent); a.o_ts = o_token_stride; a.o_hs = o_head_stride;
+  a.w = static_cast<const uint16_t*>(w_uv);
+  a.out = static_cast<uint16_t*>(out); a.out_ts = out_token_stride; a.out_hs = out_head_stride;
+  a.tokens = num_tokens;
+  mla_v_up_kernel<<<dim3((unsigned)((num_tokens + 15) / 16), (unsigned)num_heads, 4), 256, 0,
+                     (hipStream_t)stream>>>(a);
+  return check_hip(hipGetLastError(), "mla_v_up launch");
 }

@@ -153,7 +153,7 @@ def other_configs(stream, only=None):
     with enough rotating caches to exceed the Infinity Cache, and the fused
     kernels either side of the path.  `only` selects one entry (its key:
     configs[1] .. configs[4], configs[1]_prefill, configs[1]_decode,
-    pre_attention, mla_pre_attention, mtp_compaction)."""
+    pre_attention, mla_pre_attention, mla_v_up, mtp_compaction)."""
     import time as _time
     import numpy as np
     from auto_infer_amd import ops, packing, workloads
@@ -305,6 +305,24 @@ def other_configs(stream, only=None):
             "shape": f"T {T}, H {H}, nope 128, rope {rope}, latent {kvl} (W_UK product on MFMA)",
             "fused_us": round(fused_us, 2), "torch_ops_us": round(torch_us, 2),
             "GBps": round(by / fused_us / 1e3, 1)}
+
+    if want("mla_v_up"):
+        note("absorbed-MLA W_UV value up-projection at the configs[2] batch and a 256-token verify step")
+        H, kvl = 16, 512
+        g = torch.Generator(device=dev).manual_seed(7)
+        w_uv = (torch.randn(H, 128, kvl, device=dev, generator=g) / 11).bfloat16()
+        for T in (64, 256):
+            o_lat = torch.randn(T, H, kvl, device=dev, generator=g).bfloat16()
+            o_buf = torch.empty(T, H, 128, device=dev, dtype=torch.bfloat16)
+            fused_us = _time_graph(lambda i: ops.mla_v_up(o_lat, w_uv, out=o_buf), stream, 5, 20)
+            torch_us = _time_graph(lambda i: torch.einsum("tnl,nvl->tnv", o_lat, w_uv), stream, 5, 20)
+            by = (o_lat.numel() + w_uv.numel() + o_buf.numel()) * 2
+            res[f"mla_v_up_T{T}"] = {
+                "shape": f"T {T}, H {H}, latent {kvl} -> v 128 (mla.py:121 einsum on MFMA)",
+                "fused_us": round(fused_us, 2), "torch_ops_us": round(torch_us, 2),
+                "GBps": round(by / fused_us / 1e3, 1),
+                "frac_of_peak": round(by / fused_us / 1e3 / HBM_PEAK_GBS, 4)}
+            del o_lat, o_buf
 
     if want("mtp_compaction"):
         note("MTP verify compaction at the configs[3] gear")

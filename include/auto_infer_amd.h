@@ -214,6 +214,17 @@ int aia_mla_q_latent(const void* q, int64_t q_token_stride, int64_t q_head_strid
                      int64_t cos_token_stride, const void* sin, int64_t sin_token_stride,
                      void* out, int64_t out_token_stride, int64_t out_head_stride, void* stream);
 
+/* Absorbed-MLA value up-projection, one launch.  Replaces
+ * einsum("tnl,nvl->tnv", o_latent, W_UV) of mla_paged_absorbed (mla.py:121):
+ * out[t][h][v] = sum_l o_latent[t][h][l] * W_UV[h][v][l] with fp32
+ * accumulation on MFMA and one bf16 rounding.  o_latent (T, H, >= 512) bf16
+ * (the attention output; the first 512 dims are read), w_uv (H, 128, 512)
+ * contiguous (build_absorb_weights, mla.py:67-73), out (T, H, 128): with
+ * out_token_stride = H * 128 it is the (T, H * 128) input of o_proj. */
+int aia_mla_v_up(const void* o_latent, int64_t o_token_stride, int64_t o_head_stride,
+                 int32_t num_tokens, int32_t num_heads, const void* w_uv, void* out,
+                 int64_t out_token_stride, int64_t out_head_stride, void* stream);
+
 /* On-device MTP verify compaction, one launch.  Replaces the accept/compact
  * block of GraphMtpRunner._target_body (auto_infer/worker/
  * graph_mtp_runner.py:224-248): for a gear of `gear` (<= 64) requests of

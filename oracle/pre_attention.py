@@ -125,6 +125,14 @@ def mla_q_latent(q, w_uk, cos, sin):
     return torch.cat([absorbed, q_pe], dim=-1)
 
 
+def mla_v_up(o_latent, w_uv):
+    """mla.py:120-121: o = einsum("tnl,nvl->tnv", o_latent[..., :kvl], W_UV)
+    for o_latent (T, H, >= kvl) and W_UV (H, vd, kvl).  A bf16 GEMM: fp32
+    products and sums, one rounding to bf16."""
+    kvl = w_uv.shape[2]
+    return torch.einsum("tnl,nvl->tnv", o_latent[..., :kvl].float(), w_uv.float()).to(o_latent.dtype)
+
+
 def mla_latents_f64(q, w_uk, ckv_full, norm_weight, eps, positions, kv_lora_rank=512,
                     base=10000.0):
     """q_latent and k_latent in float64 with exact angles (no rounding)."""

@@ -237,7 +237,8 @@ def test_gqa_backend_long_prefill_on_prefill_kernel():
 def test_mla_fused_pre_attention_matches_torch_path():
     """The latent-query and latent-KV kernels against the torch ops they
     replace (split, rms_norm, ds_rope_interleave, RoPE, einsum with W_UK,
-    cat), end to end through attention() with DeepSeek-V2-Lite head shapes
+    cat), and the W_UV kernel against the einsum after attention, end to end
+    through attention() with DeepSeek-V2-Lite head shapes
     (nope 128, rope 64, latent 512): the latent caches within one bf16 ulp of
     each row's largest value (the norm's sum order), outputs within 2e-2."""
     g = torch.Generator().manual_seed(9)

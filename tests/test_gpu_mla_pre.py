@@ -1,5 +1,6 @@
-"""Absorbed-MLA pre-attention kernels (latent query, latent KV row) vs the
-bf16 torch restatement in oracle/pre_attention.py.
+"""Absorbed-MLA pre-attention kernels (latent query, latent KV row) and the
+W_UV value up-projection vs the bf16 torch restatement in
+oracle/pre_attention.py.
 
 Bars: the RoPE parts are bit-exact (the kernels round where the torch ops
 round).  The normed latent is within one bf16 ulp of the row's largest value
@@ -12,7 +13,7 @@ import pytest
 import torch
 
 from auto_infer_amd import ops
-from oracle.pre_attention import mla_kv_latent, mla_q_latent, rope_tables
+from oracle.pre_attention import mla_kv_latent, mla_q_latent, mla_v_up, rope_tables
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -92,3 +93,36 @@ def test_rejects_bad_shapes():
     with pytest.raises(ValueError, match="ckv_full"):
         ops.mla_kv_latent(torch.zeros(4, 512, dtype=torch.bfloat16, device=DEV),
                           torch.zeros(512, dtype=torch.bfloat16, device=DEV), 1e-6, cos, cos)
+
+
+@pytest.mark.parametrize("T,H", [(1, 16), (7, 16), (64, 16), (65, 16), (300, 4), (200, 128),
+                                 (2049, 16)])
+def test_v_up_vs_oracle(T, H):
+    """Decode / verify sizes and, beyond the rows the backend routes to it,
+    long steps, with ragged last token tiles."""
+    g = torch.Generator().manual_seed(T * 7 + H)
+    o = (torch.randn(T, H, 512, generator=g) / 4).bfloat16()
+    w_uv = (torch.randn(H, 128, 512, generator=g) / 11).bfloat16()
+    got = ops.mla_v_up(o.to(DEV), w_uv.to(DEV)).cpu()
+    close_to_one_ulp(got, mla_v_up(o, w_uv), row_relative=False)
+
+
+def test_v_up_strided_views():
+    """o_latent as the first 512 dims of (T, H, 576) rows and out as a view of
+    the (T, H * 128) o_proj input give the same values as dense tensors."""
+    T, H = 33, 16
+    g = torch.Generator().manual_seed(5)
+    wide = (torch.randn(T, H, 576, generator=g) / 4).bfloat16().to(DEV)
+    w_uv = (torch.randn(H, 128, 512, generator=g) / 11).bfloat16().to(DEV)
+    flat = torch.full((T, H * 128), 7.0, dtype=torch.bfloat16, device=DEV)
+    ops.mla_v_up(wide, w_uv, out=flat.view(T, H, 128))
+    dense = ops.mla_v_up(wide[..., :512].contiguous(), w_uv)
+    assert torch.equal(flat.view(T, H, 128), dense)
+
+
+def test_v_up_rejects_bad_shapes():
+    o = torch.zeros(4, 16, 512, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="w_uv"):
+        ops.mla_v_up(o, torch.zeros(16, 512, 128, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(ValueError, match="o_latent"):
+        ops.mla_v_up(o[..., :256], torch.zeros(16, 128, 512, dtype=torch.bfloat16, device=DEV))

@@ -155,3 +155,29 @@ def test_mla_bf16_restatement_tracks_float64():
     for got, exp in ((ql[..., 512:], el[..., 512:]), (kl, ek)):
         row = exp.abs().amax(dim=-1, keepdim=True)
         assert bool(((got - exp).abs() <= row * 2.0 ** -6).all())
+
+
+def test_mla_v_up_is_the_non_absorbed_value_path():
+    """Absorbed == non-absorbed for the value side (the identity the
+    reference states at mla.py:80-84 and checks in
+    scripts/verify_mla_absorb.py:114-141): with attention weights P over the
+    latent rows ckv, mla_v_up(P ckv, W_UV) equals P V where V is built the
+    non-absorbed way, straight from kv_b_proj: (ckv kv_b^T).view(T, H, nope +
+    vd)[..., nope:].  A wrong head index or a transposed W_UV fails it; the
+    bf16 restatement is within one bf16 ulp plus fp32 reassociation."""
+    from oracle.pre_attention import mla_v_up
+    from auto_infer_amd.attention.mla import build_absorb_weights
+    g = torch.Generator().manual_seed(9)
+    T, H, nope, vd, kvl, L = 5, 3, 128, 128, 512, 7
+    kv_b = torch.randn(H * (nope + vd), kvl, generator=g, dtype=torch.float64) / 20
+    ckv = torch.randn(L, kvl, generator=g, dtype=torch.float64)
+    P = torch.softmax(torch.randn(T, H, L, generator=g, dtype=torch.float64), dim=-1)
+    v = (ckv @ kv_b.T).view(L, H, nope + vd)[..., nope:]             # (L, H, vd)
+    expect = torch.einsum("thl,lhv->thv", P, v)
+    _, w_uv = build_absorb_weights(kv_b, H, nope, vd, kvl)
+    o_latent = torch.einsum("thl,lk->thk", P, ckv)                      # (T, H, kvl)
+    got = mla_v_up(o_latent, w_uv)
+    assert torch.allclose(got, expect, rtol=1e-5, atol=1e-6)     # fp32 sums
+    got16 = mla_v_up(o_latent.bfloat16(), w_uv.bfloat16()).double()
+    exact = torch.einsum("thl,hvl->thv", o_latent.bfloat16().double(), w_uv.bfloat16().double())
+    assert bool(((got16 - exact).abs() <= exact.abs() * 2.0 ** -8 + 1e-6).all())

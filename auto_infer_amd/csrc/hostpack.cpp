@@ -15,6 +15,8 @@
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
 
+#include <cstdint>
+
 namespace {
 
 struct Ref {            // owned reference
@@ -296,7 +298,88 @@ PyObject* build_rows(PyObject*, PyObject* args) {
                        all_decode ? Py_True : Py_False, qacc, width);
 }
 
+// list of ints -> int64 / int32 array; a_width != 0: out[k] = a[k] * a_width + b[k]
+// (a and b are lists or tuples: PySequence_Fast_ITEMS reads both)
+bool fill_ll(PyObject* a, PyObject* b, long long a_width, long long* out, Py_ssize_t n) {
+  bool err = false;
+  PyObject** ai = PySequence_Fast_ITEMS(a);
+  PyObject** bi = b ? PySequence_Fast_ITEMS(b) : nullptr;
+  for (Py_ssize_t k = 0; k < n && !err; ++k) {
+    long long v = as_ll(ai[k], &err);
+    if (bi) v = v * a_width + as_ll(bi[k], &err);
+    out[k] = v;
+  }
+  return !err;
+}
+
+bool fill_i32(PyObject* a, int* out, Py_ssize_t n) {
+  bool err = false;
+  PyObject** ai = PySequence_Fast_ITEMS(a);
+  for (Py_ssize_t k = 0; k < n && !err; ++k) {
+    const long long v = as_ll(ai[k], &err);
+    if (v < INT32_MIN || v > INT32_MAX) {
+      PyErr_SetString(PyExc_OverflowError, "value does not fit int32");
+      return false;
+    }
+    out[k] = (int)v;
+  }
+  return !err;
+}
+
+PyObject* get_list(PyObject* o, const char* name) {
+  PyObject* v = PyObject_GetAttrString(o, name);
+  if (v && !PyList_Check(v)) {
+    Py_DECREF(v);
+    PyErr_Format(PyExc_TypeError, "updates.%s must be a list", name);
+    return nullptr;
+  }
+  return v;
+}
+
+// Writes one step's uploads into host memory at `base` (the upload layout of
+// _Uploader.upload: token pool index / value int64, block pool index int64 /
+// value int32, row descriptors int32 x row_ints), at the byte offsets the
+// caller computed for these list lengths.
+PyObject* stage(PyObject*, PyObject* args) {
+  PyObject* upd;
+  unsigned long long base;
+  long long tw, bw, o0, o1, o2, o3, o4, row_ints;
+  if (!PyArg_ParseTuple(args, "OKLLLLLLLL", &upd, &base, &tw, &bw, &o0, &o1, &o2, &o3, &o4,
+                        &row_ints))
+    return nullptr;
+  char* h = reinterpret_cast<char*>(base);
+  Ref ts(get_list(upd, "tok_slot")), ti(get_list(upd, "tok_idx")), tv(get_list(upd, "tok_val"));
+  Ref bsl(get_list(upd, "blk_slot")), bi(get_list(upd, "blk_idx")), bv(get_list(upd, "blk_val"));
+  Ref rows(get_list(upd, "rows"));
+  if (!ts || !ti || !tv || !bsl || !bi || !bv || !rows) return nullptr;
+  const Py_ssize_t nt = PyList_GET_SIZE(ti.get()), nb = PyList_GET_SIZE(bi.get());
+  const Py_ssize_t nr = PyList_GET_SIZE(rows.get());
+  if (PyList_GET_SIZE(ts.get()) != nt || PyList_GET_SIZE(tv.get()) != nt ||
+      PyList_GET_SIZE(bsl.get()) != nb || PyList_GET_SIZE(bv.get()) != nb) {
+    PyErr_SetString(PyExc_ValueError, "update lists differ in length");
+    return nullptr;
+  }
+  if (!fill_ll(ts.get(), ti.get(), tw, reinterpret_cast<long long*>(h + o0), nt) ||
+      !fill_ll(tv.get(), nullptr, 0, reinterpret_cast<long long*>(h + o1), nt) ||
+      !fill_ll(bsl.get(), bi.get(), bw, reinterpret_cast<long long*>(h + o2), nb) ||
+      !fill_i32(bv.get(), reinterpret_cast<int*>(h + o3), nb))
+    return nullptr;
+  int* rp = reinterpret_cast<int*>(h + o4);
+  for (Py_ssize_t r = 0; r < nr; ++r) {
+    PyObject* row = PyList_GET_ITEM(rows.get(), r);
+    if (!PyTuple_Check(row) || PyTuple_GET_SIZE(row) != row_ints) {
+      PyErr_SetString(PyExc_ValueError, "row descriptors must be tuples of row_ints ints");
+      return nullptr;
+    }
+    if (!fill_i32(row, rp + r * row_ints, row_ints)) return nullptr;
+  }
+  Py_RETURN_NONE;
+}
+
 PyMethodDef methods[] = {
+    {"stage", stage, METH_VARARGS,
+     "stage(updates, host_address, token_width, block_width, off_tok_idx, off_tok_val, "
+     "off_blk_idx, off_blk_val, off_rows, row_ints) -> None"},
     {"build_rows", build_rows, METH_VARARGS,
      "build_rows(table, scheduled, get_request, block_tables, block_size, updates, live) -> "
      "(cu_seqlens_q, seqlens_kv, sample_idx, decode_splice, all_decode, tokens, width)"},

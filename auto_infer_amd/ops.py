@@ -13,12 +13,14 @@ from auto_infer_amd import _native
 _BF16 = torch.bfloat16
 
 
+# Pointers and streams go to the C-ABI as plain ints: every pointer
+# parameter is declared c_void_p, which converts them (and None -> NULL).
 def _stream(device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 def _ptr(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    return t.data_ptr() if t is not None else None
 
 
 def _require(cond, msg):

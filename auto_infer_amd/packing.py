@@ -168,6 +168,26 @@ class _Updates:
         self.rows.append((slot, start, n, nblocks, base, q_off, zero_tokens, sample_slot))
 
 
+def _stage_py(upd, h, token_width, block_width, offs):
+    """Writes one step's uploads into the uint8 host array h at offs (token
+    pool index / value int64, block pool index int64 / value int32, row
+    descriptors int32): the specification of ``_hostpack.stage``."""
+    nt, nb, nr = len(upd.tok_idx), len(upd.blk_idx), len(upd.rows)
+    if nt:
+        h[offs[0]:offs[0] + nt * 8].view(np.int64)[:] = (
+            np.asarray(upd.tok_slot, dtype=np.int64) * token_width +
+            np.asarray(upd.tok_idx, dtype=np.int64))
+        h[offs[1]:offs[1] + nt * 8].view(np.int64)[:] = upd.tok_val
+    if nb:
+        h[offs[2]:offs[2] + nb * 8].view(np.int64)[:] = (
+            np.asarray(upd.blk_slot, dtype=np.int64) * block_width +
+            np.asarray(upd.blk_idx, dtype=np.int64))
+        h[offs[3]:offs[3] + nb * 4].view(np.int32)[:] = upd.blk_val
+    if nr:
+        h[offs[4]:offs[4] + nr * _ROW_INTS * 4].view(np.int32)[:] = np.asarray(
+            upd.rows, dtype=np.int32).reshape(-1)
+
+
 class _Uploader:
     """Pinned host staging -> one device buffer per step.  Two host buffers
     alternate; before one is rewritten, the copy that last read it is waited
@@ -177,10 +197,12 @@ class _Uploader:
         self.device = torch.device(device)
         self._host = [None, None]
         self._event = [None, None]
+        self._used = [False, False]
         self._dev = None
         self._turn = 0
+        self._views = {}           # (turn, bytes) -> (device slice, host slice)
 
-    def upload(self, upd, token_width, block_width):
+    def upload(self, upd, token_width, block_width, stream=None):
         nt, nb, nr = len(upd.tok_idx), len(upd.blk_idx), len(upd.rows)
         sizes = [nt * 8, nt * 8, nb * 8, nb * 4, nr * _ROW_INTS * 4]
         offs, total = [], 0
@@ -190,34 +212,30 @@ class _Uploader:
         total = max(total, 16)
         i = self._turn
         self._turn ^= 1
-        if self._event[i] is not None:
+        if self._used[i]:
             self._event[i].synchronize()
         host = self._host[i]
         if host is None or host.numel() < total:
             cap = max(total * 2, 4096)
             host = torch.empty(cap, dtype=torch.uint8, pin_memory=self.device.type == "cuda")
             self._host[i] = host
+            self._views.clear()
         if self._dev is None or self._dev.numel() < total:
             self._dev = torch.empty(max(total * 2, 4096), dtype=torch.uint8, device=self.device)
-        h = host.numpy()
-        if nt:
-            h[offs[0]:offs[0] + nt * 8].view(np.int64)[:] = (
-                np.asarray(upd.tok_slot, dtype=np.int64) * token_width +
-                np.asarray(upd.tok_idx, dtype=np.int64))
-            h[offs[1]:offs[1] + nt * 8].view(np.int64)[:] = upd.tok_val
-        if nb:
-            h[offs[2]:offs[2] + nb * 8].view(np.int64)[:] = (
-                np.asarray(upd.blk_slot, dtype=np.int64) * block_width +
-                np.asarray(upd.blk_idx, dtype=np.int64))
-            h[offs[3]:offs[3] + nb * 4].view(np.int32)[:] = upd.blk_val
-        if nr:
-            h[offs[4]:offs[4] + nr * _ROW_INTS * 4].view(np.int32)[:] = np.asarray(
-                upd.rows, dtype=np.int32).reshape(-1)
-        self._dev[:total].copy_(host[:total], non_blocking=True)
+            self._views.clear()
+        if _hostpack is not None:
+            _hostpack.stage(upd, host.data_ptr(), token_width, block_width, *offs, _ROW_INTS)
+        else:
+            _stage_py(upd, host.numpy(), token_width, block_width, offs)
+        views = self._views.get((i, total))
+        if views is None:
+            views = self._views[(i, total)] = (self._dev[:total], host[:total])
+        views[0].copy_(views[1], non_blocking=True)
         if self.device.type == "cuda":
-            ev = torch.cuda.Event()
-            ev.record(torch.cuda.current_stream(self.device))
-            self._event[i] = ev
+            if self._event[i] is None:
+                self._event[i] = torch.cuda.Event()
+            self._event[i].record(stream or torch.cuda.current_stream(self.device))
+            self._used[i] = True
         base = self._dev.data_ptr()
         return [base + o for o in offs]
 
@@ -235,8 +253,10 @@ class PackedStep:
 
 
 def _launch(table, uploader, upd, *, block_size, bt_width, token_ids, positions, slot_mapping,
-            block_table, cu, kv, last_rows, sample_rows=None, sample_count=0):
-    ptrs = uploader.upload(upd, table.token_pool.shape[1], table.block_pool.shape[1])
+            block_table, cu, kv, last_rows, sample_rows=None, sample_count=0, stream=None):
+    if stream is None:
+        stream = torch.cuda.current_stream(table.device)
+    ptrs = uploader.upload(upd, table.token_pool.shape[1], table.block_pool.shape[1], stream)
     nt, nb, nr = len(upd.tok_idx), len(upd.blk_idx), len(upd.rows)
     cap = sample_rows.numel() if sample_rows is not None else 0
     _native.call(
@@ -244,7 +264,7 @@ def _launch(table, uploader, upd, *, block_size, bt_width, token_ids, positions,
         _ptr(table.token_pool), table.token_pool.shape[1], _ptr(table.block_pool),
         table.block_pool.shape[1], ptrs[4], nr, block_size, bt_width, _ptr(token_ids),
         _ptr(positions), _ptr(slot_mapping), _ptr(block_table), _ptr(cu), _ptr(kv),
-        _ptr(last_rows), _ptr(sample_rows), sample_count, cap, _stream(table.device))
+        _ptr(last_rows), _ptr(sample_rows), sample_count, cap, stream.cuda_stream)
 
 
 def _check_blocks(rid, blocks, end, block_size):
@@ -324,6 +344,7 @@ class DeviceBatchPacker:
         self.kv_buf = torch.zeros(n_seqs, dtype=torch.int32, device=dev)
         self.last_buf = torch.zeros(n_seqs, dtype=torch.int64, device=dev)
         self._tokens, self._seqs, self._blocks = n_tokens, n_seqs, n_blocks
+        self._views = {}           # (T, B, width) -> output views
 
     def build(self, plan, attn_backend=None, kv_caches=None, attn_mask=None):
         bs = self.block_size
@@ -338,18 +359,23 @@ class DeviceBatchPacker:
         if T > self._tokens or B > self._seqs or width > self._blocks:
             self._alloc(T * 2 if T > self._tokens else T, B * 2 if B > self._seqs else B,
                         width * 2 if width > self._blocks else width)
-        bt = self.block_table_buf[:B * width].view(B, width)
+        views = self._views.get((T, B, width))
+        if views is None:      # steady decode steps repeat their shape
+            views = self._views[(T, B, width)] = (
+                self.token_ids_buf[:T], self.positions_buf[:T], self.slot_mapping_buf[:T],
+                self.block_table_buf[:B * width].view(B, width), self.cu_buf[:B + 1],
+                self.kv_buf[:B])
+        bt = views[3]
         _launch(self.table, self._uploader, upd, block_size=bs, bt_width=width,
                 token_ids=self.token_ids_buf, positions=self.positions_buf,
                 slot_mapping=self.slot_mapping_buf, block_table=bt, cu=self.cu_buf,
                 kv=self.kv_buf, last_rows=self.last_buf)
         ctx = ForwardContext(
-            token_ids=self.token_ids_buf[:T], positions=self.positions_buf[:T],
-            slot_mapping=self.slot_mapping_buf[:T], block_table=bt, cu_seqlens_q=cu,
-            seqlens_kv=kv, attn_mask=attn_mask, attn_backend=attn_backend,
+            token_ids=views[0], positions=views[1], slot_mapping=views[2], block_table=bt,
+            cu_seqlens_q=cu, seqlens_kv=kv, attn_mask=attn_mask, attn_backend=attn_backend,
             kv_caches=kv_caches, is_decode=all_decode)
-        ctx.aia_cu_seqlens_q = self.cu_buf[:B + 1]
-        ctx.aia_seqlens_kv = self.kv_buf[:B]
+        ctx.aia_cu_seqlens_q = views[4]
+        ctx.aia_seqlens_kv = views[5]
         return ctx, sample_idx, decode_splice
 
 

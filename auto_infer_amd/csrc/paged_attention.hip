@@ -115,7 +115,8 @@ Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_
   // only pays once the step has kMlaRb2Rows query rows to fill the chip;
   // short verify steps of a few dozen requests stay at one block.)
   const bool mla_rb2 = dv == 512 && (int64_t)tokens * hq >= kMlaRb2Rows;
-  g.rb = ((!g.pf && dv == kHeadDim) || mla_rb2) && tokens > (int64_t)batch * g.qb ? 2 : 1;
+  g.rb = ((!g.pf && (dv == kHeadDim || dv == 64)) || mla_rb2) && tokens > (int64_t)batch * g.qb
+             ? 2 : 1;
   g.qs = g.qb * g.rb;                                   // query tokens per segment
   return g;
 }
@@ -693,9 +694,10 @@ __device__ __forceinline__ float4_t qk_step(uint4 kk, uint4 q, float4_t acc) {
 // 16x16x16 MFMA, in one instruction.  (The stores take vector values: an
 // aggregate copy of the tile registers keeps them in a private array, which
 // the compiler then places in LDS, serialising the load pipeline.)
-__device__ __forceinline__ void stage_v(uint16_t* vs, int n, int g, const uint4 (&vv)[4]) {
+template <int KJ>
+__device__ __forceinline__ void stage_v(uint16_t* vs, int n, int g, const uint4 (&vv)[KJ]) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(vs + n * kVStride + 32 * j + 8 * g) = as_u4(vv[j]);
+  for (int j = 0; j < KJ; ++j) *reinterpret_cast<u32x4_t*>(vs + n * kVStride + 32 * j + 8 * g) = as_u4(vv[j]);
 }
 template <int STRIDE = kVStride>
 __device__ __forceinline__ short4_t vt_frag(const uint16_t* vs, int n, int g, int dt) {
@@ -718,10 +720,12 @@ constexpr int kPipe = AIA_PIPE;
 // (qb = 16 / hb).  Every K/V tile is loaded once and used by all blocks, so a
 // prefill chunk reads its keys 1/RB as often; blocks past the segment's last
 // token are skipped (a uniform branch), so a decode segment costs one block.
-template <int RB>
+template <int RB, int D>
 __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, int s, int lt0,
                                             int lt1, int w, int tpw, uint16_t* vt, int lane,
                                             int wid, bool use_pre, int pre) {
+  constexpr int KJ = D / 32;   // 32-dim MFMA k-steps = 16-byte chunks per lane and row
+  constexpr int DT = D / 16;   // 16-dim output tiles
   const int n = lane & 15, g = lane >> 4;
   const int b = rec[0], kvh = (rec[1] & 0xffff) * a.nw + wid, hbi = (rec[1] >> 16) & 0x3fff;
   const int qtok0 = rec[2], nq = rec[3] & 0xff, q0 = rec[3] >> 8, lim_base = rec[4];
@@ -745,7 +749,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   for (int r = 0; r < RB; ++r) lim_lo = rv[r] ? min(lim_lo, lim[r]) : lim_lo;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) lim_lo = min(lim_lo, __shfl_xor(lim_lo, d));
-  const int row_elems = a.hkv * kHeadDim;
+  const int row_elems = a.hkv * D;
   // this step's new keys sit at positions [new_start, Lk); the request's last
   // query block (head block 0) owns writing them into the cache
   const int new_start = a.kn ? lim_base - q0 : 0x7fffffff;
@@ -756,26 +760,26 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   const int nblk_vis = (visible + a.bs - 1) / a.bs;
   int blk_base = 0, btv = 0, w1 = 0;
 
-  uint4 qf[RB][4];
+  uint4 qf[RB][KJ];
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
     if (rv[r]) {
       const uint4* qp = reinterpret_cast<const uint4*>(
           a.q + (int64_t)(qtok0 + qi[r]) * a.q_ts + (int64_t)head * a.q_hs);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) qf[r][j] = qp[4 * j + g];
+      for (int j = 0; j < KJ; ++j) qf[r][j] = qp[4 * j + g];
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) qf[r][j] = make_uint4(0, 0, 0, 0);
+      for (int j = 0; j < KJ; ++j) qf[r][j] = make_uint4(0, 0, 0, 0);
     }
   }
 
-  float4_t o[RB][8];
+  float4_t o[RB][DT];
   float m[RB], lsum[RB];
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[r][dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < DT; ++dt) o[r][dt] = float4_t{0.f, 0.f, 0.f, 0.f};
     m[r] = -1e30f;
     lsum[r] = 0.f;
   }
@@ -787,40 +791,40 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   // window's first key row, K and V, again: an L1 hit, and a different row
   // for every range, so no memory channel is hammered) so the load stream is
   // straight-line and the compiler can wait for each tile with an exact count.
-  auto load = [&](int lt, uint4 (&kk)[4], uint4 (&vv)[4], int64_t& wdst) {
+  auto load = [&](int lt, uint4 (&kk)[KJ], uint4 (&vv)[KJ], int64_t& wdst) {
     const bool live = lt < w1;
     const int tok = live ? min(lt * kTile + n, visible - 1) : blk_base * a.bs;
     const int bi = tok / a.bs;
     // block ids outside the pool are clamped so a bad table cannot fault
     const int blk = min(max(__shfl(btv, bi - blk_base), 0), a.nb - 1);
     const int off = tok - bi * a.bs;
-    const int64_t base = ((int64_t)blk * a.bs + off) * row_elems + (int64_t)kvh * kHeadDim;
+    const int64_t base = ((int64_t)blk * a.bs + off) * row_elems + (int64_t)kvh * D;
     const bool fresh = live && tok >= new_start;
     const int64_t nrow = (int64_t)(q_begin + tok - new_start);
     const uint4* kp = reinterpret_cast<const uint4*>(
-        fresh ? a.kn + nrow * a.kn_ts + (int64_t)kvh * kHeadDim : a.kc + base);
+        fresh ? a.kn + nrow * a.kn_ts + (int64_t)kvh * D : a.kc + base);
     const uint4* vp = reinterpret_cast<const uint4*>(
-        fresh ? a.vn + nrow * a.vn_ts + (int64_t)kvh * kHeadDim : a.vc + base);
+        fresh ? a.vn + nrow * a.vn_ts + (int64_t)kvh * D : a.vc + base);
     // cache slot this lane writes after the tile arrives (-1: nothing)
     wdst = (writer && fresh && lt * kTile + n < visible) ? base : (int64_t)-1;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) kk[j] = kp[4 * j + g];
+    for (int j = 0; j < KJ; ++j) kk[j] = kp[4 * j + g];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) vv[j] = vp[4 * j + g];
+    for (int j = 0; j < KJ; ++j) vv[j] = vp[4 * j + g];
   };
 
-  auto compute = [&](int lt, const uint4 (&kk)[4], const uint4 (&vv)[4], int64_t wdst) {
+  auto compute = [&](int lt, const uint4 (&kk)[KJ], const uint4 (&vv)[KJ], int64_t wdst) {
     if (wdst >= 0) {   // KV slot write of a new row (its bytes just arrived)
       uint4* kd = reinterpret_cast<uint4*>(a.kc + wdst);
       uint4* vd = reinterpret_cast<uint4*>(a.vc + wdst);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) { kd[4 * j + g] = kk[j]; vd[4 * j + g] = vv[j]; }
+      for (int j = 0; j < KJ; ++j) { kd[4 * j + g] = kk[j]; vd[4 * j + g] = vv[j]; }
     }
 #ifdef AIA_NOCOMPUTE
     {
       uint32_t x = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x ^= kk[j].x ^ kk[j].y ^ kk[j].z ^ kk[j].w ^ vv[j].x ^ vv[j].y ^ vv[j].z ^ vv[j].w;
+      for (int j = 0; j < KJ; ++j) x ^= kk[j].x ^ kk[j].y ^ kk[j].z ^ kk[j].w ^ vv[j].x ^ vv[j].y ^ vv[j].z ^ vv[j].w;
       o[0][0][0] += __uint_as_float(x & 0x3fffffu);
       return;
     }
@@ -831,7 +835,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
       acc[r] = float4_t{0.f, 0.f, 0.f, 0.f};
       if (r == 0 || r < nblk) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[r] = qk_step(kk[j], qf[r][j], acc[r]);
+        for (int j = 0; j < KJ; ++j) acc[r] = qk_step(kk[j], qf[r][j], acc[r]);
       }
     }
     stage_v(vt, n, g, vv);
@@ -858,7 +862,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
         const float alpha = __builtin_amdgcn_exp2f(m[r] - mnew);
         lsum[r] = lsum[r] * alpha + psum;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[r][dt] *= alpha;
+        for (int dt = 0; dt < DT; ++dt) o[r][dt] *= alpha;
       } else {
         lsum[r] += psum;
       }
@@ -867,7 +871,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
     }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
+    for (int dt = 0; dt < DT; ++dt) {
       const short4_t va = vt_frag(vt, n, g, dt);
 #pragma unroll
       for (int r = 0; r < RB; ++r)
@@ -877,7 +881,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
     __builtin_amdgcn_wave_barrier();
   };
 
-  uint4 kbuf[kPipe][4], vbuf[kPipe][4];
+  uint4 kbuf[kPipe][KJ], vbuf[kPipe][KJ];
   int64_t wbuf[kPipe];
   for (int w0 = lt0; w0 < lt1;) {
     blk_base = (w0 * kTile) / a.bs;
@@ -919,7 +923,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
       const float inv = lsum[r] > 0.f ? 1.f / lsum[r] : 0.f;
       uint16_t* op = a.out + (int64_t)(qtok0 + qi[r]) * a.o_ts + (int64_t)head * a.o_hs;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
+      for (int dt = 0; dt < DT; ++dt) {
         uint2 wv;
         wv.x = aia::pack_bf16x2(o[r][dt][0] * inv, o[r][dt][1] * inv);
         wv.y = aia::pack_bf16x2(o[r][dt][2] * inv, o[r][dt][3] * inv);
@@ -928,7 +932,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
     }
   } else {
     const int part = part_base + (w - first_wave);
-    if (a.fused_merge) {
+    if (D == 128 && a.fused_merge) {   // lanes x 2 dims cover a 128-wide row
       // In-kernel merge.  Partials go out with agent-coherent stores (sc1,
       // written through past the per-XCD L2), the wave waits for them to
       // complete, then bumps the segment's per-head counter; the wave that
@@ -939,9 +943,9 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
       for (int r = 0; r < RB; ++r) {
         if (!rv[r]) continue;
         const int64_t prow = ((int64_t)part * a.nw + wid) * seg_rows + r * kRows + n;
-        uint64_t* pp = reinterpret_cast<uint64_t*>(a.part_o + prow * kHeadDim);
+        uint64_t* pp = reinterpret_cast<uint64_t*>(a.part_o + prow * D);
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
+        for (int dt = 0; dt < DT; ++dt) {
           const int e = (16 * dt + 4 * g) / 2;
           __hip_atomic_store(pp + e, pack_f2(o[r][dt][0], o[r][dt][1]), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
@@ -1003,7 +1007,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
               for (int j = 0; j < 16; ++j) {
                 const int kk = k0 + min(j0 + j, kn - 1);
                 v[j] = unpack_f2(__hip_atomic_load(
-                    reinterpret_cast<const uint64_t*>(a.part_o + (row0 + kk * pstride) * kHeadDim) +
+                    reinterpret_cast<const uint64_t*>(a.part_o + (row0 + kk * pstride) * D) +
                         lane,
                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
               }
@@ -1029,9 +1033,9 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
       for (int r = 0; r < RB; ++r) {
         if (!rv[r]) continue;
         const int64_t prow = ((int64_t)part * a.nw + wid) * seg_rows + r * kRows + n;
-        float* pp = a.part_o + prow * kHeadDim;
+        float* pp = a.part_o + prow * D;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
+        for (int dt = 0; dt < DT; ++dt)
           *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * g) = o[r][dt];
         if (g == 0) a.part_ml[prow] = make_float2(m[r], lsum[r]);
       }
@@ -1052,7 +1056,8 @@ __device__ __forceinline__ int xcd_range(int b, int n) {
 }
 
 // One work-group per key range, one wave per kv head of the segment's group.
-template <int NW, int RB>
+// D: head dim, 128 or 64.
+template <int NW, int RB, int D>
 #ifndef AIA_GQA_WAVES_PER_EU
 #define AIA_GQA_WAVES_PER_EU 2
 #endif
@@ -1083,7 +1088,7 @@ void gqa_attn_kernel(AttnArgs a) {
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
       if ((rec[1] & 0xffff) * NW + wid < a.hkv)
-        gqa_segment<RB>(a, rec, s, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane, wid, first,
+        gqa_segment<RB, D>(a, rec, s, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane, wid, first,
                         pre);
       first = false;
       t = chunk_end;
@@ -2056,8 +2061,8 @@ extern "C" int aia_paged_attention_gqa(
     int64_t workspace_bytes, void* stream) {
   using namespace aia;
   if (int rc = check_heads("aia_paged_attention_gqa", num_q_heads, num_kv_heads)) return rc;
-  if (head_dim != kHeadDim)
-    return fail(AIA_ERR_UNSUPPORTED, "aia_paged_attention_gqa: head_dim %d (only 128)", head_dim);
+  if (head_dim != kHeadDim && head_dim != 64)
+    return fail(AIA_ERR_UNSUPPORTED, "aia_paged_attention_gqa: head_dim %d (128 or 64)", head_dim);
   if (!(scale > 0.f))
     return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: scale %g must be positive", (double)scale);
   if (block_size <= 0 || num_blocks <= 0)
@@ -2109,11 +2114,15 @@ extern "C" int aia_paged_attention_gqa(
   a.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
   a.batch = batch; a.tokens = num_tokens;
   a.counters = reinterpret_cast<int32_t*>(ws + L.cnt);
-  a.fused_merge = (flags & AIA_ATTN_FUSED_MERGE) && !(flags & AIA_ATTN_SKIP_MERGE) ? 1 : 0;
+  // (the in-kernel merge exists for head_dim 128; 64 always merges in its own pass)
+  a.fused_merge =
+      (flags & AIA_ATTN_FUSED_MERGE) && !(flags & AIA_ATTN_SKIP_MERGE) && head_dim == kHeadDim;
   hipStream_t s = (hipStream_t)stream;
-#define AIA_GQA_LAUNCH(NW)                                                      \
-  (g.rb == 2 ? gqa_attn_kernel<NW, 2><<<waves, 64 * NW, 0, s>>>(a)             \
-             : gqa_attn_kernel<NW, 1><<<waves, 64 * NW, 0, s>>>(a))
+#define AIA_GQA_LAUNCH_D(NW, D)                                                 \
+  (g.rb == 2 ? gqa_attn_kernel<NW, 2, D><<<waves, 64 * NW, 0, s>>>(a)          \
+             : gqa_attn_kernel<NW, 1, D><<<waves, 64 * NW, 0, s>>>(a))
+#define AIA_GQA_LAUNCH(NW) \
+  (head_dim == 64 ? AIA_GQA_LAUNCH_D(NW, 64) : AIA_GQA_LAUNCH_D(NW, kHeadDim))
   switch (g.nw) {
     case 1: AIA_GQA_LAUNCH(1); break;
     case 2: AIA_GQA_LAUNCH(2); break;
@@ -2125,6 +2134,7 @@ extern "C" int aia_paged_attention_gqa(
     default: AIA_GQA_LAUNCH(8); break;
   }
 #undef AIA_GQA_LAUNCH
+#undef AIA_GQA_LAUNCH_D
   if (int rc = check_hip(hipGetLastError(), "gqa_attn_kernel launch")) return rc;
   if (L.pf_cap > 0) {
     PrefillArgs pa;

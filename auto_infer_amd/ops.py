@@ -370,11 +370,11 @@ def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None, fl
                         key_new=None, value_new=None):
     """Paged GQA attention (reference base.py:48-61 FIA semantics).
 
-    query (T, Hq, 128) bf16; key/value caches (NB, bs, Hkv, 128) bf16
-    contiguous; ``plan`` an ``AttentionPlan`` of this step.  Returns
-    (T, Hq, 128) bf16.  With ``key_new`` / ``value_new`` (this step's new rows,
-    (T, Hkv, 128)) the kernel also writes them into the caches at the slots
-    the block table assigns (the fused form of ``write_kv``).
+    query (T, Hq, D) bf16 with D = 128 or 64; key/value caches (NB, bs, Hkv,
+    D) bf16 contiguous; ``plan`` an ``AttentionPlan`` of this step (head_dim_v
+    D).  Returns (T, Hq, D) bf16.  With ``key_new`` / ``value_new`` (this
+    step's new rows, (T, Hkv, D)) the kernel also writes them into the caches
+    at the slots the block table assigns (the fused form of ``write_kv``).
     """
     _check_device_tensor(query, "query", _BF16)
     _check_device_tensor(key_cache, "key_cache", _BF16)

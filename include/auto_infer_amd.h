@@ -86,11 +86,15 @@ int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
  * query:  (num_tokens, Hq, head_dim) with the given token/head strides.
  * caches: contiguous (num_blocks, block_size, Hkv, head_dim).
  * out:    (num_tokens, Hq, head_dim) with the given strides.
- * head_dim must be 128 and scale positive (AIA_ERR_INVALID otherwise).
+ * head_dim must be 128 (Qwen2-7B, Qwen3) or 64 (Qwen2 / Qwen2.5 0.5B:
+ * hidden 896 over 14 heads), AIA_ERR_UNSUPPORTED otherwise; scale must be
+ * positive (AIA_ERR_INVALID otherwise).  Prefill items exist for head_dim
+ * 128; at 64 every row runs on the split-K kernel (two query blocks per key
+ * tile for prefill chunks) and AIA_ATTN_FUSED_MERGE is ignored.
  * The workspace must hold a plan made by
  * aia_attn_plan with the same metadata, head counts and num_waves.
  * key_new / value_new (optional, both or neither): this step's new K/V rows
- * (num_tokens, Hkv, 128), query token t being position Lk - Lq + i of its
+ * (num_tokens, Hkv, head_dim), query token t being position Lk - Lq + i of its
  * request.  When given, the kernel also performs the KV slot write of those
  * rows (what aia_kv_write would do, at slot block_table[b, pos / bs] * bs +
  * pos % bs -- the slot_mapping every packer produces) and reads the new keys

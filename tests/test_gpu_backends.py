@@ -277,3 +277,32 @@ def test_mla_fused_pre_attention_matches_torch_path():
         err = (of.float() - op.float()).abs().max().item()
         print(f"output max-abs diff {err:.3e} (scale {scale:.2f})", flush=True)
         assert err <= TOL * max(1.0, scale)
+
+
+def test_gqa_backend_head_dim_64_qwen25_05b_shape():
+    """Qwen2.5-0.5B attention shape (14 query heads, 2 KV heads, head_dim 64
+    = 896 / 14, qkv bias; the reference's own smoke-test model): prefill,
+    decode, and a chunked continuation beside a decode row on the split-K
+    path, caches bit-exact and outputs within tolerance."""
+    g = torch.Generator().manual_seed(11)
+    hq, hkv, d, hidden, bs = 14, 2, 64, 896, 16
+    p = "model.layers.0.self_attn."
+    w = {
+        p + "qkv_proj.weight": (torch.randn((hq + 2 * hkv) * d, hidden, generator=g) / 30).bfloat16(),
+        p + "qkv_proj.bias": (torch.randn((hq + 2 * hkv) * d, generator=g) / 4).bfloat16(),
+        p + "o_proj.weight": (torch.randn(hidden, hq * d, generator=g) / 30).bfloat16(),
+    }
+    w = {k: v.to(DEV) for k, v in w.items()}
+    kw = dict(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, scale=d ** -0.5, num_layers=1,
+              device=DEV, dtype=torch.bfloat16, w=w, rms_eps=1e-6)
+    hip = GqaHipBackend(**kw)
+    twin = oracle_twin(GqaHipBackend)(**kw)
+    caches_h = hip.alloc_kv_caches(20, bs)
+    caches_r = twin.alloc_kv_caches(20, bs)
+    a, b = [3, 9, 4], [7, 1, 11, 2, 5, 13, 17, 6]
+    steps = [
+        [(0, 37, a), (0, 70, b[:5])],              # two prompts
+        [(37, 1, a), (70, 1, b[:5])],              # decode
+        [(38, 1, a), (71, 50, b)],                 # decode + chunked continuation
+    ]
+    run_pair(hip, twin, steps, caches_h, caches_r, bs, hidden, seed=12)

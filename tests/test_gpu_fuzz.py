@@ -102,3 +102,38 @@ def test_random_mla_steps_match_the_oracle(seed):
     err = (out.float().cpu() - exp).abs().max().item()
     print(f"max-abs err {err:.3e}", flush=True)
     assert err <= TOL
+
+
+HEADS_64 = [(14, 2), (16, 2), (8, 8), (32, 4), (12, 2), (16, 16), (64, 8)]
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_steps_head_dim_64_match_the_oracle(seed):
+    """head_dim 64 (Qwen2 / Qwen2.5 0.5B: hidden 896 over 14 heads): the
+    same random steps on the split-K kernel, fused KV write included."""
+    c = draw(4000 + seed)
+    c["hq"], c["hkv"] = random.Random(seed).choice(HEADS_64)
+    print(f"case {seed}: {c}", flush=True)
+    step = workloads.make_gqa_step(lqs=c["lqs"], lks=c["lks"], num_q_heads=c["hq"],
+                                   num_kv_heads=c["hkv"], head_dim=64, block_size=c["bs"],
+                                   seed=seed, extra_blocks=3)
+    kc, vc = step.k_cache.to(DEV), step.v_cache.to(DEV)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, c["hq"], c["hkv"], 64, c["bs"],
+                                        num_waves=c["waves"])
+    ek, ev = step.k_cache, step.v_cache
+    if c["fused"]:
+        ek, ev = ek.clone(), ev.clone()
+        kv_write(step.k_new, step.v_new, ek, ev, step.slot_mapping)
+        out = ops.paged_attention_gqa(step.q.to(DEV), kc, vc, plan, step.scale,
+                                      key_new=step.k_new.to(DEV), value_new=step.v_new.to(DEV))
+    else:
+        out = ops.paged_attention_gqa(step.q.to(DEV), kc, vc, plan, step.scale)
+    torch.cuda.synchronize()
+    if c["fused"]:
+        assert torch.equal(kc.cpu(), ek) and torch.equal(vc.cpu(), ev)
+    exp = paged_attention(step.q, ek, ev, step.block_table, step.cu_seqlens_q, step.seqlens_kv,
+                          step.scale)
+    err = (out.float().cpu() - exp.float()).abs().max().item()
+    print(f"max-abs err {err:.3e}", flush=True)
+    assert err <= TOL

@@ -101,5 +101,16 @@ def check(rc, what):
     raise RuntimeError(msg)
 
 
+_addr = {}
+
+
+def address(name):
+    """Address of an exported entry point, for native callers."""
+    a = _addr.get(name)
+    if a is None:
+        a = _addr[name] = ctypes.cast(getattr(load(), name), ctypes.c_void_p).value
+    return a
+
+
 def call(name, *args):
     check(getattr(load(), name)(*args), name)

@@ -34,10 +34,15 @@ HOSTPACK = os.path.join(PKG, "_hostpack" + sysconfig.get_config_var("EXT_SUFFIX"
 
 
 def build_hostpack(verbose=False):
-    """The packer's native host loop (CPython extension, g++)."""
+    """The packer's native host loop, upload staging and pack launch
+    (CPython extension, g++)."""
     tmp = HOSTPACK + ".tmp"
-    cmd = ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall",
-           "-I", sysconfig.get_paths()["include"], os.path.join(HERE, "hostpack.cpp"), "-o", tmp]
+    # links the HIP runtime by SONAME: loaded after torch, it is torch's
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    cmd = ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",
+           "-I", sysconfig.get_paths()["include"], "-I", os.path.join(rocm, "include"),
+           os.path.join(HERE, "hostpack.cpp"), "-o", tmp, "-L", os.path.join(rocm, "lib"),
+           "-lamdhip64"]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

@@ -17,6 +17,8 @@
 
 #include <cstdint>
 
+#include <hip/hip_runtime_api.h>
+
 namespace {
 
 struct Ref {            // owned reference
@@ -336,47 +338,114 @@ PyObject* get_list(PyObject* o, const char* name) {
   return v;
 }
 
-// Writes one step's uploads into host memory at `base` (the upload layout of
+// Writes one step's uploads into host memory at `h` (the upload layout of
 // _Uploader.upload: token pool index / value int64, block pool index int64 /
 // value int32, row descriptors int32 x row_ints), at the byte offsets the
-// caller computed for these list lengths.
-PyObject* stage(PyObject*, PyObject* args) {
-  PyObject* upd;
-  unsigned long long base;
-  long long tw, bw, o0, o1, o2, o3, o4, row_ints;
-  if (!PyArg_ParseTuple(args, "OKLLLLLLLL", &upd, &base, &tw, &bw, &o0, &o1, &o2, &o3, &o4,
-                        &row_ints))
-    return nullptr;
-  char* h = reinterpret_cast<char*>(base);
+// caller computed for these list lengths; reports the lengths.
+bool stage_impl(PyObject* upd, char* h, long long tw, long long bw, const long long (&o)[5],
+                long long row_ints, Py_ssize_t* nt_out, Py_ssize_t* nb_out, Py_ssize_t* nr_out) {
   Ref ts(get_list(upd, "tok_slot")), ti(get_list(upd, "tok_idx")), tv(get_list(upd, "tok_val"));
   Ref bsl(get_list(upd, "blk_slot")), bi(get_list(upd, "blk_idx")), bv(get_list(upd, "blk_val"));
   Ref rows(get_list(upd, "rows"));
-  if (!ts || !ti || !tv || !bsl || !bi || !bv || !rows) return nullptr;
+  if (!ts || !ti || !tv || !bsl || !bi || !bv || !rows) return false;
   const Py_ssize_t nt = PyList_GET_SIZE(ti.get()), nb = PyList_GET_SIZE(bi.get());
   const Py_ssize_t nr = PyList_GET_SIZE(rows.get());
   if (PyList_GET_SIZE(ts.get()) != nt || PyList_GET_SIZE(tv.get()) != nt ||
       PyList_GET_SIZE(bsl.get()) != nb || PyList_GET_SIZE(bv.get()) != nb) {
     PyErr_SetString(PyExc_ValueError, "update lists differ in length");
-    return nullptr;
+    return false;
   }
-  if (!fill_ll(ts.get(), ti.get(), tw, reinterpret_cast<long long*>(h + o0), nt) ||
-      !fill_ll(tv.get(), nullptr, 0, reinterpret_cast<long long*>(h + o1), nt) ||
-      !fill_ll(bsl.get(), bi.get(), bw, reinterpret_cast<long long*>(h + o2), nb) ||
-      !fill_i32(bv.get(), reinterpret_cast<int*>(h + o3), nb))
-    return nullptr;
-  int* rp = reinterpret_cast<int*>(h + o4);
+  if (!fill_ll(ts.get(), ti.get(), tw, reinterpret_cast<long long*>(h + o[0]), nt) ||
+      !fill_ll(tv.get(), nullptr, 0, reinterpret_cast<long long*>(h + o[1]), nt) ||
+      !fill_ll(bsl.get(), bi.get(), bw, reinterpret_cast<long long*>(h + o[2]), nb) ||
+      !fill_i32(bv.get(), reinterpret_cast<int*>(h + o[3]), nb))
+    return false;
+  int* rp = reinterpret_cast<int*>(h + o[4]);
   for (Py_ssize_t r = 0; r < nr; ++r) {
     PyObject* row = PyList_GET_ITEM(rows.get(), r);
     if (!PyTuple_Check(row) || PyTuple_GET_SIZE(row) != row_ints) {
       PyErr_SetString(PyExc_ValueError, "row descriptors must be tuples of row_ints ints");
-      return nullptr;
+      return false;
     }
-    if (!fill_i32(row, rp + r * row_ints, row_ints)) return nullptr;
+    if (!fill_i32(row, rp + r * row_ints, row_ints)) return false;
   }
+  *nt_out = nt; *nb_out = nb; *nr_out = nr;
+  return true;
+}
+
+PyObject* stage(PyObject*, PyObject* args) {
+  PyObject* upd;
+  unsigned long long base;
+  long long tw, bw, row_ints, o[5];
+  if (!PyArg_ParseTuple(args, "OKLLLLLLLL", &upd, &base, &tw, &bw, &o[0], &o[1], &o[2], &o[3],
+                        &o[4], &row_ints))
+    return nullptr;
+  Py_ssize_t nt, nb, nr;
+  if (!stage_impl(upd, reinterpret_cast<char*>(base), tw, bw, o, row_ints, &nt, &nb, &nr))
+    return nullptr;
   Py_RETURN_NONE;
 }
 
+// aia_pack_rows (include/auto_infer_amd.h), reached through the address the
+// Python side reads from the loaded library.
+typedef int (*PackRowsFn)(const int64_t*, const int64_t*, int32_t, const int64_t*, const int32_t*,
+                          int32_t, int64_t*, int64_t, int32_t*, int64_t, const int32_t*, int32_t,
+                          int32_t, int32_t, int64_t*, int64_t*, int32_t*, int32_t*, int32_t*,
+                          int32_t*, int64_t*, int64_t*, int32_t, int32_t, void*);
+
+constexpr int kHipError = -1000;   // returned (negated HIP code added) on a runtime failure
+
+// One step's upload and pack launch, the native form of _Uploader.upload +
+// _launch: wait for the event of the last copy that read this staging
+// buffer (if any), stage the updates into it at the caller's offsets, copy
+// the `total` bytes to the device buffer and record the event on `stream`,
+// then call aia_pack_rows on the staged arrays.  Returns aia_pack_rows'
+// status, or kHipError - code when a runtime call fails.
+PyObject* upload_pack(PyObject*, PyObject* args) {
+  PyObject* upd;
+  unsigned long long fn, host, dev, wait_ev, rec_ev, stream, token_pool, block_pool;
+  unsigned long long token_ids, positions, slot_mapping, block_table, cu, kv, last_rows, sample_rows;
+  long long tw, bw, total, o[5], row_ints, tp_stride, bp_stride;
+  int block_size, bt_width, sample_count, sample_cap;
+  if (!PyArg_ParseTuple(args, "OKKKKKKLLLLLLLLLKLKLiiKKKKKKKKii", &upd, &fn, &host, &dev, &wait_ev,
+                        &rec_ev, &stream, &tw, &bw, &total, &o[0], &o[1], &o[2], &o[3], &o[4],
+                        &row_ints, &token_pool, &tp_stride, &block_pool, &bp_stride, &block_size,
+                        &bt_width, &token_ids, &positions, &slot_mapping, &block_table, &cu, &kv,
+                        &last_rows, &sample_rows, &sample_count, &sample_cap))
+    return nullptr;
+  if (wait_ev) {
+    const hipError_t e = hipEventSynchronize(reinterpret_cast<hipEvent_t>(wait_ev));
+    if (e != hipSuccess) return PyLong_FromLong(kHipError - (int)e);
+  }
+  Py_ssize_t nt, nb, nr;
+  if (!stage_impl(upd, reinterpret_cast<char*>(host), tw, bw, o, row_ints, &nt, &nb, &nr))
+    return nullptr;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e = hipMemcpyAsync(reinterpret_cast<void*>(dev), reinterpret_cast<const void*>(host),
+                                (size_t)total, hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = hipEventRecord(reinterpret_cast<hipEvent_t>(rec_ev), st);
+  if (e != hipSuccess) return PyLong_FromLong(kHipError - (int)e);
+  char* d = reinterpret_cast<char*>(dev);
+  const int rc = reinterpret_cast<PackRowsFn>(fn)(
+      reinterpret_cast<const int64_t*>(d + o[0]), reinterpret_cast<const int64_t*>(d + o[1]),
+      (int32_t)nt, reinterpret_cast<const int64_t*>(d + o[2]), reinterpret_cast<const int32_t*>(d + o[3]),
+      (int32_t)nb, reinterpret_cast<int64_t*>(token_pool), tp_stride,
+      reinterpret_cast<int32_t*>(block_pool), bp_stride, reinterpret_cast<const int32_t*>(d + o[4]),
+      (int32_t)nr, block_size, bt_width, reinterpret_cast<int64_t*>(token_ids),
+      reinterpret_cast<int64_t*>(positions), reinterpret_cast<int32_t*>(slot_mapping),
+      reinterpret_cast<int32_t*>(block_table), reinterpret_cast<int32_t*>(cu),
+      reinterpret_cast<int32_t*>(kv), reinterpret_cast<int64_t*>(last_rows),
+      reinterpret_cast<int64_t*>(sample_rows), sample_count, sample_cap,
+      reinterpret_cast<void*>(stream));
+  return PyLong_FromLong(rc);
+}
+
 PyMethodDef methods[] = {
+    {"upload_pack", upload_pack, METH_VARARGS,
+     "upload_pack(updates, pack_rows_fn, host, dev, wait_event, record_event, stream, token_width, "
+     "block_width, total, 5 offsets, row_ints, token_pool, token_pool_stride, block_pool, "
+     "block_pool_stride, block_size, bt_width, token_ids, positions, slot_mapping, block_table, "
+     "cu, kv, last_rows, sample_rows, sample_count, sample_cap) -> status"},
     {"stage", stage, METH_VARARGS,
      "stage(updates, host_address, token_width, block_width, off_tok_idx, off_tok_val, "
      "off_blk_idx, off_blk_val, off_rows, row_ints) -> None"},

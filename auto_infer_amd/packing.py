@@ -34,6 +34,7 @@ except ImportError:
 from auto_infer_amd.ops import _check_device_tensor, _ptr, _stream
 
 _ROW_INTS = 8
+_HIP_ERROR = -1000      # _hostpack.upload_pack: statuses at or below are HIP runtime errors
 
 
 class DeviceRequestTable:
@@ -195,12 +196,44 @@ class _Uploader:
 
     def __init__(self, device):
         self.device = torch.device(device)
+        self.device_index = (self.device.index if self.device.index is not None
+                             else torch.cuda.current_device() if self.device.type == "cuda" else -1)
         self._host = [None, None]
         self._event = [None, None]
         self._used = [False, False]
         self._dev = None
         self._turn = 0
         self._views = {}           # (turn, bytes) -> (device slice, host slice)
+
+    def reserve(self, upd):
+        """Offsets and buffers of this step's upload, for the native upload
+        (``_hostpack.upload_pack``): (host address, device address, offsets,
+        total bytes, raw event to wait for or 0, raw event to record)."""
+        nt, nb, nr = len(upd.tok_idx), len(upd.blk_idx), len(upd.rows)
+        offs, total = [], 0
+        for sz in (nt * 8, nt * 8, nb * 8, nb * 4, nr * _ROW_INTS * 4):
+            offs.append(total)
+            total += (sz + 15) & ~15
+        total = max(total, 16)
+        i = self._turn
+        self._turn ^= 1
+        host = self._host[i]
+        if host is None or host.numel() < total:
+            if self._used[i]:
+                self._event[i].synchronize()      # the old buffer may still be read
+            host = torch.empty(max(total * 2, 4096), dtype=torch.uint8, pin_memory=True)
+            self._host[i] = host
+            self._views.clear()
+        if self._dev is None or self._dev.numel() < total:
+            self._dev = torch.empty(max(total * 2, 4096), dtype=torch.uint8, device=self.device)
+            self._views.clear()
+        if self._event[i] is None:
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(self.device))   # creates the runtime event
+            self._event[i] = ev
+        wait = self._event[i].cuda_event if self._used[i] else 0
+        self._used[i] = True
+        return host.data_ptr(), self._dev.data_ptr(), offs, total, wait, self._event[i].cuda_event
 
     def upload(self, upd, token_width, block_width, stream=None):
         nt, nb, nr = len(upd.tok_idx), len(upd.blk_idx), len(upd.rows)
@@ -254,11 +287,28 @@ class PackedStep:
 
 def _launch(table, uploader, upd, *, block_size, bt_width, token_ids, positions, slot_mapping,
             block_table, cu, kv, last_rows, sample_rows=None, sample_count=0, stream=None):
+    cap = sample_rows.numel() if sample_rows is not None else 0
+    if _hostpack is not None and uploader.device.type == "cuda":
+        # one native call: event wait, staging, copy, event record, pack launch
+        sp = (stream.cuda_stream if stream is not None
+              else torch._C._cuda_getCurrentRawStream(uploader.device_index))
+        host, dev, offs, total, wait, rec = uploader.reserve(upd)
+        rc = _hostpack.upload_pack(
+            upd, _native.address("aia_pack_rows"), host, dev, wait, rec, sp,
+            table.token_pool.shape[1], table.block_pool.shape[1], total, *offs, _ROW_INTS,
+            table.token_pool.data_ptr(), table.token_pool.shape[1], table.block_pool.data_ptr(),
+            table.block_pool.shape[1], block_size, bt_width, token_ids.data_ptr(),
+            positions.data_ptr(), slot_mapping.data_ptr(), block_table.data_ptr(), cu.data_ptr(),
+            kv.data_ptr(), last_rows.data_ptr(),
+            sample_rows.data_ptr() if sample_rows is not None else 0, sample_count, cap)
+        if rc <= _HIP_ERROR:
+            raise RuntimeError(f"aia_pack_rows upload: HIP runtime error {_HIP_ERROR - rc}")
+        _native.check(rc, "aia_pack_rows")
+        return
     if stream is None:
         stream = torch.cuda.current_stream(table.device)
     ptrs = uploader.upload(upd, table.token_pool.shape[1], table.block_pool.shape[1], stream)
     nt, nb, nr = len(upd.tok_idx), len(upd.blk_idx), len(upd.rows)
-    cap = sample_rows.numel() if sample_rows is not None else 0
     _native.call(
         "aia_pack_rows", ptrs[0], ptrs[1], nt, ptrs[2], ptrs[3], nb,
         _ptr(table.token_pool), table.token_pool.shape[1], _ptr(table.block_pool),

@@ -137,3 +137,26 @@ def test_random_steps_head_dim_64_match_the_oracle(seed):
     err = (out.float().cpu() - exp.float()).abs().max().item()
     print(f"max-abs err {err:.3e}", flush=True)
     assert err <= TOL
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_mla_steps_other_head_counts(seed):
+    """Absorbed MLA at head counts other than configs[2]'s 16: fewer heads
+    than a 16-row block (1, 8), several head blocks per token (32, 128 as in
+    DeepSeek-V2), with decode, verify and prefill-sized rows."""
+    from oracle.paged_attn import mla_absorbed_attention
+    heads = [1, 8, 32, 128][seed % 4]
+    c = draw_mla(5000 + seed)
+    print(f"case {seed}: heads {heads} {c}", flush=True)
+    step = workloads.make_mla_step(lqs=c["lqs"], lks=c["lks"], num_heads=heads, block_size=c["bs"],
+                                   seed=seed)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, heads, 1, 512, c["bs"],
+                                        num_waves=c["waves"])
+    out = ops.paged_attention_mla(step.q_latent.to(DEV), step.cache.to(DEV), plan, step.scale)
+    torch.cuda.synchronize()
+    exp = mla_absorbed_attention(step.q_latent, step.cache, step.block_table, step.cu_seqlens_q,
+                                 step.seqlens_kv, step.scale, 512)
+    err = (out.float().cpu() - exp).abs().max().item()
+    print(f"max-abs err {err:.3e}", flush=True)
+    assert err <= TOL

@@ -1078,13 +1078,12 @@ template <int NW, int RB, int D>
 #ifndef AIA_GQA_WAVES_PER_EU
 #define AIA_GQA_WAVES_PER_EU 2
 #endif
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(AIA_GQA_WAVES_PER_EU, AIA_GQA_WAVES_PER_EU)))
-void gqa_attn_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t vt_all[NW][kTile * kVStride];
+__device__ __forceinline__ void gqa_attn_body(const AttnArgs& a, int bid, int nblocks,
+                                              uint16_t (*vt_all)[kTile * kVStride]) {
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if ((int)blockIdx.x >= a.waves) return;
-  const int w = xcd_range(blockIdx.x, gridDim.x);
+  if (bid >= a.waves) return;
+  const int w = xcd_range(bid, nblocks);
   const int* wr = a.wave_rec + (int64_t)w * kRecInts;
   const int pre = wr[16 + (lane & (kRecBlocks - 1))];   // issued with the header
   const int nseg = a.hdr[0], total_tiles = a.hdr[1];
@@ -1117,6 +1116,13 @@ void gqa_attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) rec[i] = r[i];
   }
+}
+
+template <int NW, int RB, int D>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(AIA_GQA_WAVES_PER_EU, AIA_GQA_WAVES_PER_EU)))
+void gqa_attn_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t vt_all[NW][kTile * kVStride];
+  gqa_attn_body<NW, RB, D>(a, blockIdx.x, gridDim.x, vt_all);
 }
 
 // ---------------------------------------------------------------- prefill
@@ -1185,17 +1191,16 @@ constexpr float kLazyLog2 = AIA_PF_LAZY;              // max growth (log2) befor
 #define AIA_PF_WPE 2
 #endif
 template <bool ONE_BLOCK, bool FUSED>
-__global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(AIA_PF_WPE, AIA_PF_WPE)))
-void gqa_prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kPfKeys * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vs[2][kPfKeys * kPfVStride];
+__device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
+                                                 uint16_t (*ks)[kPfKeys * kKStride],
+                                                 uint16_t (*vs)[kPfKeys * kPfVStride]) {
   // Work-group b takes (kv head, item) pair xcd_range(b, pairs), kv-head
   // major: each XCD gets a contiguous run of pairs, so the items that re-read
   // one request's keys for one kv head share an XCD's L2.
   const int count = a.hdr[6];
   const int pairs = count * a.hkv;
-  if ((int)blockIdx.x >= pairs) return;
-  const int pair = xcd_range(blockIdx.x, pairs);
+  if (wg >= pairs) return;
+  const int pair = xcd_range(wg, pairs);
   const int kvh = pair / count, unit = pair - kvh * count;
   const int4 it = a.units[unit];
   const int b = it.x, row0 = it.y, t0 = it.z, t1 = it.w;
@@ -1506,6 +1511,46 @@ void gqa_prefill_kernel(PrefillArgs a) {
       *reinterpret_cast<uint2*>(op + 16 * dt + 4 * g) = wv;
     }
   }
+}
+
+template <bool ONE_BLOCK, bool FUSED>
+__global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(AIA_PF_WPE, AIA_PF_WPE)))
+void gqa_prefill_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kPfKeys * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[2][kPfKeys * kPfVStride];
+  gqa_prefill_body<ONE_BLOCK, FUSED>(a, blockIdx.x, ks, vs);
+}
+
+// Mixed steps (prefill items beside split-K decode ranges) in one grid, for
+// kPfWaves-wave decode groups (Hkv = kPfWaves).  Launched separately, the
+// two kernels cannot share a CU: VGPRs are allocated in blocks of 8, so one
+// prefill wave (232) plus two decode waves (2 x 144) exceed a SIMD's 512, and
+// the second kernel waits for the first to drain.  In one grid every
+// work-group gets the prefill budget and does one job or the other, so the
+// compute-bound prefill runs while the HBM-bound decode streams beside it.
+#ifndef AIA_MIXED
+#define AIA_MIXED 1
+#endif
+static_assert(kPfWaves * kTile * kVStride <= 2 * kPfKeys * kKStride,
+              "decode V^T staging must fit the prefill K buffers");
+template <bool ONE_BLOCK, bool FUSED>
+__global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(AIA_PF_WPE, AIA_PF_WPE)))
+void gqa_mixed_kernel(AttnArgs a, PrefillArgs pa, int npf, int ndec) {
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kPfKeys * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[2][kPfKeys * kPfVStride];
+  // Prefill units take the first npf block ids and the decode ranges the
+  // rest: the units are dealt out first, one or two per CU, and the ranges
+  // fill the remaining slots and every slot a unit frees.  (Alternating the
+  // roles by block id measured slower: 590 us against 449 on configs[1] in
+  // runs of 8 ids, 459-462 in runs of 64; runs of 256 matched.)
+  const int b = blockIdx.x;
+  const bool prefill = b < npf;
+  const int idx = prefill ? b : b - npf;
+  if (prefill)
+    gqa_prefill_body<ONE_BLOCK, FUSED>(pa, idx, ks, vs);
+  else
+    gqa_attn_body<kPfWaves, 1, kHeadDim>(a, idx, ndec,
+                                         reinterpret_cast<uint16_t(*)[kTile * kVStride]>(&ks[0][0]));
 }
 
 struct MergeArgs {
@@ -2138,26 +2183,8 @@ extern "C" int aia_paged_attention_gqa(
   a.fused_merge =
       (flags & AIA_ATTN_FUSED_MERGE) && !(flags & AIA_ATTN_SKIP_MERGE) && head_dim == kHeadDim;
   hipStream_t s = (hipStream_t)stream;
-#define AIA_GQA_LAUNCH_D(NW, D)                                                 \
-  (g.rb == 2 ? gqa_attn_kernel<NW, 2, D><<<waves, 64 * NW, 0, s>>>(a)          \
-             : gqa_attn_kernel<NW, 1, D><<<waves, 64 * NW, 0, s>>>(a))
-#define AIA_GQA_LAUNCH(NW) \
-  (head_dim == 64 ? AIA_GQA_LAUNCH_D(NW, 64) : AIA_GQA_LAUNCH_D(NW, kHeadDim))
-  switch (g.nw) {
-    case 1: AIA_GQA_LAUNCH(1); break;
-    case 2: AIA_GQA_LAUNCH(2); break;
-    case 3: AIA_GQA_LAUNCH(3); break;
-    case 4: AIA_GQA_LAUNCH(4); break;
-    case 5: AIA_GQA_LAUNCH(5); break;
-    case 6: AIA_GQA_LAUNCH(6); break;
-    case 7: AIA_GQA_LAUNCH(7); break;
-    default: AIA_GQA_LAUNCH(8); break;
-  }
-#undef AIA_GQA_LAUNCH
-#undef AIA_GQA_LAUNCH_D
-  if (int rc = check_hip(hipGetLastError(), "gqa_attn_kernel launch")) return rc;
+  PrefillArgs pa = {};
   if (L.pf_cap > 0) {
-    PrefillArgs pa;
     pa.q = a.q; pa.q_ts = a.q_ts; pa.q_hs = a.q_hs;
     pa.kc = a.kc; pa.vc = a.vc; pa.kn = a.kn; pa.vn = a.vn; pa.kn_ts = a.kn_ts; pa.vn_ts = a.vn_ts;
     pa.bt = block_table; pa.bt_stride = block_table_stride;
@@ -2171,13 +2198,44 @@ extern "C" int aia_paged_attention_gqa(
     pa.part_o = reinterpret_cast<float*>(ws + L.pf_o);
     pa.part_ml = reinterpret_cast<float2*>(ws + L.pf_ml);
     pa.part_units = (int32_t)(L.pf_slots / g.hkv);
-    const dim3 grid((unsigned)(L.pf_unit_cap * g.hkv));
-    const bool one_block = block_size % kPfKeys == 0;
-    if (one_block && pa.kn) gqa_prefill_kernel<true, true><<<grid, kPfWaves * 64, 0, s>>>(pa);
-    else if (one_block) gqa_prefill_kernel<true, false><<<grid, kPfWaves * 64, 0, s>>>(pa);
-    else if (pa.kn) gqa_prefill_kernel<false, true><<<grid, kPfWaves * 64, 0, s>>>(pa);
-    else gqa_prefill_kernel<false, false><<<grid, kPfWaves * 64, 0, s>>>(pa);
-    if (int rc = check_hip(hipGetLastError(), "gqa_prefill_kernel launch")) return rc;
+  }
+  const bool one_block = block_size % kPfKeys == 0;
+  if (AIA_MIXED && L.pf_cap > 0 && g.nw == kPfWaves && g.rb == 1 && head_dim == kHeadDim &&
+      !a.fused_merge) {
+    const int npf = (int)(L.pf_unit_cap * g.hkv);
+    const dim3 grid((unsigned)(npf + waves));
+    if (one_block && pa.kn) gqa_mixed_kernel<true, true><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf, waves);
+    else if (one_block) gqa_mixed_kernel<true, false><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf, waves);
+    else if (pa.kn) gqa_mixed_kernel<false, true><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf, waves);
+    else gqa_mixed_kernel<false, false><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf, waves);
+    if (int rc = check_hip(hipGetLastError(), "gqa_mixed_kernel launch")) return rc;
+  } else {
+#define AIA_GQA_LAUNCH_D(NW, D)                                                   \
+  (g.rb == 2 ? gqa_attn_kernel<NW, 2, D><<<waves, 64 * NW, 0, s>>>(a)            \
+             : gqa_attn_kernel<NW, 1, D><<<waves, 64 * NW, 0, s>>>(a))
+#define AIA_GQA_LAUNCH(NW) \
+  (head_dim == 64 ? AIA_GQA_LAUNCH_D(NW, 64) : AIA_GQA_LAUNCH_D(NW, kHeadDim))
+    switch (g.nw) {
+      case 1: AIA_GQA_LAUNCH(1); break;
+      case 2: AIA_GQA_LAUNCH(2); break;
+      case 3: AIA_GQA_LAUNCH(3); break;
+      case 4: AIA_GQA_LAUNCH(4); break;
+      case 5: AIA_GQA_LAUNCH(5); break;
+      case 6: AIA_GQA_LAUNCH(6); break;
+      case 7: AIA_GQA_LAUNCH(7); break;
+      default: AIA_GQA_LAUNCH(8); break;
+    }
+#undef AIA_GQA_LAUNCH
+#undef AIA_GQA_LAUNCH_D
+    if (int rc = check_hip(hipGetLastError(), "gqa_attn_kernel launch")) return rc;
+    if (L.pf_cap > 0) {
+      const dim3 grid((unsigned)(L.pf_unit_cap * g.hkv));
+      if (one_block && pa.kn) gqa_prefill_kernel<true, true><<<grid, kPfWaves * 64, 0, s>>>(pa);
+      else if (one_block) gqa_prefill_kernel<true, false><<<grid, kPfWaves * 64, 0, s>>>(pa);
+      else if (pa.kn) gqa_prefill_kernel<false, true><<<grid, kPfWaves * 64, 0, s>>>(pa);
+      else gqa_prefill_kernel<false, false><<<grid, kPfWaves * 64, 0, s>>>(pa);
+      if (int rc = check_hip(hipGetLastError(), "gqa_prefill_kernel launch")) return rc;
+    }
   }
   if (a.fused_merge || (flags & AIA_ATTN_SKIP_MERGE)) return AIA_OK;
   return launch_merge(ws, L, g, g.nw, head_dim, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,

@@ -35,6 +35,9 @@ from auto_infer_amd.ops import _check_device_tensor, _ptr, _stream
 
 _ROW_INTS = 8
 _HIP_ERROR = -1000      # _hostpack.upload_pack: statuses at or below are HIP runtime errors
+# the current stream's raw handle without building a Stream object (about 2 us
+# less per step than torch.cuda.current_stream); the public call where absent
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 class DeviceRequestTable:
@@ -291,7 +294,8 @@ def _launch(table, uploader, upd, *, block_size, bt_width, token_ids, positions,
     if _hostpack is not None and uploader.device.type == "cuda":
         # one native call: event wait, staging, copy, event record, pack launch
         sp = (stream.cuda_stream if stream is not None
-              else torch._C._cuda_getCurrentRawStream(uploader.device_index))
+              else _raw_stream(uploader.device_index) if _raw_stream is not None
+              else torch.cuda.current_stream(uploader.device).cuda_stream)
         host, dev, offs, total, wait, rec = uploader.reserve(upd)
         rc = _hostpack.upload_pack(
             upd, _native.address("aia_pack_rows"), host, dev, wait, rec, sp,

@@ -337,13 +337,15 @@ def test_prefill_chunked_items(lqs, lks, hq, hkv, bs):
     check(step)
 
 
-def test_prefill_route_in_a_hip_graph():
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (28, 4)])
+def test_prefill_route_in_a_hip_graph(hq, hkv):
     """The planner, the split-K kernel, the prefill kernel (with chunked
-    items) and the merge captured in one HIP graph: every replay, with eager
-    work and synchronisation between replays, equals the eager result, and
-    the metadata updated in place between replays is picked up."""
-    step = workloads.make_gqa_step(lqs=[128, 1, 2], lks=[6000, 700, 90], num_q_heads=16,
-                                   num_kv_heads=8, block_size=64, seed=71)
+    items) and the merge captured in one HIP graph -- with 4 kv heads the
+    prefill units and split-K ranges are one mixed launch: every replay, with
+    eager work and synchronisation between replays, equals the eager result,
+    and the metadata updated in place between replays is picked up."""
+    step = workloads.make_gqa_step(lqs=[128, 1, 2], lks=[6000, 700, 90], num_q_heads=hq,
+                                   num_kv_heads=hkv, block_size=64, seed=71)
     q, kc, vc = step.q.to(DEV), step.k_cache.to(DEV), step.v_cache.to(DEV)
     bt = step.block_table.to(DEV)
     cu = torch.tensor([0, *step.cu_seqlens_q], dtype=torch.int32, device=DEV)
@@ -351,7 +353,7 @@ def test_prefill_route_in_a_hip_graph():
     T = step.cu_seqlens_q[-1]
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
-        plan = ops.AttentionPlan(bt, cu, kv, T, 16, 8, 128, 64)
+        plan = ops.AttentionPlan(bt, cu, kv, T, hq, hkv, 128, 64)
         eager = ops.paged_attention_gqa(q, kc, vc, plan, step.scale).clone()
         out = torch.empty_like(eager)
         g = torch.cuda.CUDAGraph()
@@ -382,3 +384,26 @@ def test_prefill_chunk_at_32k_keys():
     many 64-block windows, against the oracle."""
     check(workloads.make_gqa_step(lqs=[512], lks=[32768], num_q_heads=28, num_kv_heads=4,
                                   block_size=128, seed=73))
+
+
+def test_mixed_launch_with_fused_kv_write():
+    """4 kv heads: prefill chunks (routed to prefill units) beside decode and
+    verify rows (split-K ranges) in one mixed launch, with this step's new
+    K/V rows written by the kernel: caches bit-exact, outputs within TOL."""
+    from oracle.paged_attn import kv_write
+    step = workloads.make_gqa_step(lqs=[300, 1, 1, 3, 200, 1], lks=[1300, 900, 50, 400, 200, 3000],
+                                   num_q_heads=28, num_kv_heads=4, block_size=16, seed=33,
+                                   extra_blocks=5)
+    kc, vc = step.k_cache.to(DEV), step.v_cache.to(DEV)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, 28, 4, 128, 16)
+    out = ops.paged_attention_gqa(step.q.to(DEV), kc, vc, plan, step.scale,
+                                  key_new=step.k_new.to(DEV), value_new=step.v_new.to(DEV))
+    torch.cuda.synchronize()
+    ek, ev = step.k_cache.clone(), step.v_cache.clone()
+    kv_write(step.k_new, step.v_new, ek, ev, step.slot_mapping)
+    assert torch.equal(kc.cpu(), ek) and torch.equal(vc.cpu(), ev)
+    step.k_cache, step.v_cache = ek, ev
+    err = (out.float().cpu() - oracle(step)).abs().max().item()
+    print(f"max-abs err {err:.3e}", flush=True)
+    assert err <= TOL

@@ -256,18 +256,6 @@ constexpr int kPlanRegChunks = 8;        // segments kept in registers: 8 x 1024
 #endif
 constexpr int kPadBelow = AIA_PAD_BELOW;  // pad segments when ranges are shorter (tiles)
 
-// Key ranges.  A plan cuts its T tiles into R ranges with boundaries
-// b_w = floor(w T / R), so ranges differ by at most one tile and every
-// work-group slot w < R gets one; tile t then lies in range
-// ceil((t + 1) R / T) - 1.  (Padded plans have T = R x tpw: ranges of exactly
-// tpw tiles.)
-__device__ __forceinline__ int range_begin(int w, int nr, int nt) {
-  return (int)((int64_t)w * nt / nr);
-}
-__device__ __forceinline__ int range_of(int t, int nr, int nt) {
-  return (int)(((int64_t)(t + 1) * nr + nt - 1) / nt) - 1;
-}
-
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ kvlen,
     const int32_t* __restrict__ block_table, int64_t bt_stride, int32_t block_size,
@@ -500,9 +488,6 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     }
     total_tiles = carry;
   }
-  // ranges: padded plans cut exactly at multiples of tpw; otherwise every
-  // slot takes floor / ceil (T / waves) tiles
-  const int nranges = total_tiles == 0 ? 0 : pad ? total_tiles / tpw : min(waves, total_tiles);
   __syncthreads();   // request metadata in LDS is no longer needed
 
   // segments' first tiles into LDS for the per-range search
@@ -532,8 +517,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
         tb = seg[(int64_t)s * 8 + 5];
         nt = seg[(int64_t)s * 8 + 6] - tb;
       }
-      np = nt > 0 ? range_of(tb + nt - 1, nranges, total_tiles) - range_of(tb, nranges, total_tiles) + 1
-                  : 0;
+      np = (tb + nt - 1) / tpw - tb / tpw + 1;
     }
     // merge work of a split segment: one record per (kv head, slice of 64
     // elements of its row span), so the merge kernel visits only real work
@@ -575,7 +559,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     carry += tot;
   }
   if (tid == 0) {
-    hdr[0] = nseg; hdr[1] = total_tiles; hdr[2] = nranges; hdr[3] = carry; hdr[4] = waves;
+    hdr[0] = nseg; hdr[1] = total_tiles; hdr[2] = tpw; hdr[3] = carry; hdr[4] = waves;
     hdr[5] = mcarry; hdr[6] = units; hdr[7] = pmerges;
     // sentinel record so readers may look one past the end
     int* r = seg + (int64_t)nseg * 8;
@@ -586,13 +570,13 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
 
   // 4) per-range record (see kRecInts)
   for (int w = tid; w < waves; w += kPlanThreads) {
+    const int t0 = w * tpw;
     int* out = wave_rec + (int64_t)w * kRecInts;
-    if (w >= nranges) {
-      out[0] = -1; out[1] = 0; out[2] = 0; out[3] = nranges;
+    if (t0 >= total_tiles) {
+      out[0] = -1; out[1] = 0; out[2] = 0; out[3] = tpw;
       continue;
     }
-    const int t0 = range_begin(w, nranges, total_tiles);
-    const int t1 = range_begin(w + 1, nranges, total_tiles);
+    const int t1 = min(total_tiles, t0 + tpw);
     int lo = 0, hi = nseg - 1;  // last s with tile_begin <= t0
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -605,7 +589,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       const int tb = tb_lds ? lds[mid] : seg[(int64_t)mid * 8 + 5];
       if (tb < t1) lo2 = mid; else hi2 = mid - 1;
     }
-    out[0] = lo; out[1] = t0; out[2] = t1; out[3] = nranges;
+    out[0] = lo; out[1] = t0; out[2] = t1; out[3] = tpw;
     const int* r = seg + (int64_t)lo * 8;
     int rr[8];
 #pragma unroll
@@ -738,8 +722,7 @@ constexpr int kPipe = AIA_PIPE;
 // token are skipped (a uniform branch), so a decode segment costs one block.
 template <int RB, int D>
 __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, int s, int lt0,
-                                            int lt1, int w, int nranges, int ntiles, uint16_t* vt,
-                                            int lane,
+                                            int lt1, int w, int tpw, uint16_t* vt, int lane,
                                             int wid, bool use_pre, int pre) {
   constexpr int KJ = D / 32;   // 32-dim MFMA k-steps = 16-byte chunks per lane and row
   constexpr int DT = D / 16;   // 16-dim output tiles
@@ -930,8 +913,8 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   for (int r = 0; r < RB; ++r) {
     lsum[r] = aia::group4_sum(lsum[r]);
   }
-  const int first_wave = range_of(tile_begin, nranges, ntiles);
-  const int nparts = range_of(tile_end - 1, nranges, ntiles) - first_wave + 1;
+  const int first_wave = tile_begin / tpw;
+  const int nparts = (tile_end - 1) / tpw - first_wave + 1;
   constexpr int seg_rows = RB * kRows;
   if (nparts == 1) {
 #pragma unroll
@@ -1090,9 +1073,8 @@ __device__ __forceinline__ void gqa_attn_body(const AttnArgs& a, int bid, int nb
   const int ngroups = (a.hkv + NW - 1) / NW, nhb = (a.group + a.hb - 1) / a.hb;
   int s = wr[0];
   int t = wr[1];
-  const int t_end = wr[2], nranges = wr[3], s_last = wr[13];
-  if (s < 0 || s >= nseg || t < 0 || t >= t_end || t_end > total_tiles || nranges < 1 ||
-      w >= nranges ||
+  const int t_end = wr[2], tpw = wr[3], s_last = wr[13];
+  if (s < 0 || s >= nseg || t < 0 || t >= t_end || t_end > total_tiles || tpw < 1 ||
       s_last < s || s_last >= nseg)
     return;
   int rec[8];
@@ -1105,8 +1087,8 @@ __device__ __forceinline__ void gqa_attn_body(const AttnArgs& a, int bid, int nb
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
       if ((rec[1] & 0xffff) * NW + wid < a.hkv)
-        gqa_segment<RB, D>(a, rec, s, t - rec[5], chunk_end - rec[5], w, nranges, total_tiles, vt,
-                           lane, wid, first, pre);
+        gqa_segment<RB, D>(a, rec, s, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane, wid, first,
+                        pre);
       first = false;
       t = chunk_end;
       if (t >= t_end) break;
@@ -1767,8 +1749,7 @@ struct MlaArgs {
 // verify or prefill step reads its keys 1/RB as often.
 template <int RB>
 __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, int lt0, int lt1,
-                                            int w, int nranges, int ntiles, uint16_t* vt, float* sx,
-                                            float* smax,
+                                            int w, int tpw, uint16_t* vt, float* sx, float* smax,
                                             int lane, int wid, bool use_pre, int pre) {
   const int n = lane & 15, g = lane >> 4;
   const int b = rec[0], hbi = (rec[1] >> 16) & 0x3fff;
@@ -1927,8 +1908,8 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
 
 #pragma unroll
   for (int r = 0; r < RB; ++r) lsum[r] = aia::group4_sum(lsum[r]);
-  const int first_wave = range_of(tile_begin, nranges, ntiles);
-  const int nparts = range_of(tile_end - 1, nranges, ntiles) - first_wave + 1;
+  const int first_wave = tile_begin / tpw;
+  const int nparts = (tile_end - 1) / tpw - first_wave + 1;
   const int d0 = 128 * wid;
   constexpr int seg_rows = RB * kRows;
   if (nparts == 1) {
@@ -2008,9 +1989,8 @@ void mla_attn_kernel(MlaArgs a) {
   const int nhb = (a.group + a.hb - 1) / a.hb;
   int s = wr[0];
   int t = wr[1];
-  const int t_end = wr[2], nranges = wr[3], s_last = wr[13];
-  if (s < 0 || s >= nseg || t < 0 || t >= t_end || t_end > total_tiles || nranges < 1 ||
-      w >= nranges ||
+  const int t_end = wr[2], tpw = wr[3], s_last = wr[13];
+  if (s < 0 || s >= nseg || t < 0 || t >= t_end || t_end > total_tiles || tpw < 1 ||
       s_last < s || s_last >= nseg)
     return;
   int rec[8];
@@ -2021,8 +2001,8 @@ void mla_attn_kernel(MlaArgs a) {
     if (!rec_ok(rec, total_tiles, a.batch, a.tokens, 1, nhb)) return;
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
-      mla_segment<RB>(a, rec, t - rec[5], chunk_end - rec[5], w, nranges, total_tiles, vt_all[wid],
-                      sx, smax, lane, wid, first, pre);
+      mla_segment<RB>(a, rec, t - rec[5], chunk_end - rec[5], w, tpw, vt_all[wid], sx, smax, lane,
+                      wid, first, pre);
       first = false;
       t = chunk_end;
       if (t >= t_end) break;

@@ -720,7 +720,9 @@ constexpr int kPipe = AIA_PIPE;
 // (qb = 16 / hb).  Every K/V tile is loaded once and used by all blocks, so a
 // prefill chunk reads its keys 1/RB as often; blocks past the segment's last
 // token are skipped (a uniform branch), so a decode segment costs one block.
-template <int RB, int D>
+// FM: the optional in-kernel merge is compiled in (its own instantiation,
+// so the default kernel carries none of its code).
+template <int RB, int D, bool FM>
 __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, int s, int lt0,
                                             int lt1, int w, int tpw, uint16_t* vt, int lane,
                                             int wid, bool use_pre, int pre) {
@@ -932,7 +934,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
     }
   } else {
     const int part = part_base + (w - first_wave);
-    if (D == 128 && a.fused_merge) {   // lanes x 2 dims cover a 128-wide row
+    if (FM && D == 128) {   // lanes x 2 dims cover a 128-wide row
       // In-kernel merge.  Partials go out with agent-coherent stores (sc1,
       // written through past the per-XCD L2), the wave waits for them to
       // complete, then bumps the segment's per-head counter; the wave that
@@ -1056,8 +1058,8 @@ __device__ __forceinline__ int xcd_range(int b, int n) {
 }
 
 // One work-group per key range, one wave per kv head of the segment's group.
-// D: head dim, 128 or 64.
-template <int NW, int RB, int D>
+// D: head dim, 128 or 64; FM: the in-kernel merge variant.
+template <int NW, int RB, int D, bool FM>
 #ifndef AIA_GQA_WAVES_PER_EU
 #define AIA_GQA_WAVES_PER_EU 2
 #endif
@@ -1087,7 +1089,7 @@ __device__ __forceinline__ void gqa_attn_body(const AttnArgs& a, int bid, int nb
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
       if ((rec[1] & 0xffff) * NW + wid < a.hkv)
-        gqa_segment<RB, D>(a, rec, s, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane, wid, first,
+        gqa_segment<RB, D, FM>(a, rec, s, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane, wid, first,
                         pre);
       first = false;
       t = chunk_end;
@@ -1100,11 +1102,11 @@ __device__ __forceinline__ void gqa_attn_body(const AttnArgs& a, int bid, int nb
   }
 }
 
-template <int NW, int RB, int D>
+template <int NW, int RB, int D, bool FM>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(AIA_GQA_WAVES_PER_EU, AIA_GQA_WAVES_PER_EU)))
 void gqa_attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vt_all[NW][kTile * kVStride];
-  gqa_attn_body<NW, RB, D>(a, blockIdx.x, gridDim.x, vt_all);
+  gqa_attn_body<NW, RB, D, FM>(a, blockIdx.x, gridDim.x, vt_all);
 }
 
 // ---------------------------------------------------------------- prefill
@@ -1531,7 +1533,7 @@ void gqa_mixed_kernel(AttnArgs a, PrefillArgs pa, int npf, int ndec) {
   if (prefill)
     gqa_prefill_body<ONE_BLOCK, FUSED>(pa, idx, ks, vs);
   else
-    gqa_attn_body<kPfWaves, 1, kHeadDim>(a, idx, ndec,
+    gqa_attn_body<kPfWaves, 1, kHeadDim, false>(a, idx, ndec,
                                          reinterpret_cast<uint16_t(*)[kTile * kVStride]>(&ks[0][0]));
 }
 
@@ -2190,11 +2192,13 @@ extern "C" int aia_paged_attention_gqa(
     else gqa_mixed_kernel<false, false><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf, waves);
     if (int rc = check_hip(hipGetLastError(), "gqa_mixed_kernel launch")) return rc;
   } else {
-#define AIA_GQA_LAUNCH_D(NW, D)                                                   \
-  (g.rb == 2 ? gqa_attn_kernel<NW, 2, D><<<waves, 64 * NW, 0, s>>>(a)            \
-             : gqa_attn_kernel<NW, 1, D><<<waves, 64 * NW, 0, s>>>(a))
-#define AIA_GQA_LAUNCH(NW) \
-  (head_dim == 64 ? AIA_GQA_LAUNCH_D(NW, 64) : AIA_GQA_LAUNCH_D(NW, kHeadDim))
+#define AIA_GQA_LAUNCH_D(NW, D, FM)                                               \
+  (g.rb == 2 ? gqa_attn_kernel<NW, 2, D, FM><<<waves, 64 * NW, 0, s>>>(a)        \
+             : gqa_attn_kernel<NW, 1, D, FM><<<waves, 64 * NW, 0, s>>>(a))
+#define AIA_GQA_LAUNCH(NW)                                                        \
+  (head_dim == 64 ? AIA_GQA_LAUNCH_D(NW, 64, false)                               \
+   : a.fused_merge ? AIA_GQA_LAUNCH_D(NW, kHeadDim, true)                         \
+                   : AIA_GQA_LAUNCH_D(NW, kHeadDim, false))
     switch (g.nw) {
       case 1: AIA_GQA_LAUNCH(1); break;
       case 2: AIA_GQA_LAUNCH(2); break;

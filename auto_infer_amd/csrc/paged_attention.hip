@@ -256,6 +256,16 @@ constexpr int kPlanRegChunks = 8;        // segments kept in registers: 8 x 1024
 #endif
 constexpr int kPadBelow = AIA_PAD_BELOW;  // pad segments when ranges are shorter (tiles)
 
+// Padded MLA plans: a request's tiles are split over its ranges evenly
+// (sizes floor / ceil of nt / k, never crossing requests) and the ranges are
+// dealt to work-group slots by size in a snake order over the CUs' slots
+// (slots w, w + kMlaCUs, w + 2 kMlaCUs share a CU: work-groups go out one
+// per CU per round), so every CU gets about the mean number of tiles.
+constexpr int kMlaCUs = 256;
+#ifndef AIA_MLA_BALANCE
+#define AIA_MLA_BALANCE 1
+#endif
+
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ kvlen,
     const int32_t* __restrict__ block_table, int64_t bt_stride, int32_t block_size,
@@ -502,6 +512,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   }
 
   // 3) partial slots: a segment split over k ranges owns k consecutive slots
+  const int pb0 = nseg + 1;     // LDS: segments' first partial slots (balanced MLA plans)
+  const bool bal = AIA_MLA_BALANCE && pad && dv == 512 && waves % kMlaCUs == 0 &&
+                   2 * (nseg + 1) + 32 <= kPlanLds;
   carry = 0;
   int mcarry = 0;
   for (int base = 0, c = 0; base < nseg; base += kPlanThreads, ++c) {
@@ -540,6 +553,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int2 ex2 = block_exclusive_scan2(make_int2(np, mcnt), wave_sums2, &tot2);
     const int ex = ex2.x, tot = tot2.x, mex = ex2.y, mtot = tot2.y;
     if (s < nseg) seg[(int64_t)s * 8 + 7] = carry + ex;
+    if (bal && s < nseg) lds[pb0 + s] = carry + ex;
     if (mcnt > 0) {
       const int seg_rows = kRows * g.rb;
       for (int i = 0; i < mcnt; ++i) {
@@ -569,6 +583,78 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   __syncthreads();
 
   // 4) per-range record (see kRecInts)
+  auto write_rec = [&](int* out, int lo, int lo2, int t0, int t1, int j, int k) {
+    out[0] = lo; out[1] = t0; out[2] = t1; out[3] = tpw;
+    const int* r = seg + (int64_t)lo * 8;
+    int rr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rr[i] = r[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[4 + i] = rr[i];
+    const int b = rr[0], nq = rr[3] & 0xff, lim_base = rr[4];
+    const int visible = max(0, lim_base + nq);
+    const int nblk_vis = (visible + block_size - 1) / block_size;
+    const int blk_base = ((t0 - rr[5]) * kTile) / block_size;
+    out[12] = blk_base; out[13] = lo2; out[14] = j; out[15] = k;
+    const int32_t* btrow = block_table + (int64_t)b * bt_stride;
+    int bv[kRecBlocks];
+#pragma unroll
+    for (int i = 0; i < kRecBlocks; ++i) bv[i] = blk_base + i < nblk_vis ? btrow[blk_base + i] : 0;
+#pragma unroll
+    for (int i = 0; i < kRecBlocks; ++i) out[16 + i] = bv[i];
+  };
+  if (bal) {
+    // ranges = the partial slots of the padded plan; range r is number
+    // r - pb[s] of segment s's k ranges, of floor / ceil (nt / k) tiles
+    int* hist = lds + pb0 + nseg + 1;          // 16 size counters, then 16 offsets
+    int* offs = hist + 16;
+    if (tid == 0) lds[pb0 + nseg] = carry;
+    if (tid < 32) hist[tid] = 0;
+    __syncthreads();
+    const int nr = carry;
+    auto locate = [&](int r, int& s_, int& j_, int& k_, int& a_, int& b_) {
+      int lo_ = 0, hi_ = nseg - 1;   // last s with pb[s] <= r (segments with k = 0 share it)
+      while (lo_ < hi_) {
+        const int mid = (lo_ + hi_ + 1) >> 1;
+        if (lds[pb0 + mid] <= r) lo_ = mid; else hi_ = mid - 1;
+      }
+      s_ = lo_;
+      j_ = r - lds[pb0 + lo_];
+      k_ = lds[pb0 + lo_ + 1] - lds[pb0 + lo_];
+      const int nt_ = seg[(int64_t)lo_ * 8 + 6] - seg[(int64_t)lo_ * 8 + 5];
+      a_ = (int)((int64_t)j_ * nt_ / k_);
+      b_ = (int)((int64_t)(j_ + 1) * nt_ / k_);
+    };
+    for (int r = tid; r < nr; r += kPlanThreads) {
+      int s_, j_, k_, a_, b_;
+      locate(r, s_, j_, k_, a_, b_);
+      atomicAdd(&hist[min(b_ - a_, 15)], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {            // largest ranges first
+      int acc = 0;
+      for (int sz = 15; sz >= 0; --sz) { offs[sz] = acc; acc += hist[sz]; }
+    }
+    __syncthreads();
+    for (int r = tid; r < nr; r += kPlanThreads) {
+      int s_, j_, k_, a_, b_;
+      locate(r, s_, j_, k_, a_, b_);
+      const int rank = atomicAdd(&offs[min(b_ - a_, 15)], 1);
+      const int round = rank / kMlaCUs, pos = rank - round * kMlaCUs;
+      const int slot = round * kMlaCUs + ((round & 1) ? kMlaCUs - 1 - pos : pos);
+      const int tb = seg[(int64_t)s_ * 8 + 5];
+      write_rec(wave_rec + (int64_t)slot * kRecInts, s_, s_, tb + a_, tb + b_, j_, k_);
+    }
+    for (int w = tid; w < waves; w += kPlanThreads) {   // slots no rank maps to
+      const int round = w / kMlaCUs, cu = w - round * kMlaCUs;
+      const int rank = round * kMlaCUs + ((round & 1) ? kMlaCUs - 1 - cu : cu);
+      if (rank >= nr) {
+        int* out = wave_rec + (int64_t)w * kRecInts;
+        out[0] = -1; out[1] = 0; out[2] = 0; out[3] = tpw;
+      }
+    }
+    return;
+  }
   for (int w = tid; w < waves; w += kPlanThreads) {
     const int t0 = w * tpw;
     int* out = wave_rec + (int64_t)w * kRecInts;
@@ -589,24 +675,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       const int tb = tb_lds ? lds[mid] : seg[(int64_t)mid * 8 + 5];
       if (tb < t1) lo2 = mid; else hi2 = mid - 1;
     }
-    out[0] = lo; out[1] = t0; out[2] = t1; out[3] = tpw;
-    const int* r = seg + (int64_t)lo * 8;
-    int rr[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) rr[i] = r[i];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) out[4 + i] = rr[i];
-    const int b = rr[0], nq = rr[3] & 0xff, lim_base = rr[4];
-    const int visible = max(0, lim_base + nq);
-    const int nblk_vis = (visible + block_size - 1) / block_size;
-    const int blk_base = ((t0 - rr[5]) * kTile) / block_size;
-    out[12] = blk_base; out[13] = lo2; out[14] = 0; out[15] = 0;
-    const int32_t* btrow = block_table + (int64_t)b * bt_stride;
-    int bv[kRecBlocks];
-#pragma unroll
-    for (int i = 0; i < kRecBlocks; ++i) bv[i] = blk_base + i < nblk_vis ? btrow[blk_base + i] : 0;
-#pragma unroll
-    for (int i = 0; i < kRecBlocks; ++i) out[16 + i] = bv[i];
+    write_rec(out, lo, lo2, t0, t1, 0, 0);
   }
 }
 
@@ -1751,7 +1820,8 @@ struct MlaArgs {
 // verify or prefill step reads its keys 1/RB as often.
 template <int RB>
 __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, int lt0, int lt1,
-                                            int w, int tpw, uint16_t* vt, float* sx, float* smax,
+                                            int w, int tpw, int jrec, int krec, uint16_t* vt,
+                                            float* sx, float* smax,
                                             int lane, int wid, bool use_pre, int pre) {
   const int n = lane & 15, g = lane >> 4;
   const int b = rec[0], hbi = (rec[1] >> 16) & 0x3fff;
@@ -1910,8 +1980,10 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
 
 #pragma unroll
   for (int r = 0; r < RB; ++r) lsum[r] = aia::group4_sum(lsum[r]);
-  const int first_wave = tile_begin / tpw;
-  const int nparts = (tile_end - 1) / tpw - first_wave + 1;
+  // balanced plans give the range's number within the segment and the
+  // segment's range count in its record; otherwise ranges are tpw tiles
+  const int first_wave = krec > 0 ? w - jrec : tile_begin / tpw;
+  const int nparts = krec > 0 ? krec : (tile_end - 1) / tpw - first_wave + 1;
   const int d0 = 128 * wid;
   constexpr int seg_rows = RB * kRows;
   if (nparts == 1) {
@@ -2003,8 +2075,8 @@ void mla_attn_kernel(MlaArgs a) {
     if (!rec_ok(rec, total_tiles, a.batch, a.tokens, 1, nhb)) return;
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
-      mla_segment<RB>(a, rec, t - rec[5], chunk_end - rec[5], w, tpw, vt_all[wid], sx, smax, lane,
-                      wid, first, pre);
+      mla_segment<RB>(a, rec, t - rec[5], chunk_end - rec[5], w, tpw, wr[14], wr[15], vt_all[wid],
+                      sx, smax, lane, wid, first, pre);
       first = false;
       t = chunk_end;
       if (t >= t_end) break;

@@ -226,13 +226,14 @@ def config3_mla(seed=0, device="cpu"):
                          device=device)
 
 
-def fragmented_block_tables(lks, *, num_blocks, block_size, ops=10000, seed=0):
+def fragmented_block_tables(lks, *, num_blocks, block_size, ops=10000, seed=0, allocator=None):
     """Block tables for requests of context lengths ``lks`` drawn from an
     allocator that first ran a seeded trace of ``ops`` allocate/free
-    operations, so the tables are non-contiguous."""
-    from auto_infer_amd.kv_cache_manager import KVCacheManager
+    operations, so the tables are non-contiguous.
+    ``allocator``: the allocator class (default: the product's)."""
+    from auto_infer_amd.block_allocator import KVCacheManager
     rng = np.random.default_rng(seed)
-    kv = KVCacheManager(num_blocks, block_size)
+    kv = (allocator or KVCacheManager)(num_blocks, block_size)
     live = []
     for _ in range(ops):
         if live and (rng.random() < 0.45 or kv.num_free_blocks() < num_blocks // 4):

@@ -1,17 +1,23 @@
-"""Paged KV block allocator with prefix caching (host side).
+"""Restatement of the reference's paged KV block allocator, as a checker.
 
-Produces the block tables the packing kernel consumes.  Same policy as the
-reference's ``KVCacheManager`` (auto_infer/engine/kv_cache_manager.py:4-124)
-so that a seeded allocate/free trace yields the same block ids: a LIFO free
-list initialised to 0..N-1 (``pop()`` from the tail), refcounts, full-block
-prefix hashes ``hash((prev_hash, chunk))`` with a token-tuple collision
-guard, and freed-but-registered blocks kept in an LRU pool that is evicted
-oldest-first only when the free list is empty.
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).  Follows
+auto_infer/engine/kv_cache_manager.py:4-124 method by method (same state
+dictionaries and the same order of operations), so that a seeded trace
+replayed through it yields the reference's block ids.  The product
+allocator, ``auto_infer_amd.block_allocator.KVCacheManager``, is an
+array-based design of the same policy and is checked against this class on
+random traces (tests/test_block_allocator.py).
+
+Policy: a LIFO free list initialised to 0..N-1 (``pop()`` from the tail,
+:12,41-44); refcounts; full-block prefix hashes ``hash((prev_hash, chunk))``
+with a token-tuple collision guard (:78-111); freed blocks that carry a
+registered hash go to an LRU pool instead of the free list (:63-73) and are
+evicted oldest-first only when the free list is empty (:34-40).
 """
 from collections import OrderedDict
 
 
-class KVCacheManager:
+class RefKVCacheManager:
 
     def __init__(self, num_blocks: int, block_size: int):
         self.num_blocks = num_blocks

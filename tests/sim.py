@@ -9,7 +9,7 @@ allocator mirror.  Used to drive the packers over many steps.
 import numpy as np
 
 from auto_infer_amd.execution import BatchPlan, RequestView, ScheduledRequest
-from auto_infer_amd.kv_cache_manager import KVCacheManager
+from auto_infer_amd.block_allocator import KVCacheManager
 
 
 class _Req:

@@ -36,7 +36,12 @@ class GqaHipBackend(AttentionBackend):
         self.rms_eps = rms_eps
         # With fuse_kv_write, _write_kv defers the slot write to the attention
         # kernel of the following _attn (same cache contents, one launch less);
-        # attention() always calls the two in that order.
+        # attention() always calls the two in that order.  The kernel writes
+        # each new row at the slot its request's block table gives its
+        # position, so the write is deferred only for contexts that declare
+        # their slot_mapping equal to those slots
+        # (ctx.aia_slots_from_block_table, set by this package's packers);
+        # any other slot_mapping is written as given, by its own launch.
         self.fuse_kv_write = fuse_kv_write
         # With fuse_pre_attention, the split / QK-RMSNorm / RoPE steps run as
         # one in-place kernel over the qkv projection (bf16 rounding where the
@@ -85,7 +90,8 @@ class GqaHipBackend(AttentionBackend):
 
     def _write_kv(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor, ctx) -> None:
         cache = ctx.kv_caches[layer_idx]
-        if self.fuse_kv_write and k.shape[0] == ctx.slot_mapping.shape[0]:
+        if (self.fuse_kv_write and getattr(ctx, "aia_slots_from_block_table", False)
+                and k.shape[0] == ctx.slot_mapping.shape[0]):
             self._pending = (layer_idx, id(ctx), k, v)
             return
         ops.write_kv(k, v, cache[0], cache[1], ctx.slot_mapping)

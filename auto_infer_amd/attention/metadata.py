@@ -6,6 +6,8 @@ and a device block table.  Our kernels read device int32 copies and a
 split-K plan; both depend only on the step, so they are built once per
 ``ForwardContext`` (on first use, or by the GPU packer which attaches them
 as ``ctx.aia_cu_seqlens_q`` / ``ctx.aia_seqlens_kv``) and cached on it.
+Every context's plan owns its workspace, so steps in flight on different
+streams do not share scratch memory.
 """
 import torch
 
@@ -26,16 +28,22 @@ def step_plan(ctx, num_q_heads, num_kv_heads, head_dim_v, block_size):
     kv = getattr(ctx, "aia_seqlens_kv", None)
     if cu is None or kv is None:
         dev = bt.device
+        ops.check_lists(ctx.cu_seqlens_q, ctx.seqlens_kv, bt.shape[1] * block_size)
         cu = torch.tensor([0, *ctx.cu_seqlens_q], dtype=torch.int32).to(dev)
         kv = torch.tensor(list(ctx.seqlens_kv), dtype=torch.int32).to(dev)
         ctx.aia_cu_seqlens_q, ctx.aia_seqlens_kv = cu, kv
+        owned = [cu, kv]
+    else:
+        owned = []
     T = int(ctx.cu_seqlens_q[-1]) if len(ctx.cu_seqlens_q) else 0
     if bt.dtype != torch.int32:
         bt = bt.to(torch.int32)
+        owned.append(bt)
+    # each context (one step in flight) gets its own workspace from the
+    # caching allocator: two steps on two streams never share one, and the
+    # plan records every stream it is used on, so the memory is not handed
+    # out again while a step on another stream still reads it
     plan = ops.AttentionPlan(bt, cu, kv, T, num_q_heads, num_kv_heads, head_dim_v, block_size,
-                             workspace=ops.DEFAULT_WORKSPACE.get(
-                                 bt.device, ops.workspace_bytes(kv.shape[0], T, num_q_heads,
-                                                                num_kv_heads, head_dim_v),
-                                 tag=key))
+                             owned=owned)
     plans[key] = plan
     return plan

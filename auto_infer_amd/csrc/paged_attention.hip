@@ -313,7 +313,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   // Query lengths that do not sum to the step's token count can ask for
   // more work than the workspace was sized for: plan nothing rather than
   // write past it.
-  if (carry > seg_cap || pcarry > pf_cap) { carry = 0; pcarry = 0; }
+  int overflow = 0;
+  if (carry > seg_cap || pcarry > pf_cap) { carry = 0; pcarry = 0; overflow = 1; }
   if (tid == 0) req_off[batch] = carry;
 
   // 1b) prefill units.  Items are listed per request, last rows first (under
@@ -383,7 +384,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     }
     units = ucarry;
     pmerges = mcarry2;
-    if (units > pf_unit_cap || pmerges > pf_mrg_cap) { units = 0; pmerges = 0; }
+    if (units > pf_unit_cap || pmerges > pf_mrg_cap) { units = 0; pmerges = 0; overflow = 1; }
   }
   __syncthreads();
   const int nseg = req_off[batch];
@@ -575,6 +576,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   if (tid == 0) {
     hdr[0] = nseg; hdr[1] = total_tiles; hdr[2] = tpw; hdr[3] = carry; hdr[4] = waves;
     hdr[5] = mcarry; hdr[6] = units; hdr[7] = pmerges;
+    hdr[8] = overflow ? -1 : 0;   // status: -1 = the metadata asked for more work than fits
     // sentinel record so readers may look one past the end
     int* r = seg + (int64_t)nseg * 8;
     r[0] = 0; r[1] = 0; r[2] = 0; r[3] = 0; r[4] = 0;
@@ -891,15 +893,6 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
 #pragma unroll
       for (int j = 0; j < KJ; ++j) { kd[4 * j + g] = kk[j]; vd[4 * j + g] = vv[j]; }
     }
-#ifdef AIA_NOCOMPUTE
-    {
-      uint32_t x = 0;
-#pragma unroll
-      for (int j = 0; j < KJ; ++j) x ^= kk[j].x ^ kk[j].y ^ kk[j].z ^ kk[j].w ^ vv[j].x ^ vv[j].y ^ vv[j].z ^ vv[j].w;
-      o[0][0][0] += __uint_as_float(x & 0x3fffffu);
-      return;
-    }
-#endif
     float4_t acc[RB];
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
@@ -1889,15 +1882,6 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
 
   int parity = 0;
   auto compute = [&](int lt, const uint4 (&kk)[5]) {
-#ifdef AIA_NOCOMPUTE
-    {
-      uint32_t x = 0;
-#pragma unroll
-      for (int j = 0; j < 5; ++j) x ^= kk[j].x ^ kk[j].y ^ kk[j].z ^ kk[j].w;
-      o[0][0][0] += __uint_as_float(x & 0x3fffffu);
-      return;
-    }
-#endif
     // partial S^T over this wave's dims, one per row block; the 4 waves'
     // partials are summed through LDS (double-buffered by tile parity)
     float* xb = sx + parity * (4 * RB * 256);
@@ -2187,6 +2171,8 @@ extern "C" int aia_paged_attention_gqa(
   if (block_size <= 0 || num_blocks <= 0)
     return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: block_size %d / num_blocks %d",
                 block_size, num_blocks);
+  if (flags & ~AIA_ATTN_FUSED_MERGE)
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: unknown flags 0x%x", flags);
   if (num_tokens == 0 || batch == 0) return AIA_OK;    // empty step (zero-size tensors)
   if (!query || !key_cache || !value_cache || !block_table || !out || !workspace || !cu_seqlens_q ||
       !seqlens_kv)
@@ -2235,7 +2221,7 @@ extern "C" int aia_paged_attention_gqa(
   a.counters = reinterpret_cast<int32_t*>(ws + L.cnt);
   // (the in-kernel merge exists for head_dim 128; 64 always merges in its own pass)
   a.fused_merge =
-      (flags & AIA_ATTN_FUSED_MERGE) && !(flags & AIA_ATTN_SKIP_MERGE) && head_dim == kHeadDim;
+      (flags & AIA_ATTN_FUSED_MERGE) && head_dim == kHeadDim;
   hipStream_t s = (hipStream_t)stream;
   PrefillArgs pa = {};
   if (L.pf_cap > 0) {
@@ -2293,7 +2279,7 @@ extern "C" int aia_paged_attention_gqa(
       if (int rc = check_hip(hipGetLastError(), "gqa_prefill_kernel launch")) return rc;
     }
   }
-  if (a.fused_merge || (flags & AIA_ATTN_SKIP_MERGE)) return AIA_OK;
+  if (a.fused_merge) return AIA_OK;
   return launch_merge(ws, L, g, g.nw, head_dim, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
                       cu_seqlens_q, s);
 }
@@ -2307,6 +2293,7 @@ extern "C" int aia_paged_attention_mla(
     void* workspace, int64_t workspace_bytes, void* stream) {
   using namespace aia;
   (void)cu_seqlens_q; (void)seqlens_kv;
+  if (flags != 0) return fail(AIA_ERR_INVALID, "aia_paged_attention_mla: flags must be 0");
   if (kv_lora_rank != kMlaV || rope_dim != kMlaK - kMlaV)
     return fail(AIA_ERR_UNSUPPORTED, "aia_paged_attention_mla: latent %d + rope %d (only 512 + 64)",
                 kv_lora_rank, rope_dim);
@@ -2351,7 +2338,6 @@ extern "C" int aia_paged_attention_mla(
   if (g.rb == 2) mla_attn_kernel<2><<<waves, 256, 0, s>>>(a);
   else mla_attn_kernel<1><<<waves, 256, 0, s>>>(a);
   if (int rc = check_hip(hipGetLastError(), "mla_attn_kernel launch")) return rc;
-  if (flags & AIA_ATTN_SKIP_MERGE) return AIA_OK;
   return launch_merge(ws, L, g, 1, kMlaV, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
                       cu_seqlens_q, s);
 }

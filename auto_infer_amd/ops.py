@@ -102,8 +102,8 @@ def mla_kv_latent(ckv_full, norm_weight, eps, cos, sin, out=None):
              "norm_weight must be 512 contiguous values")
     if out is None:
         out = torch.empty(T, 1, MLA_LATENT + MLA_ROPE, dtype=_BF16, device=ckv_full.device)
-    _require(out.is_contiguous() and out.numel() == T * (MLA_LATENT + MLA_ROPE),
-             "out must be a contiguous (T, 1, 576) tensor")
+    _check_out(out, "out", (T, 1, MLA_LATENT + MLA_ROPE), ckv_full.device)
+    _require(out.is_contiguous(), "out must be a contiguous (T, 1, 576) tensor")
     _native.call("aia_mla_kv_latent", _ptr(ckv_full), ckv_full.stride(0), T, _ptr(norm_weight),
                  float(eps), _ptr(cos), cts, _ptr(sin), sts, _ptr(out), MLA_LATENT + MLA_ROPE,
                  _stream(ckv_full.device))
@@ -126,8 +126,7 @@ def mla_q_latent(q, w_uk_t, cos, sin, out=None):
     cts, sts = _rope_rows(cos, "cos", T, MLA_ROPE), _rope_rows(sin, "sin", T, MLA_ROPE)
     if out is None:
         out = torch.empty(T, H, MLA_LATENT + MLA_ROPE, dtype=_BF16, device=q.device)
-    _require(tuple(out.shape) == (T, H, MLA_LATENT + MLA_ROPE) and out.stride(2) == 1,
-             "out must be (T, H, 576) with unit inner stride")
+    _check_out(out, "out", (T, H, MLA_LATENT + MLA_ROPE), q.device)
     _native.call("aia_mla_q_latent", _ptr(q), q.stride(0), q.stride(1), T, H, _ptr(w_uk_t),
                  _ptr(cos), cts, _ptr(sin), sts, _ptr(out), out.stride(0), out.stride(1),
                  _stream(q.device))
@@ -157,9 +156,7 @@ def mla_v_up(o_latent, w_uv, out=None):
              "w_uv must be a contiguous (H, 128, 512) tensor")
     if out is None:
         out = torch.empty(T, H, 128, dtype=_BF16, device=o_latent.device)
-    _check_device_tensor(out, "out", _BF16)
-    _require(tuple(out.shape) == (T, H, 128) and out.stride(2) == 1,
-             "out must be (T, H, 128) with unit inner stride")
+    _check_out(out, "out", (T, H, 128), o_latent.device)
     _native.call("aia_mla_v_up", _ptr(o_latent), o_latent.stride(0), o_latent.stride(1), T, H,
                  _ptr(w_uv), _ptr(out), out.stride(0), out.stride(1), _stream(o_latent.device))
     return out
@@ -255,26 +252,6 @@ def write_kv(key, value, key_cache, value_cache, slot_mapping):
 
 # ---------------------------------------------------------------- attention
 
-class Workspace:
-    """Grow-only device scratch buffers owned by torch, one per (device,
-    tag).  Consecutive steps reuse a buffer in stream order; distinct plans
-    that live at the same time must use distinct tags."""
-
-    def __init__(self):
-        self._buf = {}
-
-    def get(self, device, nbytes, tag=None):
-        key = (torch.device(device), tag)
-        buf = self._buf.get(key)
-        if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=key[0])
-            self._buf[key] = buf
-        return buf
-
-
-DEFAULT_WORKSPACE = Workspace()
-
-
 def workspace_bytes(batch, num_tokens, num_q_heads, num_kv_heads, head_dim_v):
     out = ctypes.c_int64(0)
     _native.call("aia_attn_workspace_bytes", batch, num_tokens, num_q_heads, num_kv_heads,
@@ -294,7 +271,7 @@ class AttentionPlan:
     """
 
     def __init__(self, block_table, cu_seqlens_q, seqlens_kv, num_tokens, num_q_heads,
-                 num_kv_heads, head_dim_v, block_size, num_waves=0, workspace=None):
+                 num_kv_heads, head_dim_v, block_size, num_waves=0, workspace=None, owned=None):
         _check_device_tensor(block_table, "block_table", torch.int32)
         _check_device_tensor(cu_seqlens_q, "cu_seqlens_q", torch.int32)
         _check_device_tensor(seqlens_kv, "seqlens_kv", torch.int32)
@@ -318,8 +295,15 @@ class AttentionPlan:
         nbytes = workspace_bytes(batch, self.num_tokens, num_q_heads, num_kv_heads, head_dim_v)
         if workspace is None:
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=block_table.device)
+        _check_device_tensor(workspace, "workspace", torch.uint8)
         _require(workspace.numel() >= nbytes, "attention workspace too small")
         self.workspace = workspace
+        # streams the plan's own device tensors are known to be used on: the
+        # caching allocator may hand their memory to the allocating stream's
+        # next allocation once they are dropped, so every other stream that
+        # reads or writes them is recorded (Tensor.record_stream)
+        self._streams = {torch.cuda.current_stream(block_table.device)}
+        self._owned = [workspace] if owned is None else [workspace, *owned]
         self.replan()
 
     def replan(self):
@@ -327,11 +311,28 @@ class AttentionPlan:
         metadata tensors; graph-capturable.  The plan is then valid on the
         current stream (attention calls on another stream wait for it)."""
         self.stream = torch.cuda.current_stream(self.block_table.device)
+        self._use_on(self.stream)
         _native.call("aia_attn_plan", _ptr(self.cu_seqlens_q), _ptr(self.seqlens_kv),
                      _ptr(self.block_table), self.block_table.stride(0), self.block_size,
                      self.batch, self.num_tokens, self.num_q_heads, self.num_kv_heads,
                      self.head_dim_v, self.num_waves, _ptr(self.workspace),
                      self.workspace.numel(), _stream(self.block_table.device))
+
+    def _use_on(self, stream):
+        if stream not in self._streams:
+            self._streams.add(stream)
+            for t in self._owned:
+                t.record_stream(stream)
+
+    def status(self):
+        """Synchronising check of the last plan: raises ValueError if the
+        planner found more work than the workspace was sized for (query
+        lengths that do not add up to ``num_tokens``); the kernels then ran
+        an empty plan and left the output unwritten."""
+        code = int(self.workspace[32:36].view(torch.int32).item())
+        if code != 0:
+            raise ValueError(f"attention planner overflow (status {code}): cu_seqlens_q does "
+                             f"not describe {self.num_tokens} query tokens")
 
     @classmethod
     def from_lists(cls, block_table, cu_seqlens_q, seqlens_kv, num_q_heads, num_kv_heads,
@@ -339,30 +340,56 @@ class AttentionPlan:
         """From the reference's host lists (cumulative ends without the
         leading 0, per-request KV lengths)."""
         dev = block_table.device
-        bs = block_size
-        if len(seqlens_kv):
-            _require(block_table.shape[1] * bs >= max(seqlens_kv),
-                     "block_table has fewer columns than the longest context needs")
+        check_lists(cu_seqlens_q, seqlens_kv, block_table.shape[1] * block_size)
         cu = torch.tensor([0, *cu_seqlens_q], dtype=torch.int32).to(dev, non_blocking=True)
         kv = torch.tensor(list(seqlens_kv), dtype=torch.int32).to(dev, non_blocking=True)
         total = cu_seqlens_q[-1] if len(cu_seqlens_q) else 0
         return cls(block_table, cu, kv, total, num_q_heads, num_kv_heads, head_dim_v, block_size,
-                   **kw)
+                   owned=[cu, kv], **kw)
+
+
+def check_lists(cu_seqlens_q, seqlens_kv, max_context):
+    """Host check of the reference's metadata lists (cumulative query ends,
+    per-request KV lengths; forward_context.py:14-15): same length,
+    non-decreasing ends, every KV length within the block table (the
+    kernels read block ids up to it)."""
+    _require(len(cu_seqlens_q) == len(seqlens_kv),
+             "cu_seqlens_q and seqlens_kv must have one entry per request")
+    prev = 0
+    for end, lk in zip(cu_seqlens_q, seqlens_kv):
+        _require(end >= prev, "cu_seqlens_q must be non-decreasing")
+        _require(0 <= lk <= max_context,
+                 f"KV length {lk} does not fit the block table ({max_context} slots)")
+        prev = end
 
 
 def _ready(plan, device):
     """Order the attention launch after the planner: on another stream, make
     the current stream wait for the plan's stream (not allowed while
-    capturing a graph, where the plan must be made on the capturing stream)."""
+    capturing a graph, where the plan must be made on the capturing stream)
+    and record the plan's buffers as in use there."""
     cur = torch.cuda.current_stream(device)
     if cur != plan.stream:
         if torch.cuda.is_current_stream_capturing():
             raise ValueError("attention plan was made on another stream than the one being "
                              "captured; call plan.replan() on the capturing stream")
         cur.wait_stream(plan.stream)
+        plan._use_on(cur)
 
 
-ATTN_SKIP_MERGE = 1         # diagnostic: the split kernel alone, split rows unmerged
+def _check_out(out, name, shape, device):
+    """A caller-supplied output: bf16 on the same GPU, of ``shape``, unit
+    inner stride, rows (heads, dim) not overlapping."""
+    _check_device_tensor(out, name, _BF16)
+    _require(out.device == device, f"{name} must be on {device}")
+    _require(tuple(out.shape) == tuple(shape), f"{name} must have shape {tuple(shape)}, "
+             f"got {tuple(out.shape)}")
+    _require(out.stride(-1) == 1, f"{name} must have unit inner stride")
+    if out.dim() == 3:
+        _require(out.stride(1) >= out.shape[2] and out.stride(0) >= out.shape[1] * out.stride(1),
+                 f"{name} rows must not overlap")
+
+
 ATTN_FUSED_MERGE = 2        # merge split rows inside the split kernel (default: 2nd kernel)
 
 
@@ -390,6 +417,8 @@ def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None, fl
              and bs == plan.block_size, "plan was made for another shape")
     if out is None:
         out = torch.empty(T, hq, d, dtype=_BF16, device=query.device)
+    else:
+        _check_out(out, "out", (T, hq, d), query.device)
     kn_ts = vn_ts = 0
     if key_new is not None or value_new is not None:
         _check_device_tensor(key_new, "key_new", _BF16)
@@ -405,13 +434,6 @@ def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None, fl
                  out.stride(1), _ptr(key_new), _ptr(value_new), kn_ts, vn_ts, plan.num_waves,
                  flags, _ptr(plan.workspace), plan.workspace.numel(), _stream(query.device))
     return out
-
-
-def paged_attention_kernel_only(query, key_cache, value_cache, plan, scale, out=None):
-    """The split-K attention kernel without the merge pass (timing only:
-    rows split over several waves are left unmerged)."""
-    return paged_attention_gqa(query, key_cache, value_cache, plan, scale, out,
-                               flags=ATTN_SKIP_MERGE)
 
 
 MLA_LATENT, MLA_ROPE = 512, 64
@@ -441,6 +463,8 @@ def paged_attention_mla(q_latent, latent_cache, plan, scale, out=None, flags=0):
              "plan was not made for this MLA shape")
     if out is None:
         out = torch.empty(T, h, MLA_LATENT, dtype=_BF16, device=q_latent.device)
+    else:
+        _check_out(out, "out", (T, h, MLA_LATENT), q_latent.device)
     _ready(plan, q_latent.device)
     _native.call("aia_paged_attention_mla", _ptr(q_latent), q_latent.stride(0),
                  q_latent.stride(1), _ptr(latent_cache), _ptr(plan.block_table),

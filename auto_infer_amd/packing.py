@@ -430,6 +430,9 @@ class DeviceBatchPacker:
             kv_caches=kv_caches, is_decode=all_decode)
         ctx.aia_cu_seqlens_q = views[4]
         ctx.aia_seqlens_kv = views[5]
+        # every slot this packer writes is block_table[pos // bs] * bs + pos % bs
+        # of its row's block table, so the attention kernel may do the KV write
+        ctx.aia_slots_from_block_table = True
         return ctx, sample_idx, decode_splice
 
 

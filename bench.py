@@ -14,12 +14,16 @@ Infinity Cache) so KV reads come from HBM.  Steps are replayed from a HIP
 graph captured on the timed stream (the reference replays ACL graphs for
 decode too).
 
+--steps K and --warmup W count layer-steps exactly: W untimed, then K timed
+(the timed K-step region is replayed until it spans ~50 ms; the median
+repeat is reported, with the repeat count and the min / max).
+
 Prints ONE JSON line: the metric (tok/s of the step), the timing, the
-roofline of the attention kernel (algorithmic bytes per launch / kernel
-time against 8 TB/s, with the HBM traffic per launch measured by rocprofv3
-FETCH_SIZE + WRITE_SIZE), the CPU baseline (the oracle on this host's
-cores, a bounded sample) and the other BASELINE configs plus the fused
-kernels either side of the path (``other_configs``).
+roofline of one layer's attention (split-K kernel + merge: algorithmic
+bytes / their time against 8 TB/s, with the HBM traffic per layer measured
+by rocprofv3 FETCH_SIZE + WRITE_SIZE), the CPU baseline (the oracle on this
+host's cores, a bounded sample) and the other BASELINE configs plus the
+fused kernels either side of the path (``other_configs``).
 """
 import argparse
 import json
@@ -179,7 +183,7 @@ def other_configs(stream, only=None):
     def want(key):
         return only is None or only == key
 
-    def gqa(name, step, pools):
+    def gqa(name, step, pools, write=False):
         kcs = [step.k_cache] + [torch.empty_like(step.k_cache).copy_(step.k_cache)
                                 for _ in range(pools - 1)]
         vcs = [step.v_cache] + [torch.empty_like(step.v_cache).copy_(step.v_cache)
@@ -189,10 +193,15 @@ def other_configs(stream, only=None):
                                             step.seqlens_kv, hq, hkv, d, step.k_cache.shape[1])
         out = torch.empty(step.num_tokens, hq, d, dtype=torch.bfloat16, device=dev)
         torch.cuda.synchronize()
+        kn = step.k_new if write else None
+        vn = step.v_new if write else None
         us = _time_graph(lambda i: ops.paged_attention_gqa(step.q, kcs[i % pools],
                                                            vcs[i % pools], plan, step.scale,
-                                                           out=out), stream, 5, 2 * pools)
+                                                           out=out, key_new=kn, value_new=vn),
+                         stream, 5, 2 * pools)
         by = step.kv_bytes_read() + 2 * out.numel() * 2
+        if write:      # new rows read once, written once per cache
+            by += 2 * 2 * step.k_new.numel() * 2
         # QK^T and PV flops over the visible (causal) keys of every query row
         starts = [0] + list(step.cu_seqlens_q[:-1])
         vis = sum(lq * (lk - lq) + lq * (lq + 1) // 2 for lq, lk in
@@ -230,8 +239,8 @@ def other_configs(stream, only=None):
                 on_device(workloads.subset(full, list(range(3, 515)))[0]), 1)
         del full
     if want("configs[3]"):
-        note("configs[3] MTP verify")
-        gqa("configs[3]_mtp_verify", workloads.config4_mtp(seed=0, device=dev), 3)
+        note("configs[3] MTP verify (with the KV write of both query tokens)")
+        gqa("configs[3]_mtp_verify", workloads.config4_mtp(seed=0, device=dev), 3, write=True)
     if want("configs[2]"):
         note("configs[2] absorbed MLA")
 
@@ -465,50 +474,57 @@ def main():
     plan = ops.AttentionPlan(bt, cu, kvl, T, hq, hkv, d, step.k_cache.shape[1])
     torch.cuda.synchronize()
 
-    def model_step():
-        """Planner once, then L layers of (KV write + attention)."""
-        plan.replan()
-        for layer in range(L):
-            # the KV slot write of the 16 new rows runs inside the attention kernel
+    def layer_steps(start, n):
+        """n layer-steps from layer-step index `start`: the planner at every
+        model-step boundary (its plan serves the L layers), then each layer's
+        attention with the KV write of the 16 new rows fused into it."""
+        for i in range(start, start + n):
+            layer = i % L
+            if layer == 0 or i == start:
+                plan.replan()
             ops.paged_attention_gqa(q, kcs[layer], vcs[layer], plan, step.scale, out=out,
                                     key_new=k_new, value_new=v_new)
 
     stream = torch.cuda.Stream(device=dev)
-    with torch.cuda.stream(stream):
-        for _ in range(3):
-            model_step()
-    stream.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        model_step()
-    # Graph replays cover L layer-steps each.
-    n_replay = max(1, (args.steps + L - 1) // L)
-    n_warm = max(1, (args.warmup + L - 1) // L)
-    with torch.cuda.stream(stream):
-        for _ in range(n_warm):
-            graph.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(n_replay):
-            graph.replay()
-        e1.record(stream)
-    torch.cuda.synchronize()
-    steps = n_replay * L
-    ms_per_step = e0.elapsed_time(e1) / steps
 
-    # Dominant kernel alone (the split-K attention kernel, without its merge
-    # pass): back-to-back launches on the same stream, averaged over the
-    # timed region (HIP events on that stream).
+    def capture(fn):
+        with torch.cuda.stream(stream):
+            fn()                                   # warm the launch path outside the graph
+            stream.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                fn()
+        return g
+
+    K, W = args.steps, args.warmup
+    g_warm = capture(lambda: layer_steps(0, W)) if W > 0 else None
+    g_timed = capture(lambda: layer_steps(W, K))
+    # The timed region (exactly K layer-steps) is replayed R times so that it
+    # spans at least ~50 ms in total; ms_per_step is the median repeat.
+    reps = []
+    with torch.cuda.stream(stream):
+        if g_warm is not None:
+            g_warm.replay()
+        torch.cuda.synchronize()
+        while len(reps) < 3 or (sum(reps) < 50.0 and len(reps) < 1000):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            g_timed.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            reps.append(e0.elapsed_time(e1))
+    reps_sorted = sorted(reps)
+    ms_per_step = reps_sorted[len(reps) // 2] / K
+
+    # Dominant kernel: the attention of one layer (split-K kernel + its merge
+    # pass; the planner is timed on its own below), L layers back to back in
+    # a graph on `stream`, HIP events on that stream around 50 replays.
     n_k = 50 * L
     with torch.cuda.stream(stream):
-        for i in range(L):
-            ops.paged_attention_gqa(q, kcs[i], vcs[i], plan, step.scale, out=out)
         a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        g2 = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g2, stream=stream):
-            for i in range(L):
-                ops.paged_attention_kernel_only(q, kcs[i], vcs[i], plan, step.scale, out=out)
+        g2 = capture(lambda: [ops.paged_attention_gqa(q, kcs[i], vcs[i], plan, step.scale,
+                                                      out=out) for i in range(L)])
         g2.replay()
         torch.cuda.synchronize()
         a0.record(stream)
@@ -584,8 +600,10 @@ def main():
         "value": round(B / step_s, 1),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": n_warm * L,
+        "steps": K,
+        "warmup": W,
+        "timed_repeats": len(reps),
+        "ms_per_step_min_max": [round(reps_sorted[0] / K, 5), round(reps_sorted[-1] / K, 5)],
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -597,10 +615,13 @@ def main():
                         "batch 16, Lq 1, Lk~U[128,2048], block 128, 512-block pool/layer",
             "batch": B, "kv_tokens": int(sum(step.seqlens_kv)),
             "layers_rotated": L, "timing": "HIP graph replay, HIP events",
+            "step": "one attention layer: KV write of the 16 new rows fused into split-K "
+                    "attention + merge, and the planner once per L layer-steps; value = 16 "
+                    "tokens / layer-step time (tok/s per attention layer)",
         },
         "step_hbm_GBps": round(step_alg_bytes / step_s / 1e9, 1),
         "step_frac_of_peak": round(step_alg_bytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
-        "attention_kernel_us": round(attn_us, 3),
+        "attention_us": round(attn_us, 3),
         "packing_us_per_step": round(pack_host_us + plan_us, 2),
         "packing": {"batch_plan_to_device_metadata_host_us": round(pack_host_us, 2),
                     "attention_planner_device_us": round(plan_us, 3),

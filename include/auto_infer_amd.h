@@ -69,7 +69,12 @@ int aia_attn_workspace_bytes(int32_t batch, int32_t num_tokens,
  * into key chunks when they are too few to fill the chip).  The plan depends
  * only on step metadata, so one plan serves every layer of the step.
  * num_waves: number of key ranges (work-groups); 0 picks the default (about
- * 2048 waves in flight for GQA, 768 four-wave groups for MLA). */
+ * 2048 waves in flight for GQA, 768 four-wave groups for MLA).
+ * Status: the int32 at byte offset 32 of the workspace is 0 after a good
+ * plan and -1 when the query lengths ask for more work than a step of
+ * num_tokens rows can hold (cu_seqlens_q not ending at num_tokens, or
+ * decreasing); the plan is then empty and the attention calls leave `out`
+ * unwritten.  Reading it is the caller's choice (it costs a sync). */
 int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
                   const int32_t* block_table, int32_t block_table_stride,
                   int32_t block_size, int32_t batch, int32_t num_tokens,
@@ -103,9 +108,7 @@ int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
  * (O, max, sum) partials by log-sum-exp, by default in a second kernel.
  * flags: AIA_ATTN_FUSED_MERGE merges in the split kernel instead (the last
  * work-group of a split row to finish merges it, via agent-coherent partial
- * stores and a per-segment counter); AIA_ATTN_SKIP_MERGE launches only the
- * split kernel (diagnostic: split rows are left unmerged). */
-#define AIA_ATTN_SKIP_MERGE 1
+ * stores and a per-segment counter).  Other bits must be 0. */
 #define AIA_ATTN_FUSED_MERGE 2
 int aia_paged_attention_gqa(const void* query, int64_t q_token_stride,
                             int64_t q_head_stride,
@@ -134,7 +137,7 @@ int aia_paged_attention_gqa(const void* query, int64_t q_token_stride,
  * latent_cache: contiguous (num_blocks, block_size, 1, 576).
  * out:          (num_tokens, num_heads, 512).
  * The plan must come from aia_attn_plan(num_q_heads = num_heads,
- * num_kv_heads = 1, head_dim_v = 512, same num_waves). */
+ * num_kv_heads = 1, head_dim_v = 512, same num_waves).  flags must be 0. */
 int aia_paged_attention_mla(const void* q_latent, int64_t q_token_stride,
                             int64_t q_head_stride, const void* latent_cache,
                             const int32_t* block_table, int32_t block_table_stride,

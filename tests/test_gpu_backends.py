@@ -25,8 +25,10 @@ def rope_tables(positions, dim, base=10000.0):
     return emb.cos()[:, None].bfloat16(), emb.sin()[:, None].bfloat16()
 
 
-def make_ctx(backend, caches, plan_rows, block_size):
-    """plan_rows: list of (start, n, block_ids) per request."""
+def make_ctx(backend, caches, plan_rows, block_size, derived=True):
+    """plan_rows: list of (start, n, block_ids) per request.  ``derived``:
+    declare the slot mapping block-table derived (as this package's packers
+    do), which lets the GQA backend fuse the KV write into attention."""
     slots, pos, cu, kv, acc = [], [], [], [], 0
     width = max(len(r[2]) for r in plan_rows)
     bt = torch.zeros(len(plan_rows), width, dtype=torch.int32)
@@ -39,11 +41,14 @@ def make_ctx(backend, caches, plan_rows, block_size):
         cu.append(acc)
         kv.append(start + n)
     positions = torch.tensor(pos)
-    return ForwardContext(
+    ctx = ForwardContext(
         token_ids=torch.zeros(acc, dtype=torch.long, device=DEV), positions=positions.to(DEV),
         slot_mapping=torch.tensor(slots, dtype=torch.int32, device=DEV), block_table=bt.to(DEV),
         cu_seqlens_q=cu, seqlens_kv=kv, attn_mask=None, attn_backend=backend,
-        kv_caches=caches, is_decode=all(n == 1 for _, n, _ in plan_rows)), positions
+        kv_caches=caches, is_decode=all(n == 1 for _, n, _ in plan_rows))
+    if derived:
+        ctx.aia_slots_from_block_table = True
+    return ctx, positions
 
 
 class _Capture:
@@ -306,3 +311,105 @@ def test_gqa_backend_head_dim_64_qwen25_05b_shape():
         [(38, 1, a), (71, 50, b)],                 # decode + chunked continuation
     ]
     run_pair(hip, twin, steps, caches_h, caches_r, bs, hidden, seed=12)
+
+
+def _gqa_weights(seed, hq, hkv, d, hidden):
+    g = torch.Generator().manual_seed(seed)
+    p = "model.layers.0.self_attn."
+    w = {p + "qkv_proj.weight": (torch.randn((hq + 2 * hkv) * d, hidden, generator=g) / 16).bfloat16(),
+         p + "o_proj.weight": (torch.randn(hidden, hq * d, generator=g) / 32).bfloat16()}
+    return {k: v.to(DEV) for k, v in w.items()}, g
+
+
+def test_gqa_backend_writes_a_foreign_slot_mapping_as_given():
+    """A context whose slot_mapping is not the block-table slot of each
+    position (a caller's own padding or scratch slots) and that does not
+    declare it derived: the backend writes K/V where slot_mapping says (the
+    reference's write_kv semantics, base.py:41-45) instead of fusing the
+    write, so the caches match the oracle bit for bit and attention reads
+    what the block table points at."""
+    hq, hkv, d, hidden, bs = 8, 2, 128, 256, 16
+    w, g = _gqa_weights(21, hq, hkv, d, hidden)
+    kw = dict(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, scale=d ** -0.5, num_layers=1,
+              device=DEV, dtype=torch.bfloat16, w=w, rms_eps=1e-6)
+    hip = GqaHipBackend(**kw)
+    twin = oracle_twin(GqaHipBackend)(**kw)
+    ch, cr = hip.alloc_kv_caches(16, bs), twin.alloc_kv_caches(16, bs)
+    rows = [(20, 3, [2, 5]), (7, 1, [9])]
+    T = 4
+    x = (torch.randn(T, hidden, generator=g) * 0.5).bfloat16().to(DEV)
+    ctx_h, positions = make_ctx(hip, ch, rows, bs, derived=False)
+    ctx_r, _ = make_ctx(twin, cr, rows, bs, derived=False)
+    # the first request's rows go to scratch block 14, the decode row to 15
+    foreign = torch.tensor([14 * bs, 14 * bs + 1, 14 * bs + 2, 15 * bs + 3], dtype=torch.int32,
+                           device=DEV)
+    ctx_h.slot_mapping = ctx_r.slot_mapping = foreign
+    cos, sin = rope_tables(positions, d)
+    ctx_h.cos = ctx_r.cos = cos.to(DEV)
+    ctx_h.sin = ctx_r.sin = sin.to(DEV)
+    twin.captured = []
+    out_h = hip.attention(0, x, ctx_h)
+    out_r = twin.attention(0, x, ctx_r)
+    torch.cuda.synchronize()
+    assert torch.equal(ch[0].cpu(), cr[0].cpu()), "KV cache differs from the oracle's"
+    assert ch[0][:, 14].abs().sum().item() > 0 and ch[0][:, 2].abs().sum().item() == 0
+    scale = out_r.float().abs().max().item()
+    assert (out_h.float() - out_r.float()).abs().max().item() <= TOL * max(1.0, scale)
+
+
+def test_two_contexts_in_flight_on_two_streams_through_the_backends():
+    """Two steps of different shapes through GqaHipBackend.attention and
+    MlaHipBackend.attention, launched back to back on two streams with no
+    synchronisation between them (the reference runs per-slot steps on
+    their own streams, graph_decode_runner.py:202-207, 475-481): each
+    context plans into its own workspace, and both results match the
+    oracle."""
+    from oracle.paged_attn import mla_absorbed_attention as mla_ref
+    hq, hkv, d, hidden, bs = 8, 2, 128, 256, 16
+    w, g = _gqa_weights(31, hq, hkv, d, hidden)
+    kw = dict(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, scale=d ** -0.5, num_layers=1,
+              device=DEV, dtype=torch.bfloat16, w=w, rms_eps=1e-6)
+    gqa = GqaHipBackend(**kw)
+    nh = 16
+    mla = MlaHipBackend({}, num_heads=nh, qk_nope=128, qk_rope=64, v_head_dim=128,
+                        kv_lora_rank=512, q_lora_rank=None, rms_eps=1e-6,
+                        softmax_scale=192 ** -0.5, num_layers=1, device=DEV,
+                        dtype=torch.bfloat16)
+    gc = gqa.alloc_kv_caches(64, bs)
+    mc = mla.alloc_kv_caches(64, bs)
+    gc[0].normal_(generator=None)
+    mc[0][0].normal_()
+    perm = torch.randperm(64, generator=g).tolist()
+    rows_a = [(300, 1, perm[:19]), (40, 90, perm[19:28]), (5, 1, perm[28:29])]
+    rows_b = [(600, 1, perm[:38]), (100, 2, perm[38:45]), (33, 1, perm[45:48])]
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    ctx_a, _ = make_ctx(gqa, gc, rows_a, bs)
+    ctx_b, _ = make_ctx(mla, mc, rows_b, bs)
+    Ta, Tb = sum(r[1] for r in rows_a), sum(r[1] for r in rows_b)
+    qa = (torch.randn(Ta, hq, d, generator=g) / 4).bfloat16().to(DEV)
+    qb = torch.randn(Tb, nh, 576, generator=g).bfloat16().to(DEV)
+    torch.cuda.synchronize()
+    outs = {}
+    for rep in range(3):
+        with torch.cuda.stream(s1):
+            oa = gqa._attn(0, qa, None, None, ctx_a)
+        with torch.cuda.stream(s2):
+            ob = mla._attn(0, qb, None, None, ctx_b)
+        outs.setdefault("a", []).append(oa)
+        outs.setdefault("b", []).append(ob)
+        if rep == 0:      # new contexts for the later rounds: fresh plans and workspaces
+            ctx_a, _ = make_ctx(gqa, gc, rows_a, bs)
+            ctx_b, _ = make_ctx(mla, mc, rows_b, bs)
+    torch.cuda.synchronize()
+    assert ctx_a._aia_plans and ctx_b._aia_plans
+    pa = next(iter(ctx_a._aia_plans.values()))
+    pb = next(iter(ctx_b._aia_plans.values()))
+    assert pa.workspace.data_ptr() != pb.workspace.data_ptr()
+    ref_a = paged_attention(qa.cpu(), gc[0][0].cpu(), gc[0][1].cpu(), ctx_a.block_table.cpu(),
+                            ctx_a.cu_seqlens_q, ctx_a.seqlens_kv, d ** -0.5)
+    ref_b = mla_ref(qb.cpu(), mc[0][0].cpu(), ctx_b.block_table.cpu(), ctx_b.cu_seqlens_q,
+                    ctx_b.seqlens_kv, 192 ** -0.5, 512)
+    for o in outs["a"]:
+        assert (o.float().cpu() - ref_a).abs().max().item() <= TOL
+    for o in outs["b"]:
+        assert (o.float().cpu() - ref_b).abs().max().item() <= TOL

@@ -7,6 +7,7 @@ verify (2-4 tokens) and prefill chunks (with and without a prefix), and
 optionally a forced range count.  Sizes keep the float32 oracle to well
 under a second per case.
 """
+import math
 import random
 
 import pytest
@@ -153,6 +154,36 @@ def test_random_mla_steps_other_head_counts(seed):
     plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
                                         step.seqlens_kv, heads, 1, 512, c["bs"],
                                         num_waves=c["waves"])
+    out = ops.paged_attention_mla(step.q_latent.to(DEV), step.cache.to(DEV), plan, step.scale)
+    torch.cuda.synchronize()
+    exp = mla_absorbed_attention(step.q_latent, step.cache, step.block_table, step.cu_seqlens_q,
+                                 step.seqlens_kv, step.scale, 512)
+    err = (out.float().cpu() - exp).abs().max().item()
+    print(f"max-abs err {err:.3e}", flush=True)
+    assert err <= TOL
+
+
+def draw_mla_large(seed):
+    r = random.Random(seed)
+    B = r.randint(32, 128)
+    lqs = [1 if r.random() < 0.9 else r.randint(2, 4) for _ in range(B)]
+    lks = [lq + int(math.exp(r.uniform(0, math.log(8192)))) for lq in lqs]
+    return dict(bs=r.choice([16, 64, 128]), lqs=lqs, lks=lks,
+                waves=r.choice([0, 0, 256, 512, 1024, 300]))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_large_mla_batches_match_the_oracle(seed):
+    """Batches of 32-128 requests (contexts log-uniform up to 8K, a few
+    verify rows) at several range counts: the balanced-plan path at the
+    sizes the benchmark runs."""
+    from oracle.paged_attn import mla_absorbed_attention
+    c = draw_mla_large(6000 + seed)
+    print(f"case {seed}: B {len(c['lqs'])} bs {c['bs']} waves {c['waves']}", flush=True)
+    step = workloads.make_mla_step(lqs=c["lqs"], lks=c["lks"], block_size=c["bs"], seed=seed)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, step.q_latent.shape[1], 1, 512,
+                                        c["bs"], num_waves=c["waves"])
     out = ops.paged_attention_mla(step.q_latent.to(DEV), step.cache.to(DEV), plan, step.scale)
     torch.cuda.synchronize()
     exp = mla_absorbed_attention(step.q_latent, step.cache, step.block_table, step.cu_seqlens_q,

@@ -83,7 +83,32 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(PackArgs a) {
   }
 }
 
+// Token splice: target[pairs[i].row] = *pairs[i].source for every pair, one
+// thread per pair.  Sources are addresses of int64 token ids inside the
+// caller's sampled-token tensors, so rows of any number of tensors move in
+// one launch.  Rows outside the target are skipped.
+__global__ __launch_bounds__(256) void splice_tokens_kernel(const int64_t* __restrict__ pairs,
+                                                            int32_t count, int64_t* __restrict__ target,
+                                                            int64_t target_len) {
+  const int32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  const int64_t* src = reinterpret_cast<const int64_t*>(pairs[2 * i]);
+  const int64_t row = pairs[2 * i + 1];
+  if (src != nullptr && row >= 0 && row < target_len) target[row] = *src;
+}
+
 }  // namespace
+
+extern "C" int aia_splice_tokens(const int64_t* pairs, int32_t count, int64_t* target,
+                                 int64_t target_len, void* stream) {
+  using namespace aia;
+  if (count < 0 || target_len < 0) return fail(AIA_ERR_INVALID, "aia_splice_tokens: bad sizes");
+  if (count == 0) return AIA_OK;
+  if (!pairs || !target) return fail(AIA_ERR_INVALID, "aia_splice_tokens: null pointer argument");
+  splice_tokens_kernel<<<(count + 255) / 256, 256, 0, (hipStream_t)stream>>>(pairs, count, target,
+                                                                           target_len);
+  return check_hip(hipGetLastError(), "aia_splice_tokens launch");
+}
 
 extern "C" int aia_pack_rows(const int64_t* token_update_index, const int64_t* token_update_value,
                              int32_t num_token_updates, const int64_t* block_update_index,

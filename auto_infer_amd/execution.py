@@ -49,3 +49,44 @@ class BatchPlan:
 
     def get_request(self, request_id: str) -> RequestView:
         return self.requests[request_id]
+
+
+@dataclass(frozen=True)
+class DeviceTokenRef:
+    """One row of a retained sampled-token tensor (reference
+    auto_infer/engine/execution.py:60-65): ``owner.tokens[row]``."""
+    owner: "DeviceTokenBatch"
+    row: int
+
+
+@dataclass(frozen=True)
+class DeviceTokenBatch:
+    """A step's sampled tokens, kept on the device, with the request order
+    they were sampled in (reference execution.py:68-100).  The splices in
+    ``auto_infer_amd.packing`` read ``tokens`` (int64, 1-D) and
+    ``ref.row`` only, so the reference's own objects work unchanged."""
+    tokens: object
+    order: tuple
+    row_by_request: Mapping[str, int]
+
+    @classmethod
+    def from_output(cls, tokens, order):
+        order = tuple(order)
+        if tokens.ndim != 1 or tokens.shape[0] != len(order):
+            raise ValueError("sampled tokens and request order must have equal length")
+        return cls.from_rows(tokens, order, range(len(order)))
+
+    @classmethod
+    def from_rows(cls, tokens, order, rows):
+        order, rows = tuple(order), tuple(rows)
+        if tokens.ndim != 1 or len(rows) != len(order):
+            raise ValueError("sampled rows and request order must have equal length")
+        if any(r < 0 or r >= tokens.shape[0] for r in rows):
+            raise ValueError("sampled token row is out of bounds")
+        by_rid = dict(zip(order, rows))
+        if len(by_rid) != len(order):
+            raise ValueError("sampled request order contains duplicate IDs")
+        return cls(tokens, order, MappingProxyType(by_rid))
+
+    def refs(self):
+        return {rid: DeviceTokenRef(self, row) for rid, row in self.row_by_request.items()}

@@ -14,7 +14,32 @@ import torch
 from auto_infer_amd import ops
 
 
-class DecodeGraph:
+class _GearGraph:
+    """Capture / stage / replay shared by the GQA and latent gears."""
+
+    def _body(self):
+        raise NotImplementedError
+
+    def capture(self):
+        """Capture after one staged step (the buffers hold valid metadata)."""
+        with torch.cuda.stream(self.stream):
+            self._body()                       # warm-up outside the graph
+            torch.cuda.synchronize()
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph, stream=self.stream):
+                self._body()
+        return self
+
+    def stage(self, plan, scheduled=None):
+        with torch.cuda.stream(self.stream):
+            return self.stager.stage(plan, scheduled)
+
+    def replay(self):
+        with torch.cuda.stream(self.stream):
+            self.graph.replay()
+
+
+class DecodeGraph(_GearGraph):
     """One decode gear of GQA layers captured in a HIP graph.
 
     ``stager``: a ``packing.DecodeInputStager`` or ``SpecDecodeInputStager``
@@ -30,7 +55,6 @@ class DecodeGraph:
         self.stager = stager
         self.caches = caches
         dev = stager.block_table.device
-        gear, width = stager.block_table.shape
         T = stager.slots.shape[0]
         L = len(caches)
         self.q = torch.zeros(L, T, num_q_heads, head_dim, dtype=torch.bfloat16, device=dev)
@@ -52,20 +76,43 @@ class DecodeGraph:
                                     out=self.out[layer], key_new=self.k_new[layer],
                                     value_new=self.v_new[layer])
 
-    def capture(self):
-        """Capture after one staged step (the buffers hold valid metadata)."""
-        with torch.cuda.stream(self.stream):
-            self._body()                       # warm-up outside the graph
-            torch.cuda.synchronize()
-            self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph, stream=self.stream):
-                self._body()
-        return self
 
-    def stage(self, plan, scheduled=None):
-        with torch.cuda.stream(self.stream):
-            return self.stager.stage(plan, scheduled)
+class LatentDecodeGraph(_GearGraph):
+    """One decode (or MTP verify) gear of absorbed-MLA layers in a HIP graph
+    -- the latent-cache counterpart of the reference's GraphMlaBackend
+    (auto_infer/layers/attention/mla.py:258-366), whose graph replays the
+    latent write and the 576-wide attention per layer.
 
-    def replay(self):
+    ``caches``: per layer the latent cache (NB, bs, 1, 576), or the
+    (latent, latent) pair ``MlaHipBackend.alloc_kv_caches`` returns.
+    ``q``: (L, T, H, 576) latent queries, ``latent_new``: (L, T, 1, 576) this
+    step's latent rows, both filled by the caller before each replay;
+    ``out``: (L, T, H, 512) latent attention outputs.  Per layer the graph
+    writes the new rows at the stager's slots, then attends; the planner
+    runs once per replay on the stager's device metadata.
+    """
+
+    def __init__(self, stager, caches, *, num_heads, scale=192 ** -0.5, stream=None):
+        self.stager = stager
+        self.caches = [c[0] if isinstance(c, (tuple, list)) else c for c in caches]
+        dev = stager.block_table.device
+        T = stager.slots.shape[0]
+        L = len(self.caches)
+        width = ops.MLA_LATENT + ops.MLA_ROPE
+        self.q = torch.zeros(L, T, num_heads, width, dtype=torch.bfloat16, device=dev)
+        self.latent_new = torch.zeros(L, T, 1, width, dtype=torch.bfloat16, device=dev)
+        self.out = torch.zeros(L, T, num_heads, ops.MLA_LATENT, dtype=torch.bfloat16, device=dev)
+        self.scale = scale
+        self.stream = stream or torch.cuda.Stream(device=dev)
+        block_size = self.caches[0].shape[1]
         with torch.cuda.stream(self.stream):
-            self.graph.replay()
+            self.plan = ops.AttentionPlan(stager.block_table, stager._cu, stager._kv, T,
+                                          num_heads, 1, ops.MLA_LATENT, block_size)
+        self.graph = None
+
+    def _body(self):
+        self.plan.replan()
+        for layer, latent in enumerate(self.caches):
+            ops.write_kv(self.latent_new[layer], None, latent, None, self.stager.slots)
+            ops.paged_attention_mla(self.q[layer], latent, self.plan, self.scale,
+                                    out=self.out[layer])

@@ -15,9 +15,11 @@ the sample rows.
 The classes keep the reference's names, constructor arguments, outputs and
 error messages (``DecodeInputStager``, ``SpecDecodeInputStager``,
 ``PrefillInputStager`` and ``DeviceBatchPacker.build`` for ``_build``).
-Their ``copied_block_rows`` / ``copied_block_elements`` counters count what
-this design uploads (block ids appended to the device table), not host
-staging rows.
+Their ``copied_block_rows`` / ``copied_block_elements`` counters keep the
+reference's meaning (worker/staging.py:30-48: gear block-table rows whose
+contents changed since the last stage, times the row width); what this
+design actually uploads (new block ids only) is counted by the shared
+``DeviceRequestTable.uploaded_block_rows`` / ``uploaded_block_elements``.
 """
 from dataclasses import dataclass
 
@@ -436,6 +438,92 @@ class DeviceBatchPacker:
         return ctx, sample_idx, decode_splice
 
 
+# ------------------------------------------------------- device token splice
+
+@dataclass(frozen=True)
+class PreparedTokenSplice:
+    """A splice planned by ``prepare_splice`` (reference
+    decode_input_stager.py:27-31): either one aligned owner (``fast_owner``,
+    its first ``fast_count`` tokens) or ``count`` (source address, row)
+    pairs already on the device in ``pairs``.  ``groups`` holds the owning
+    batches, which keeps their token tensors alive until the splice runs."""
+    groups: tuple
+    fast_owner: object = None
+    fast_count: int = 0
+    pairs: torch.Tensor = None
+    count: int = 0
+
+
+def _token_address(tokens, row):
+    if tokens.dtype != torch.int64 or tokens.dim() != 1 or not tokens.is_cuda:
+        raise ValueError("sampled tokens must be a 1-D int64 GPU tensor")
+    if not 0 <= row < tokens.shape[0]:
+        raise ValueError("sampled token row is out of bounds")
+    return tokens.data_ptr() + row * tokens.stride(0) * 8
+
+
+class _PairUploader:
+    """(source address, target row) pairs -> a persistent device buffer,
+    through pinned memory.  The host buffer is rewritten only after the copy
+    that last read it has finished."""
+
+    def __init__(self, device, cap):
+        self.device = torch.device(device)
+        self._cap = 0
+        self._grow(max(int(cap), 16))
+        self._event = None
+
+    def _grow(self, cap):
+        self._host = torch.empty(cap, 2, dtype=torch.int64, pin_memory=True)
+        self._dev = torch.empty(cap, 2, dtype=torch.int64, device=self.device)
+        self._cap = cap
+
+    def upload(self, pairs):
+        n = len(pairs)
+        if self._event is not None:
+            self._event.synchronize()
+        if n > self._cap:
+            self._grow(2 * n)
+        self._host.numpy()[:n] = pairs
+        dev = self._dev[:n]
+        dev.copy_(self._host[:n], non_blocking=True)
+        self._event = torch.cuda.Event()
+        self._event.record(torch.cuda.current_stream(self.device))
+        return dev
+
+
+_default_pairs = {}
+
+
+def splice_device_tokens(target, target_rows, request_order, refs, *, uploader=None):
+    """``target[target_rows[i]] = refs[request_order[i]].owner.tokens[row]``
+    for every request that has a ref, in one kernel launch whatever the
+    number of owning tensors (reference worker/staging.py:51-70 issues an
+    index_select + index_copy_ per owner).  ``target``: 1-D int64 on the
+    GPU."""
+    _check_device_tensor(target, "target", torch.int64)
+    if target.dim() != 1 or not target.is_contiguous():
+        raise ValueError("target must be a contiguous 1-D tensor")
+    pairs, owners = [], []
+    for row, rid in zip(target_rows, request_order):
+        ref = refs.get(rid)
+        if ref is None:
+            continue
+        pairs.append((_token_address(ref.owner.tokens, ref.row), int(row)))
+        owners.append(ref.owner)
+    if not pairs:
+        return
+    if uploader is None:
+        uploader = _default_pairs.get(target.device)
+        if uploader is None:
+            uploader = _default_pairs[target.device] = _PairUploader(target.device, 64)
+    dev = uploader.upload(pairs)
+    _native.call("aia_splice_tokens", _ptr(dev), len(pairs), _ptr(target), target.numel(),
+                 _stream(target.device))
+    for o in owners:          # the kernel reads them on this stream
+        o.tokens.record_stream(torch.cuda.current_stream(target.device))
+
+
 # ---------------------------------------------------------------- stagers
 
 @dataclass(frozen=True)
@@ -460,23 +548,54 @@ def _contig(t, name, dtype):
         raise ValueError(f"{name} must be contiguous")
 
 
+def _row_key(ids):
+    """The contents of a zero-padded block-table row, as a comparable key
+    (trailing zeros dropped: [5] and [5, 0] fill a row identically)."""
+    ids = tuple(ids)
+    n = len(ids)
+    while n and ids[n - 1] == 0:
+        n -= 1
+    return ids[:n]
+
+
+class _BlockRowLedger:
+    """The reference's dirty-row accounting of a gear block table
+    (worker/staging.py:20-48, used by decode_input_stager.py:115-119,
+    :246-250, :365-369 and prefill_input_stager.py:151-155): a row counts as
+    copied when its contents differ from what the last copy left, every row
+    the first time (the shadow starts at INT32_MIN); elements = rows x row
+    width.  Rows from ``active`` on are neither compared nor recorded.
+    Only keys are kept: the kernel writes the device rows either way."""
+
+    def __init__(self, rows, width):
+        self._shadow = [None] * rows
+        self._width = width
+
+    def account(self, keys, active=None):
+        n = len(keys) if active is None else min(active, len(keys))
+        copied = 0
+        for r in range(n):
+            if keys[r] != self._shadow[r]:
+                self._shadow[r] = keys[r]
+                copied += 1
+        return copied, copied * self._width
+
+
 class _GearStager:
-    def __init__(self, device, table, rows):
+    def __init__(self, device, table, rows, width):
         self.table = table or DeviceRequestTable(device)
         self._uploader = _Uploader(device)
         self._cu = torch.zeros(rows + 1, dtype=torch.int32, device=device)
         self._kv = torch.zeros(rows, dtype=torch.int32, device=device)
         self._last = torch.zeros(rows, dtype=torch.int64, device=device)
+        self._ledger = _BlockRowLedger(rows, width)
         self.copied_block_rows = 0
         self.copied_block_elements = 0
 
-    def _count(self, before):
-        rows, elems = before
-        self.copied_block_rows += self.table.uploaded_block_rows - rows
-        self.copied_block_elements += self.table.uploaded_block_elements - elems
-
-    def _mark(self):
-        return self.table.uploaded_block_rows, self.table.uploaded_block_elements
+    def _count(self, keys, active=None):
+        rows, elems = self._ledger.account(keys, active)
+        self.copied_block_rows += rows
+        self.copied_block_elements += elems
 
 
 class DecodeInputStager(_GearStager):
@@ -500,16 +619,16 @@ class DecodeInputStager(_GearStager):
         self.scratch0 = scratch0
         self.gear = tid.shape[0]
         self.max_blocks = block_table.shape[1]
-        super().__init__(tid.device, table, self.gear)
+        super().__init__(tid.device, table, self.gear, self.max_blocks)
+        self._splice_pairs = _PairUploader(tid.device, self.gear)
 
     def stage(self, plan, scheduled=None):
         scheduled = plan.scheduled if scheduled is None else scheduled
         if len(scheduled) > self.gear:
             raise ValueError(f"decode batch {len(scheduled)} exceeds gear {self.gear}")
-        mark = self._mark()
         upd = self.table.begin_step()
         live = {item.request_id for item in scheduled}
-        kv, order = [], []
+        kv, order, keys = [], [], []
         for row, item in enumerate(scheduled):
             rid = item.request_id
             req = plan.get_request(rid)
@@ -522,9 +641,11 @@ class DecodeInputStager(_GearStager):
             upd.row(slot, pos, 1, len(blocks), 0, row, 0, -1)
             kv.append(pos + 1)
             order.append(rid)
+            keys.append(_row_key(blocks))
         for row in range(len(scheduled), self.gear):
             upd.row(-1, 0, 1, 1, self.scratch0 + row, row, 1, -1)
             kv.append(1)
+            keys.append(_row_key((self.scratch0 + row,)))
         _launch(self.table, self._uploader, upd, block_size=self.block_size,
                 bt_width=self.max_blocks, token_ids=self.tid, positions=self.positions,
                 slot_mapping=self.slots, block_table=self.block_table, cu=self._cu,
@@ -532,9 +653,44 @@ class DecodeInputStager(_GearStager):
         if self.active_token_mask is not None:
             self.active_token_mask[:len(scheduled)].fill_(True)
             self.active_token_mask[len(scheduled):].fill_(False)
-        self._count(mark)
+        self._count(keys)
         return StagedDecodeInput(self.tid, self.positions, self.slots, self.block_table, kv,
                                  order, self._cu, self._kv)
+
+    # -- device token splice (decode_input_stager.py:125-170) -------------
+    def prepare_splice(self, refs, request_order):
+        """Plan the move of retained sampled tokens into ``tid`` rows: row i
+        takes ``refs[request_order[i]]`` when present.  One owner whose rows
+        0..n-1 line up with rows 0..n-1 becomes a plain copy; anything else
+        becomes (source address, row) pairs uploaded now, for one splice
+        launch in ``apply_splice``."""
+        owners, dst, src = [], [], []
+        for i, rid in enumerate(request_order):
+            ref = refs.get(rid)
+            if ref is None:
+                continue
+            if all(o is not ref.owner for o in owners):
+                owners.append(ref.owner)
+            dst.append(i)
+            src.append(ref)
+        if len(owners) == 1 and dst == list(range(len(dst))) and \
+                [r.row for r in src] == dst:
+            return PreparedTokenSplice((), owners[0], len(dst))
+        pairs = [(_token_address(r.owner.tokens, r.row), d) for r, d in zip(src, dst)]
+        buf = self._splice_pairs.upload(pairs) if pairs else None
+        return PreparedTokenSplice(tuple(owners), None, 0, buf, len(pairs))
+
+    def apply_splice(self, prepared):
+        if prepared.fast_owner is not None:
+            n = prepared.fast_count
+            self.tid[:n].copy_(prepared.fast_owner.tokens[:n])
+            return
+        if prepared.count:
+            _native.call("aia_splice_tokens", _ptr(prepared.pairs), prepared.count,
+                         _ptr(self.tid), self.tid.numel(), _stream(self.tid.device))
+
+    def splice(self, refs, request_order):
+        self.apply_splice(self.prepare_splice(refs, request_order))
 
 
 class SpecDecodeInputStager(_GearStager):
@@ -565,7 +721,7 @@ class SpecDecodeInputStager(_GearStager):
             raise ValueError("spec decode token buffer must match the configured query width")
         if active_mask is not None and tuple(active_mask.shape) != (self.gear,):
             raise ValueError("spec active mask must have one row per request")
-        super().__init__(tid.device, table, self.gear)
+        super().__init__(tid.device, table, self.gear, self.max_blocks)
         self._draft_host = torch.zeros(tuple(drafts.shape), dtype=torch.int64,
                                        pin_memory=tid.is_cuda)
         self._draft_event = None
@@ -574,11 +730,10 @@ class SpecDecodeInputStager(_GearStager):
         scheduled = plan.scheduled if scheduled is None else scheduled
         if len(scheduled) > self.gear:
             raise ValueError(f"spec decode batch {len(scheduled)} exceeds gear {self.gear}")
-        mark = self._mark()
         upd = self.table.begin_step()
         live = {item.request_id for item in scheduled}
         w = self.query_width
-        kv, order = [], []
+        kv, order, keys = [], [], []
         if self._draft_event is not None:
             self._draft_event.synchronize()
         dh = self._draft_host.numpy()
@@ -597,9 +752,11 @@ class SpecDecodeInputStager(_GearStager):
             dh[row] = req.spec_draft
             kv.append(pos + w)
             order.append(rid)
+            keys.append(_row_key(blocks))
         for row in range(len(scheduled), self.gear):
             upd.row(-1, 0, w, 1, self.scratch0 + row, row * w, 1, -1)
             kv.append(w)
+            keys.append(_row_key((self.scratch0 + row,)))
         _launch(self.table, self._uploader, upd, block_size=self.block_size,
                 bt_width=self.max_blocks, token_ids=self.tid, positions=self.positions,
                 slot_mapping=self.slots, block_table=self.block_table, cu=self._cu,
@@ -614,7 +771,7 @@ class SpecDecodeInputStager(_GearStager):
         if self.active_token_mask is not None:
             self.active_token_mask[:len(scheduled) * w].fill_(True)
             self.active_token_mask[len(scheduled) * w:].fill_(False)
-        self._count(mark)
+        self._count(keys)
         return StagedDecodeInput(self.tid, self.positions, self.slots, self.block_table, kv,
                                  order, self._cu, self._kv)
 
@@ -668,7 +825,8 @@ class PrefillInputStager(_GearStager):
         self.query_gear = token_ids.shape[0]
         self.sequence_gear = sample_rows.shape[0]
         self.max_blocks = block_table.shape[1]
-        super().__init__(token_ids.device, table, block_table.shape[0])
+        super().__init__(token_ids.device, table, block_table.shape[0], self.max_blocks)
+        self._splice_pairs = _PairUploader(token_ids.device, self.query_gear)
 
     def stage(self, plan):
         scheduled = plan.scheduled
@@ -680,10 +838,10 @@ class PrefillInputStager(_GearStager):
                 f"exceeds prefill gear ({self.query_gear}, {self.sequence_gear})")
         if not scheduled:
             raise ValueError("prefill staging requires at least one sequence")
-        mark = self._mark()
         upd = self.table.begin_step()
         live = {item.request_id for item in scheduled}
         cu, kv, sample_order, splice_order, splice_rows = [], [], [], [], []
+        keys = []
         q = 0
         for item in scheduled:
             rid = item.request_id
@@ -703,10 +861,12 @@ class PrefillInputStager(_GearStager):
             kv.append(start + n)
             splice_order.append(rid)
             splice_rows.append(q - 1)
+            keys.append(_row_key(blocks))
         padding = self.query_gear - real
         if padding:
             nblk = (padding + self.block_size - 1) // self.block_size
             upd.row(-1, 0, padding, nblk, self.scratch0, q, 1, -1)
+            keys.append(_row_key(range(self.scratch0, self.scratch0 + nblk)))
             cu.append(self.query_gear)
             kv.append(padding)
         rows = nseq + int(bool(padding))
@@ -724,8 +884,108 @@ class PrefillInputStager(_GearStager):
         if self.active_token_mask is not None:
             self.active_token_mask[:real].fill_(True)
             self.active_token_mask[real:].fill_(False)
-        self._count(mark)
+        self._count(keys, active=rows)
         return StagedPrefillInput(
             self.token_ids, self.positions, self.slots, self.block_table[:rows],
             self.sample_rows, cu, kv, sample_order, splice_order, splice_rows,
             self.query_gear, real, nseq, self._cu[:rows + 1], self._kv[:rows])
+
+    def splice(self, refs, request_order, target_rows):
+        """Retained sampled tokens into ``token_ids`` rows (reference
+        prefill_input_stager.py:164-166)."""
+        splice_device_tokens(self.token_ids, target_rows, request_order, refs,
+                             uploader=self._splice_pairs)
+
+
+@dataclass(frozen=True)
+class StagedContinuationInput:
+    kv_lengths: list
+
+
+class ContinuationInputStager:
+    """Recurrent MTP continuation gear (reference decode_input_stager.py:
+    178-251): for draft step s, live row position = num_computed_tokens +
+    accepted + s, its slot, kv length position + 1, and the request's block
+    row; padding rows use scratch block scratch0 + row with position s, slot
+    block * bs + s and kv length s + 1.  ``positions`` / ``slots`` are
+    (gear,) for one step or (steps, gear) for ``stage_all``.  All steps'
+    rows are packed by one kernel from the device request table."""
+
+    def __init__(self, *, positions, slots, block_table, block_size, scratch0, table=None):
+        _contig(positions, "positions", torch.int64)
+        _contig(slots, "slots", torch.int32)
+        _contig(block_table, "block_table", torch.int32)
+        self.positions, self.slots, self.block_table = positions, slots, block_table
+        self.block_size = block_size
+        self.scratch0 = scratch0
+        self.gear, self.max_blocks = block_table.shape
+        self._batched_steps = positions.dim() == 2
+        self.steps = positions.shape[0] if self._batched_steps else 1
+        if slots.shape != positions.shape:
+            raise ValueError("continuation positions and slots must match")
+        if positions.shape[-1] != self.gear:
+            raise ValueError("continuation positions must have one column per gear row")
+        dev = positions.device
+        self.table = table or DeviceRequestTable(dev)
+        self._uploader = _Uploader(dev)
+        n = self.steps * self.gear
+        # outputs the continuation does not use (token ids, per-step block
+        # rows, query offsets) land in private buffers
+        self._tid = torch.zeros(n, dtype=torch.int64, device=dev)
+        self._bt_all = torch.zeros(n, self.max_blocks, dtype=torch.int32, device=dev)
+        self._cu = torch.zeros(n + 1, dtype=torch.int32, device=dev)
+        self._kv = torch.zeros(n, dtype=torch.int32, device=dev)
+        self._last = torch.zeros(n, dtype=torch.int64, device=dev)
+        self._ledger = _BlockRowLedger(self.gear, self.max_blocks)
+        self.copied_block_rows = 0
+        self.copied_block_elements = 0
+
+    def stage(self, plan, scheduled, accepted, step):
+        if self._batched_steps:
+            raise ValueError("use stage_all for a multi-step continuation gear")
+        return StagedContinuationInput(self._stage_all(plan, scheduled, accepted, (step,))[0])
+
+    def stage_all(self, plan, scheduled, accepted):
+        return self._stage_all(plan, scheduled, accepted, range(1, self.steps + 1))
+
+    def _stage_all(self, plan, scheduled, accepted, steps):
+        if len(scheduled) > self.gear or len(accepted) != len(scheduled):
+            raise ValueError("continuation metadata does not match graph gear")
+        steps = list(steps)
+        upd = self.table.begin_step()
+        live = {item.request_id for item in scheduled}
+        bs, g = self.block_size, self.gear
+        slots, keys = [], []
+        for item, acc in zip(scheduled, accepted):
+            rid = item.request_id
+            req = plan.get_request(rid)
+            blocks = plan.block_tables[rid]
+            if len(blocks) > self.max_blocks:
+                raise ValueError(f"request {rid} has {len(blocks)} blocks > {self.max_blocks}")
+            _check_blocks(rid, blocks, req.num_computed_tokens + acc + max(steps) + 1, bs)
+            # blocks only: the continuation reads no token ids
+            slots.append(self.table.sync(upd, rid, req, blocks, 0, live))
+            keys.append(_row_key(blocks))
+        for row in range(len(scheduled), g):
+            keys.append(_row_key((self.scratch0 + row,)))
+        kv_by_step = []
+        for si, step in enumerate(steps):
+            kv = []
+            for row, (item, acc) in enumerate(zip(scheduled, accepted)):
+                req = plan.get_request(item.request_id)
+                pos = req.num_computed_tokens + acc + step
+                upd.row(slots[row], pos, 1, len(plan.block_tables[item.request_id]), 0,
+                        si * g + row, 1, -1)
+                kv.append(pos + 1)
+            for row in range(len(scheduled), g):
+                upd.row(-1, step, 1, 1, self.scratch0 + row, si * g + row, 1, -1)
+                kv.append(step + 1)
+            kv_by_step.append(kv)
+        _launch(self.table, self._uploader, upd, block_size=bs, bt_width=self.max_blocks,
+                token_ids=self._tid, positions=self.positions, slot_mapping=self.slots,
+                block_table=self._bt_all, cu=self._cu, kv=self._kv, last_rows=self._last)
+        self.block_table.copy_(self._bt_all[:g])
+        rows, elems = self._ledger.account(keys)
+        self.copied_block_rows += rows
+        self.copied_block_elements += elems
+        return kv_by_step

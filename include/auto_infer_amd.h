@@ -181,6 +181,18 @@ int aia_pack_rows(const int64_t* token_update_index, const int64_t* token_update
                   int32_t* seqlens_kv, int64_t* last_rows, int64_t* sample_rows,
                   int32_t sample_count, int32_t sample_cap, void* stream);
 
+/* Device token splice, one launch.  Replaces splice_device_tokens
+ * (reference auto_infer/worker/staging.py:51-70) and the stager's
+ * prepare_splice / apply_splice pair (worker/decode_input_stager.py:125-170),
+ * which move last step's sampled tokens (still on the device) into this
+ * step's token-id buffer with one index_select + index_copy_ per owning
+ * tensor: target[pairs[i][1]] = *(const int64_t*)pairs[i][0] for i < count.
+ * pairs: device int64 [count][2] = {address of the source token id (an
+ * element of any int64 device tensor), target row}; rows outside
+ * [0, target_len) are skipped. */
+int aia_splice_tokens(const int64_t* pairs, int32_t count, int64_t* target, int64_t target_len,
+                      void* stream);
+
 /* Fused pre-attention, in place over a packed qkv projection (T rows of
  * (Hq + 2 Hkv) x 128 bf16 values, token stride qkv_token_stride): per-head
  * RMSNorm of the Q and K heads with the given weights (both or neither;

@@ -28,7 +28,8 @@ SIGNATURES = {
     "aia_last_error": [],
     "aia_kv_write": [c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32,
                      c_i64, c_vp],
-    "aia_attn_workspace_bytes": [c_i32, c_i32, c_i32, c_i32, c_i32, ctypes.POINTER(c_i64)],
+    "aia_attn_workspace_bytes": [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                 ctypes.POINTER(c_i64)],
     "aia_attn_plan": [c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                       c_vp, c_i64, c_vp],
     "aia_paged_attention_gqa": [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp,

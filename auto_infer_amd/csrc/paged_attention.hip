@@ -2110,12 +2110,13 @@ int check_heads(const char* fn, int32_t hq, int32_t hkv) {
 }  // namespace
 
 extern "C" int aia_attn_workspace_bytes(int32_t batch, int32_t num_tokens, int32_t num_q_heads,
-                                        int32_t num_kv_heads, int32_t head_dim_v, int64_t* bytes) {
+                                        int32_t num_kv_heads, int32_t head_dim_v,
+                                        int32_t num_waves, int64_t* bytes) {
   if (int rc = check_heads("aia_attn_workspace_bytes", num_q_heads, num_kv_heads)) return rc;
   if (batch < 0 || num_tokens < 0 || head_dim_v <= 0 || !bytes)
     return aia::fail(AIA_ERR_INVALID, "aia_attn_workspace_bytes: bad arguments");
   const Geometry g = geometry(num_q_heads, num_kv_heads, batch, num_tokens, head_dim_v);
-  *bytes = layout(batch, num_tokens, g, head_dim_v, kMaxWaves).total;
+  *bytes = layout(batch, num_tokens, g, head_dim_v, resolve_waves(num_waves, g, head_dim_v)).total;
   return AIA_OK;
 }
 

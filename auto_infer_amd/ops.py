@@ -252,10 +252,10 @@ def write_kv(key, value, key_cache, value_cache, slot_mapping):
 
 # ---------------------------------------------------------------- attention
 
-def workspace_bytes(batch, num_tokens, num_q_heads, num_kv_heads, head_dim_v):
+def workspace_bytes(batch, num_tokens, num_q_heads, num_kv_heads, head_dim_v, num_waves=0):
     out = ctypes.c_int64(0)
     _native.call("aia_attn_workspace_bytes", batch, num_tokens, num_q_heads, num_kv_heads,
-                 head_dim_v, ctypes.byref(out))
+                 head_dim_v, num_waves, ctypes.byref(out))
     return out.value
 
 
@@ -292,7 +292,8 @@ class AttentionPlan:
         self.head_dim_v = head_dim_v
         self.num_waves = num_waves
         self.block_size = int(block_size)
-        nbytes = workspace_bytes(batch, self.num_tokens, num_q_heads, num_kv_heads, head_dim_v)
+        nbytes = workspace_bytes(batch, self.num_tokens, num_q_heads, num_kv_heads, head_dim_v,
+                                 num_waves)
         if workspace is None:
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=block_table.device)
         _check_device_tensor(workspace, "workspace", torch.uint8)

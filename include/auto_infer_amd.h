@@ -51,11 +51,12 @@ int aia_kv_write(const void* key, int64_t key_token_stride,
                  int64_t num_slots, void* stream);
 
 /* Bytes of workspace the attention planner/kernels need for a step of at
- * most `batch` requests and `num_tokens` query rows.  No reference
- * counterpart (the vendor op hides its workspace). */
+ * most `batch` requests and `num_tokens` query rows, planned with
+ * `num_waves` key ranges (0 = the default, as in aia_attn_plan).  No
+ * reference counterpart (the vendor op hides its workspace). */
 int aia_attn_workspace_bytes(int32_t batch, int32_t num_tokens,
                              int32_t num_q_heads, int32_t num_kv_heads,
-                             int32_t head_dim_v, int64_t* bytes);
+                             int32_t head_dim_v, int32_t num_waves, int64_t* bytes);
 
 /* Split-K work plan for one step: reads the device copies of
  * cu_seqlens_q (batch + 1 entries, leading 0 -- the reference keeps the

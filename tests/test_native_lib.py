@@ -35,7 +35,7 @@ def test_version_and_error_reporting_without_gpu():
     lib = _native.load()
     assert lib.aia_version() >= 100
     # argument validation happens before any device call
-    rc = lib.aia_attn_workspace_bytes(4, 4, 3, 2, 128, ctypes.byref(ctypes.c_int64()))
+    rc = lib.aia_attn_workspace_bytes(4, 4, 3, 2, 128, 0, ctypes.byref(ctypes.c_int64()))
     assert rc == _native.AIA_ERR_INVALID
     assert "multiple" in _native.last_error()
     with pytest.raises(ValueError, match="multiple"):
@@ -44,8 +44,13 @@ def test_version_and_error_reporting_without_gpu():
 
 def test_workspace_query():
     out = ctypes.c_int64(0)
-    _native.call("aia_attn_workspace_bytes", 16, 16, 16, 8, 128, ctypes.byref(out))
+    _native.call("aia_attn_workspace_bytes", 16, 16, 16, 8, 128, 0, ctypes.byref(out))
     assert out.value > 0
+    # sized for the range count asked for: the default 256 ranges of a
+    # config-1 step need tens of MB, the maximum range count far more
+    big = ctypes.c_int64(0)
+    _native.call("aia_attn_workspace_bytes", 16, 16, 16, 8, 128, 16384, ctypes.byref(big))
+    assert out.value < 64 << 20 < big.value
 
 
 def test_argument_validation_of_the_fused_kernels_without_gpu():

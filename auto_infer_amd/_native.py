@@ -36,6 +36,10 @@ SIGNATURES = {
                                 c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32,
                                 c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i32, c_i32,
                                 c_vp, c_i64, c_vp],
+    "aia_paged_attention_gqa_noalloc": [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_i32, c_vp,
+                                        c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                        c_f32, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64,
+                                        c_i32, c_i32, c_vp],
     "aia_paged_attention_mla": [c_vp, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp, c_vp, c_i32,
                                 c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp,
                                 c_i64, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp],

@@ -128,6 +128,33 @@ int aia_paged_attention_gqa(const void* query, int64_t q_token_stride,
                             int32_t flags, void* workspace, int64_t workspace_bytes,
                             void* stream);
 
+/* Allocation-free paged GQA attention: aia_attn_plan + aia_paged_attention_gqa
+ * in one call, with the plan and the split partials in a static 256 MiB
+ * device array of the library (one per GPU, held until the process ends)
+ * instead of a caller workspace.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation).  Same arguments as
+ * aia_paged_attention_gqa without the workspace; steps whose plan needs
+ * more than 256 MiB (aia_attn_workspace_bytes; every BASELINE config needs
+ * at most 132 MiB) fail with AIA_ERR_CAPACITY.
+ * All calls on one GPU share the array: calls that overlap on one GPU (two
+ * streams, two host threads) race and must be ordered by the caller. */
+int aia_paged_attention_gqa_noalloc(const void* query, int64_t q_token_stride,
+                                    int64_t q_head_stride,
+                                    const void* key_cache, const void* value_cache,
+                                    const int32_t* block_table, int32_t block_table_stride,
+                                    const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
+                                    int32_t batch, int32_t num_tokens,
+                                    int32_t num_q_heads, int32_t num_kv_heads,
+                                    int32_t head_dim, int32_t block_size,
+                                    int32_t num_blocks, float scale,
+                                    void* out, int64_t out_token_stride,
+                                    int64_t out_head_stride,
+                                    const void* key_new, const void* value_new,
+                                    int64_t new_key_token_stride,
+                                    int64_t new_value_token_stride, int32_t num_waves,
+                                    int32_t flags, void* stream);
+
 /* Absorbed-MLA paged attention over a planned step.  Replaces the FIA call of
  * mla_paged_absorbed (reference auto_infer/layers/attention/mla.py:76-122,
  * from MlaFIABackend.attention :221-241): one KV head holding the 576-wide

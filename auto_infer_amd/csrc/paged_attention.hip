@@ -184,25 +184,31 @@ int32_t resolve_waves(int32_t w, const Geometry& g, int32_t dv) {
 
 // ---------------------------------------------------------------- planner
 
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves (VALU
+// only, no LDS crossbar round trips): shifts by 1, 2, 4, 8 within each row of
+// 16 lanes (lanes shifted in from outside the row read 0), then row 0's last
+// lane is added to row 1 and row 2's to row 3 (row_bcast:15), and lane 31's
+// total to rows 2 and 3 (row_bcast:31).  Rows a broadcast does not write keep
+// the 0 passed as the old value.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);   // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);   // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);   // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);   // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return x;
+}
+
 // Exclusive scan of one value per thread across the 1024-thread block;
 // returns the exclusive prefix and writes the block total to *total.
 __device__ int block_exclusive_scan(int v, int* wave_sums, int* total) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    int y = __shfl_up(x, d);
-    if (lane >= d) x += y;
-  }
+  const int x = wave_incl_scan(v);
   if (lane == 63) wave_sums[wid] = x;
   __syncthreads();
   if (wid == 0) {
-    int s = lane < kPlanThreads / 64 ? wave_sums[lane] : 0;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      int y = __shfl_up(s, d);
-      if (lane >= d) s += y;
-    }
+    const int s = wave_incl_scan(lane < kPlanThreads / 64 ? wave_sums[lane] : 0);
     if (lane < kPlanThreads / 64) wave_sums[lane] = s;  // inclusive
   }
   __syncthreads();
@@ -215,21 +221,12 @@ __device__ int block_exclusive_scan(int v, int* wave_sums, int* total) {
 // The same for two values at once (one pass of barriers instead of two).
 __device__ int2 block_exclusive_scan2(int2 v, int2* wave_sums2, int2* total) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  int2 x = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y0 = __shfl_up(x.x, d), y1 = __shfl_up(x.y, d);
-    if (lane >= d) { x.x += y0; x.y += y1; }
-  }
+  const int2 x = make_int2(wave_incl_scan(v.x), wave_incl_scan(v.y));
   if (lane == 63) wave_sums2[wid] = x;
   __syncthreads();
   if (wid == 0) {
-    int2 s = lane < kPlanThreads / 64 ? wave_sums2[lane] : make_int2(0, 0);
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int y0 = __shfl_up(s.x, d), y1 = __shfl_up(s.y, d);
-      if (lane >= d) { s.x += y0; s.y += y1; }
-    }
+    const int2 w = lane < kPlanThreads / 64 ? wave_sums2[lane] : make_int2(0, 0);
+    const int2 s = make_int2(wave_incl_scan(w.x), wave_incl_scan(w.y));
     if (lane < kPlanThreads / 64) wave_sums2[lane] = s;  // inclusive
   }
   __syncthreads();

@@ -56,6 +56,9 @@ def parse():
     p.add_argument("--only", default=None,
                    help="run one other_configs entry and print it (for profiling): configs[1] "
                         ".. configs[4], pre_attention, mtp_compaction")
+    p.add_argument("--hbm-sweep", action="store_true",
+                   help="only time plain device copies and row sums of 36 MB to 1.1 GB (the "
+                        "practical HBM rate at the decode configs' sizes) and print them")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 256 MiB device copy 10 times (the reference "
                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -70,6 +73,50 @@ def copy_calibration():
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes": n, "launches": 10}))
+
+
+def hbm_sweep():
+    """Practical HBM rates at a given size: a device copy (read + write of
+    half the bytes each) and a row sum (read only) over rotating buffers
+    that together exceed the 256 MB Infinity Cache, timed like the bench
+    (HIP graph of 8 launches, HIP events, median of 5)."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    L = 8
+
+    def timeit(fn, reps=50):
+        with torch.cuda.stream(stream):
+            fn()
+            stream.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                fn()
+            g.replay()
+            torch.cuda.synchronize()
+            res = []
+            for _ in range(5):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(reps):
+                    g.replay()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                res.append(e0.elapsed_time(e1) * 1e3 / reps / L)
+        return sorted(res)[2]
+
+    out = []
+    for mb in (36, 72, 144, 288, 1152):
+        n = mb * (1 << 20) // 2
+        srcs = [torch.randn(n, device=dev).bfloat16() for _ in range(L)]
+        dsts = [torch.empty(n // 2, device=dev, dtype=torch.bfloat16) for _ in range(L)]
+        us_copy = timeit(lambda: [dsts[i].copy_(srcs[i][:n // 2]) for i in range(L)])
+        us_sum = timeit(lambda: [torch.sum(srcs[i].view(-1, 4096), dim=1) for i in range(L)])
+        by = mb * (1 << 20)
+        out.append({"MiB_moved": mb, "copy_us": round(us_copy, 2),
+                    "copy_TBps": round(by / us_copy / 1e6, 2), "rowsum_read_us": round(us_sum, 2),
+                    "rowsum_TBps": round(by / us_sum / 1e6, 2)})
+        del srcs, dsts
+    print(json.dumps({"hbm_sweep": out}))
 
 
 def cpu_model():
@@ -133,17 +180,53 @@ def cpu_baseline(step, budget_s):
         pack_build(bplan, bs)
         pt.append(time.perf_counter() - t0)
     pt.sort()
+    # the same numpy packing at BASELINE config 5's batch (256 decode
+    # requests, block tables from the fragmented 80 GB pool): where the GPU
+    # packer's per-step cost is compared at scale
+    bplan5 = stress_batch_plan()
+    pt5 = []
+    for _ in range(30):
+        t0 = time.perf_counter()
+        pack_build(bplan5, 128)
+        pt5.append(time.perf_counter() - t0)
+    pt5.sort()
     return {
         "value": round(len(step.seqlens_kv) / med, 1),
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
         "sample": f"{len(times)} steps of config 1 (packing of the step's plan + one layer: "
-                  f"KV write + paged attention, "
+                  f"KV write + paged attention; packing alone also timed on config 5's "
+                  f"256-request plan), "
                   f"median {med * 1e3:.1f} ms), torch {torch.__version__} CPU eager, "
                   f"{threads} threads of {os.cpu_count()} ({cpu_model()})",
         "packing_us_per_step": round(pt[len(pt) // 2] * 1e6, 1),
+        "packing_us_per_step_config5": round(pt5[len(pt5) // 2] * 1e6, 1),
     }
+
+
+def stress_batch_plan():
+    """BASELINE config 5's decode BatchPlan: 256 requests, lognormal contexts,
+    block tables drawn from the allocator after its 10k-operation trace over
+    the 80 GB pool.  Returns (plan, tables, contexts) when asked via
+    ``parts=True``."""
+    return _stress_parts()[0]
+
+
+def _stress_parts():
+    from auto_infer_amd import workloads
+    from auto_infer_amd.execution import BatchPlan, RequestView, ScheduledRequest
+    bs, hkv, d = 128, 8, 128
+    nb = int(80e9) // (bs * hkv * d * 2 * 2)
+    lks = workloads.config5_contexts(seed=0)
+    tables, _ = workloads.fragmented_block_tables(lks, num_blocks=nb, block_size=bs, ops=10000,
+                                                  seed=0)
+    views = {f"r{i}": RequestView(f"r{i}", tuple(range(lk)), lk - 1, 1, 1, ())
+             for i, lk in enumerate(lks)}
+    plan = BatchPlan.make([ScheduledRequest(f"r{i}", 1, False, tuple(t))
+                           for i, t in enumerate(tables)], views,
+                          {f"r{i}": t for i, t in enumerate(tables)})
+    return plan, tables, lks, nb
 
 
 def _time_graph(fn, stream, reps, inner):
@@ -391,18 +474,10 @@ def other_configs(stream, only=None):
         note("configs[4] stress: 80 GB pool")
         # config 5: 80 GB fragmented pool, GPU packing of the 256-request plan
         bs, hkv, d, hq = 128, 8, 128, 64
-        nb = int(80e9) // (bs * hkv * d * 2 * 2)
-        lks = workloads.config5_contexts(seed=0)
-        tables, _ = workloads.fragmented_block_tables(lks, num_blocks=nb, block_size=bs,
-                                                      ops=10000, seed=0)
+        bplan, tables, lks, nb = _stress_parts()
         step = workloads.make_gqa_step(lqs=[1] * 256, lks=lks, num_q_heads=hq, num_kv_heads=hkv,
                                        block_size=bs, num_blocks=nb, seed=2, device=dev,
                                        tables=tables)
-        views = {f"r{i}": RequestView(f"r{i}", tuple(range(lk)), lk - 1, 1, 1, ())
-                 for i, lk in enumerate(lks)}
-        bplan = BatchPlan.make([ScheduledRequest(f"r{i}", 1, False, tuple(t))
-                                for i, t in enumerate(tables)], views,
-                               {f"r{i}": t for i, t in enumerate(tables)})
         packer = packing.DeviceBatchPacker(bs, dev)
         with torch.cuda.stream(stream):
             packer.build(bplan)                     # first step uploads every block
@@ -437,6 +512,9 @@ def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.hbm_sweep:
+        hbm_sweep()
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "

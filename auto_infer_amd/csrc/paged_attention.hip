@@ -19,6 +19,7 @@
 //   gqa_merge     log-sum-exp merge of the partials of each split segment.
 #include <math.h>
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -54,7 +55,31 @@ constexpr int kMaxGroupWaves = 8;  // kv heads (waves) per work-group
 // (block_size x Hkv x D) cache slots.
 struct Geometry {
   int32_t hkv, group, hb, nhb, qb, nw, nkvg, rb, qs, pf;
+  int32_t ncu;   // compute units of the current device (MLA range count and dealing)
 };
+
+// Compute units of the current device, queried once per device (256, the
+// MI355X's count, when no device is visible, e.g. a size query on a host
+// without a GPU).
+constexpr int kMaxCuDevices = 64;
+std::atomic<int> g_device_cus[kMaxCuDevices];
+int32_t device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxCuDevices) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  int n = g_device_cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0) {
+      (void)hipGetLastError();
+      return 256;
+    }
+    g_device_cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 
 // Prefill routing: a GQA request whose query rows (query tokens x group
 // heads) fill at least one prefill work item is planned for the prefill
@@ -119,6 +144,7 @@ Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_
   g.rb = ((!g.pf && (dv == kHeadDim || dv == 64)) || mla_rb2) && tokens > (int64_t)batch * g.qb
              ? 2 : 1;
   g.qs = g.qb * g.rb;                                   // query tokens per segment
+  g.ncu = device_cus();
   return g;
 }
 
@@ -173,11 +199,11 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
 }
 
 // Number of key ranges (= work-groups).  Default: about kDefaultWaves waves
-// in flight for GQA (one per kv head of a group), 768 four-wave groups (three
-// per CU) for the 576-wide MLA latent.
-constexpr int kDefaultMlaRanges = 768;
+// in flight for GQA (one per kv head of a group), three four-wave groups per
+// CU (768 on the MI355X) for the 576-wide MLA latent.
+constexpr int kMlaRangesPerCu = 3;
 int32_t resolve_waves(int32_t w, const Geometry& g, int32_t dv) {
-  if (w <= 0) w = dv == 512 ? kDefaultMlaRanges : (kDefaultWaves + g.nw - 1) / g.nw;
+  if (w <= 0) w = dv == 512 ? kMlaRangesPerCu * g.ncu : (kDefaultWaves + g.nw - 1) / g.nw;
   if (w > kMaxWaves) w = kMaxWaves;
   return w;
 }
@@ -257,9 +283,8 @@ constexpr int kPadBelow = AIA_PAD_BELOW;  // pad segments when ranges are shorte
 // Padded MLA plans: a request's tiles are split over its ranges evenly
 // (sizes floor / ceil of nt / k, never crossing requests) and the ranges are
 // dealt to work-group slots by size in a snake order over the CUs' slots
-// (slots w, w + kMlaCUs, w + 2 kMlaCUs share a CU: work-groups go out one
-// per CU per round), so every CU gets about the mean number of tiles.
-constexpr int kMlaCUs = 256;
+// (slots w, w + ncu, w + 2 ncu share a CU: work-groups go out one per CU per
+// round), so every CU gets about the mean number of tiles.
 #ifndef AIA_MLA_BALANCE
 #define AIA_MLA_BALANCE 1
 #endif
@@ -512,7 +537,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
 
   // 3) partial slots: a segment split over k ranges owns k consecutive slots
   const int pb0 = nseg + 1;     // LDS: segments' first partial slots (balanced MLA plans)
-  const bool bal = AIA_MLA_BALANCE && pad && dv == 512 && waves % kMlaCUs == 0 &&
+  const int ncu = g.ncu;
+  const bool bal = AIA_MLA_BALANCE && pad && dv == 512 && ncu > 0 && waves % ncu == 0 &&
                    2 * (nseg + 1) + 32 <= kPlanLds;
   carry = 0;
   int mcarry = 0;
@@ -640,14 +666,14 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       int s_, j_, k_, a_, b_;
       locate(r, s_, j_, k_, a_, b_);
       const int rank = atomicAdd(&offs[min(b_ - a_, 15)], 1);
-      const int round = rank / kMlaCUs, pos = rank - round * kMlaCUs;
-      const int slot = round * kMlaCUs + ((round & 1) ? kMlaCUs - 1 - pos : pos);
+      const int round = rank / ncu, pos = rank - round * ncu;
+      const int slot = round * ncu + ((round & 1) ? ncu - 1 - pos : pos);
       const int tb = seg[(int64_t)s_ * 8 + 5];
       write_rec(wave_rec + (int64_t)slot * kRecInts, s_, s_, tb + a_, tb + b_, j_, k_);
     }
     for (int w = tid; w < waves; w += kPlanThreads) {   // slots no rank maps to
-      const int round = w / kMlaCUs, cu = w - round * kMlaCUs;
-      const int rank = round * kMlaCUs + ((round & 1) ? kMlaCUs - 1 - cu : cu);
+      const int round = w / ncu, cu = w - round * ncu;
+      const int rank = round * ncu + ((round & 1) ? ncu - 1 - cu : cu);
       if (rank >= nr) {
         int* out = wave_rec + (int64_t)w * kRecInts;
         out[0] = -1; out[1] = 0; out[2] = 0; out[3] = tpw;

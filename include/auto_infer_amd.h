@@ -70,7 +70,8 @@ int aia_attn_workspace_bytes(int32_t batch, int32_t num_tokens,
  * into key chunks when they are too few to fill the chip).  The plan depends
  * only on step metadata, so one plan serves every layer of the step.
  * num_waves: number of key ranges (work-groups); 0 picks the default (about
- * 2048 waves in flight for GQA, 768 four-wave groups for MLA).
+ * 2048 waves in flight for GQA; three four-wave groups per compute unit of the
+ * current device for MLA, 768 on the MI355X).
  * Status: the int32 at byte offset 32 of the workspace is 0 after a good
  * plan and -1 when the query lengths ask for more work than a step of
  * num_tokens rows can hold (cu_seqlens_q not ending at num_tokens, or

@@ -46,6 +46,8 @@ SIGNATURES = {
     "aia_pack_rows": [c_vp, c_vp, c_i32, c_vp, c_vp, c_i32, c_vp, c_i64, c_vp, c_i64, c_vp,
                       c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                       c_i32, c_i32, c_vp],
+    "aia_pack_rows_inline": [c_vp, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_i64, c_i32, c_i32,
+                             c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp],
     "aia_splice_tokens": [c_vp, c_i32, c_vp, c_i64, c_vp],
     "aia_qk_norm_rope": [c_vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_i64,
                          c_vp, c_vp, c_f32, c_vp],

@@ -440,7 +440,58 @@ PyObject* upload_pack(PyObject*, PyObject* args) {
   return PyLong_FromLong(rc);
 }
 
+// aia_pack_rows_inline, reached through the address the Python side reads.
+typedef int (*PackInlineFn)(const void*, int32_t, int32_t, int32_t, int64_t*, int64_t, int32_t*,
+                            int64_t, int32_t, int32_t, int64_t*, int64_t*, int32_t*, int32_t*,
+                            int32_t*, int32_t*, int64_t*, int64_t*, int32_t, int32_t, void*);
+constexpr long long kInlineBytes = 3072;   // AIA_PACK_INLINE_BYTES
+
+// A small step's pack without a staging copy: the updates and rows are
+// staged into a local buffer in the layout aia_pack_rows_inline takes (token
+// indices, token values, block indices, block values padded to a word, rows)
+// and handed to it, which passes them in the kernel launch.  Returns its
+// status; raises ValueError (from staging) on malformed updates.
+PyObject* pack_inline(PyObject*, PyObject* args) {
+  PyObject* upd;
+  unsigned long long fn, stream, token_pool, block_pool;
+  unsigned long long token_ids, positions, slot_mapping, block_table, cu, kv, last_rows, sample_rows;
+  long long tw, bw, row_ints, tp_stride, bp_stride;
+  int block_size, bt_width, sample_count, sample_cap;
+  if (!PyArg_ParseTuple(args, "OKKLLLKLKLiiKKKKKKKKii", &upd, &fn, &stream, &tw, &bw, &row_ints,
+                        &token_pool, &tp_stride, &block_pool, &bp_stride, &block_size, &bt_width,
+                        &token_ids, &positions, &slot_mapping, &block_table, &cu, &kv, &last_rows,
+                        &sample_rows, &sample_count, &sample_cap))
+    return nullptr;
+  Ref ti(get_list(upd, "tok_idx")), bi(get_list(upd, "blk_idx")), rows(get_list(upd, "rows"));
+  if (!ti || !bi || !rows) return nullptr;
+  const long long nt = PyList_GET_SIZE(ti.get()), nb = PyList_GET_SIZE(bi.get());
+  const long long nr = PyList_GET_SIZE(rows.get());
+  const long long o[5] = {0, 8 * nt, 16 * nt, 16 * nt + 8 * nb, 16 * nt + 8 * nb + 8 * ((nb + 1) / 2)};
+  const long long total = o[4] + nr * row_ints * 4;
+  if (total > kInlineBytes) {
+    PyErr_SetString(PyExc_ValueError, "step too large for the inline pack");
+    return nullptr;
+  }
+  alignas(16) char h[kInlineBytes];
+  Py_ssize_t snt, snb, snr;
+  if (!stage_impl(upd, h, tw, bw, o, row_ints, &snt, &snb, &snr)) return nullptr;
+  const int rc = reinterpret_cast<PackInlineFn>(fn)(
+      h, (int32_t)snt, (int32_t)snb, (int32_t)snr, reinterpret_cast<int64_t*>(token_pool), tp_stride,
+      reinterpret_cast<int32_t*>(block_pool), bp_stride, block_size, bt_width,
+      reinterpret_cast<int64_t*>(token_ids), reinterpret_cast<int64_t*>(positions),
+      reinterpret_cast<int32_t*>(slot_mapping), reinterpret_cast<int32_t*>(block_table),
+      reinterpret_cast<int32_t*>(cu), reinterpret_cast<int32_t*>(kv),
+      reinterpret_cast<int64_t*>(last_rows), reinterpret_cast<int64_t*>(sample_rows), sample_count,
+      sample_cap, reinterpret_cast<void*>(stream));
+  return PyLong_FromLong(rc);
+}
+
 PyMethodDef methods[] = {
+    {"pack_inline", pack_inline, METH_VARARGS,
+     "pack_inline(updates, pack_rows_inline_fn, stream, token_width, block_width, row_ints, "
+     "token_pool, token_pool_stride, block_pool, block_pool_stride, block_size, bt_width, "
+     "token_ids, positions, slot_mapping, block_table, cu, kv, last_rows, sample_rows, "
+     "sample_count, sample_cap) -> status"},
     {"upload_pack", upload_pack, METH_VARARGS,
      "upload_pack(updates, pack_rows_fn, host, dev, wait_event, record_event, stream, token_width, "
      "block_width, total, 5 offsets, row_ints, token_pool, token_pool_stride, block_pool, "

@@ -13,6 +13,8 @@
 //                 the compacted sample rows.
 // Synthetic rows (the stagers' scratch padding) take consecutive blocks
 // block_base, block_base + 1, ... and token id 0.
+#include <string.h>
+
 #include "common.h"
 
 namespace {
@@ -48,15 +50,8 @@ __global__ __launch_bounds__(256) void pack_updates_kernel(
   }
 }
 
-__global__ __launch_bounds__(256) void pack_rows_kernel(PackArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  // zero the unused tail of the sample rows (prefill stager contract)
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x + a.sample_count; i < a.sample_cap;
-       i += gridDim.x * blockDim.x)
-    a.sample_rows[i] = 0;
-  if (r >= a.num_rows) return;
-  const int32_t* d = a.rows + (int64_t)r * 8;
+// One row's outputs, by one wave.
+__device__ __forceinline__ void pack_one_row(const PackArgs& a, int r, const int32_t* d, int lane) {
   const int src = d[0], start = d[1], n = d[2], nblocks = d[3], base = d[4], q_off = d[5];
   const int zero_tokens = d[6], sample_slot = d[7];
   const int32_t* prow = src >= 0 ? a.block_pool + (int64_t)src * a.block_stride : nullptr;
@@ -81,6 +76,44 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(PackArgs a) {
     if (a.last_rows) a.last_rows[r] = q_off + n - 1;
     if (sample_slot >= 0 && sample_slot < a.sample_cap) a.sample_rows[sample_slot] = q_off + n - 1;
   }
+}
+
+__global__ __launch_bounds__(256) void pack_rows_kernel(PackArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // zero the unused tail of the sample rows (prefill stager contract)
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x + a.sample_count; i < a.sample_cap;
+       i += gridDim.x * blockDim.x)
+    a.sample_rows[i] = 0;
+  if (r >= a.num_rows) return;
+  pack_one_row(a, r, a.rows + (int64_t)r * 8, lane);
+}
+
+// The whole step in one work-group, its updates and row descriptors carried
+// in the kernel arguments (the launch copies them; no staging copy): the
+// pool updates first, then, after a work-group barrier (one CU, so its
+// stores are visible to the whole group), one wave per row.
+struct InlineBlob {
+  int64_t w[AIA_PACK_INLINE_BYTES / 8];
+};
+
+__global__ __launch_bounds__(256) void pack_inline_kernel(PackArgs a, InlineBlob blob, int32_t nt,
+                                                          int32_t nb, int64_t* token_pool,
+                                                          int32_t* block_pool) {
+  const int64_t* tidx = blob.w;
+  const int64_t* tval = blob.w + nt;
+  const int64_t* bidx = blob.w + 2 * nt;
+  const int32_t* bval = reinterpret_cast<const int32_t*>(blob.w + 2 * nt + nb);
+  const int32_t* rows = reinterpret_cast<const int32_t*>(blob.w + 2 * nt + nb + (nb + 1) / 2);
+  for (int i = threadIdx.x; i < nt + nb; i += blockDim.x) {
+    if (i < nt) token_pool[tidx[i]] = tval[i];
+    else block_pool[bidx[i - nt]] = bval[i - nt];
+  }
+  for (int i = threadIdx.x + a.sample_count; i < a.sample_cap; i += blockDim.x) a.sample_rows[i] = 0;
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  for (int r = threadIdx.x >> 6; r < a.num_rows; r += blockDim.x >> 6)
+    pack_one_row(a, r, rows + (int64_t)r * 8, lane);
 }
 
 // Token splice: target[pairs[i].row] = *pairs[i].source for every pair, one
@@ -155,4 +188,46 @@ extern "C" int aia_pack_rows(const int64_t* token_update_index, const int64_t* t
   const int grid = num_rows > 0 ? (num_rows + 3) / 4 : 1;
   pack_rows_kernel<<<grid, 256, 0, s>>>(a);
   return check_hip(hipGetLastError(), "pack_rows launch");
+}
+
+extern "C" int aia_pack_rows_inline(const void* blob, int32_t num_token_updates,
+                                    int32_t num_block_updates, int32_t num_rows,
+                                    int64_t* token_pool, int64_t token_pool_stride,
+                                    int32_t* block_pool, int64_t block_pool_stride,
+                                    int32_t block_size, int32_t block_table_width,
+                                    int64_t* token_ids, int64_t* positions, int32_t* slot_mapping,
+                                    int32_t* block_table, int32_t* cu_seqlens_q,
+                                    int32_t* seqlens_kv, int64_t* last_rows, int64_t* sample_rows,
+                                    int32_t sample_count, int32_t sample_cap, void* stream) {
+  using namespace aia;
+  const int64_t nt = num_token_updates, nb = num_block_updates, nr = num_rows;
+  if (nt < 0 || nb < 0 || nr < 0 || block_size <= 0 || block_table_width < 0 || sample_count < 0 ||
+      sample_cap < sample_count)
+    return fail(AIA_ERR_INVALID, "aia_pack_rows_inline: bad sizes");
+  const int64_t words = 2 * nt + nb + (nb + 1) / 2 + 4 * nr;
+  if (words * 8 > AIA_PACK_INLINE_BYTES)
+    return fail(AIA_ERR_CAPACITY, "aia_pack_rows_inline: %lld bytes exceed the %d inline bytes",
+                (long long)(words * 8), AIA_PACK_INLINE_BYTES);
+  if (nr > 0 && (!positions || !slot_mapping || !token_ids || !cu_seqlens_q || !seqlens_kv ||
+                 (block_table_width > 0 && !block_table)))
+    return fail(AIA_ERR_INVALID, "aia_pack_rows_inline: null output");
+  if ((nt && !token_pool) || (nb && !block_pool) || (words && !blob))
+    return fail(AIA_ERR_INVALID, "aia_pack_rows_inline: updates without a pool");
+  if (sample_cap > 0 && !sample_rows)
+    return fail(AIA_ERR_INVALID, "aia_pack_rows_inline: null sample_rows");
+  if (words == 0 && sample_cap == 0) return AIA_OK;
+  InlineBlob b;
+  memcpy(b.w, blob, (size_t)words * 8);
+  PackArgs a;
+  a.rows = nullptr; a.num_rows = (int32_t)nr;
+  a.token_pool = token_pool; a.token_stride = token_pool_stride;
+  a.block_pool = block_pool; a.block_stride = block_pool_stride > 0 ? block_pool_stride : 1;
+  a.block_size = block_size; a.bt_width = block_table_width;
+  a.token_ids = token_ids; a.positions = positions; a.slot_mapping = slot_mapping;
+  a.block_table = block_table; a.cu_seqlens_q = cu_seqlens_q; a.seqlens_kv = seqlens_kv;
+  a.last_rows = last_rows; a.sample_rows = sample_rows;
+  a.sample_count = sample_count; a.sample_cap = sample_cap;
+  pack_inline_kernel<<<1, 256, 0, (hipStream_t)stream>>>(a, b, (int32_t)nt, (int32_t)nb, token_pool,
+                                                         block_pool);
+  return check_hip(hipGetLastError(), "aia_pack_rows_inline launch");
 }

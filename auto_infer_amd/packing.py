@@ -290,9 +290,34 @@ class PackedStep:
     last_rows: torch.Tensor        # (rows,) int64
 
 
+_INLINE_BYTES = 3072    # AIA_PACK_INLINE_BYTES
+
+
+def _inline_bytes(upd):
+    nt, nb, nr = len(upd.tok_idx), len(upd.blk_idx), len(upd.rows)
+    return 16 * nt + 8 * nb + 8 * ((nb + 1) // 2) + nr * _ROW_INTS * 4
+
+
 def _launch(table, uploader, upd, *, block_size, bt_width, token_ids, positions, slot_mapping,
             block_table, cu, kv, last_rows, sample_rows=None, sample_count=0, stream=None):
     cap = sample_rows.numel() if sample_rows is not None else 0
+    if (_hostpack is not None and uploader.device.type == "cuda"
+            and _inline_bytes(upd) <= _INLINE_BYTES):
+        # small step: updates and rows travel in the launch's arguments, no
+        # staging copy (aia_pack_rows_inline)
+        sp = (stream.cuda_stream if stream is not None
+              else _raw_stream(uploader.device_index) if _raw_stream is not None
+              else torch.cuda.current_stream(uploader.device).cuda_stream)
+        rc = _hostpack.pack_inline(
+            upd, _native.address("aia_pack_rows_inline"), sp, table.token_pool.shape[1],
+            table.block_pool.shape[1], _ROW_INTS, table.token_pool.data_ptr(),
+            table.token_pool.shape[1], table.block_pool.data_ptr(), table.block_pool.shape[1],
+            block_size, bt_width, token_ids.data_ptr(), positions.data_ptr(),
+            slot_mapping.data_ptr(), block_table.data_ptr(), cu.data_ptr(), kv.data_ptr(),
+            last_rows.data_ptr(), sample_rows.data_ptr() if sample_rows is not None else 0,
+            sample_count, cap)
+        _native.check(rc, "aia_pack_rows_inline")
+        return
     if _hostpack is not None and uploader.device.type == "cuda":
         # one native call: event wait, staging, copy, event record, pack launch
         sp = (stream.cuda_stream if stream is not None

@@ -210,6 +210,27 @@ int aia_pack_rows(const int64_t* token_update_index, const int64_t* token_update
                   int32_t* seqlens_kv, int64_t* last_rows, int64_t* sample_rows,
                   int32_t sample_count, int32_t sample_cap, void* stream);
 
+/* aia_pack_rows for small steps, with no staging copy: the updates and row
+ * descriptors come in `blob`, HOST memory that the call copies into the
+ * kernel launch's arguments, and one work-group scatters the updates and
+ * packs the rows.  blob layout (8-byte words): token_update_index [nt]
+ * int64, token_update_value [nt] int64, block_update_index [nb] int64,
+ * block_update_value [nb] int32 (padded to a whole word), rows [num_rows][8]
+ * int32; at most AIA_PACK_INLINE_BYTES bytes (AIA_ERR_CAPACITY otherwise).
+ * Other arguments and the outputs as in aia_pack_rows.  No reference
+ * counterpart beyond aia_pack_rows' (it is the same packing, launched without
+ * the host-to-device copy). */
+#define AIA_PACK_INLINE_BYTES 3072
+int aia_pack_rows_inline(const void* blob, int32_t num_token_updates,
+                         int32_t num_block_updates, int32_t num_rows,
+                         int64_t* token_pool, int64_t token_pool_stride,
+                         int32_t* block_pool, int64_t block_pool_stride,
+                         int32_t block_size, int32_t block_table_width,
+                         int64_t* token_ids, int64_t* positions, int32_t* slot_mapping,
+                         int32_t* block_table, int32_t* cu_seqlens_q, int32_t* seqlens_kv,
+                         int64_t* last_rows, int64_t* sample_rows, int32_t sample_count,
+                         int32_t sample_cap, void* stream);
+
 /* Device token splice, one launch.  Replaces splice_device_tokens
  * (reference auto_infer/worker/staging.py:51-70) and the stager's
  * prepare_splice / apply_splice pair (worker/decode_input_stager.py:125-170),

@@ -212,3 +212,20 @@ def test_prefill_stager_over_simulated_run():
         assert staged.kv_lengths == exp["kv_lengths"]
         n += 1
     assert n > 30
+
+
+@pytest.mark.parametrize("inline", [True, False])
+def test_build_inline_and_staged_uploads_agree(inline, monkeypatch):
+    """Small steps go out inline (aia_pack_rows_inline: updates and rows in
+    the launch's arguments), larger ones through the staging copy
+    (aia_pack_rows); a simulated run through either path matches the
+    oracle step by step."""
+    if not inline:
+        monkeypatch.setattr(packing, "_INLINE_BYTES", 0)
+    table = packing.DeviceRequestTable(DEV, max_slots=4, max_blocks=2, max_len=8)
+    packer = packing.DeviceBatchPacker(16, DEV, table=table)
+    n = 0
+    for plan in simulate(40, seed=7, block_size=16, draft_depth=1):
+        check_build(packer, plan, 16)
+        n += 1
+    assert n > 20

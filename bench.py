@@ -703,8 +703,9 @@ def main():
         "packing_us_per_step": round(pack_host_us + plan_us, 2),
         "packing": {"batch_plan_to_device_metadata_host_us": round(pack_host_us, 2),
                     "attention_planner_device_us": round(plan_us, 3),
-                    "note": "host median of DeviceBatchPacker.build (native row loop, upload "
-                            "staging, pack-kernel enqueue) + the planner launch once per step"},
+                    "note": "host median of DeviceBatchPacker.build (native row loop, then one "
+                            "inline pack launch; larger steps: staging copy + pack launch) + the "
+                            "planner launch once per step"},
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),

@@ -417,6 +417,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
 
   // 2) segment records and their key tiles
   int my_tb[kPlanRegChunks], my_nt[kPlanRegChunks];
+  int4 my_head[kPlanRegChunks];     // each own segment's record fields 0-3
   carry = 0;
   for (int base = 0, c = 0; base < nseg; base += kPlanThreads, ++c) {
     const int s = base + tid;
@@ -456,7 +457,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     }
 #pragma unroll
     for (int i = 0; i < kPlanRegChunks; ++i)
-      if (i == c) { my_tb[i] = carry + ex; my_nt[i] = ntiles; }
+      if (i == c) {
+        my_tb[i] = carry + ex; my_nt[i] = ntiles;
+        my_head[i] = make_int4(rec[0], rec[1], rec[2], rec[3]);
+      }
     carry += tot;
   }
   // Range length.  With few segments and short ranges each segment's tile
@@ -564,8 +568,13 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     if (s < nseg) {
       for (int i = 0; i < g.nw; ++i) counters[(int64_t)s * g.nw + i] = 0;
       if (np > 1) {
+        if (regs) {      // the segment's head, kept in registers since phase 2
 #pragma unroll
-        for (int i = 0; i < 4; ++i) r0[i] = seg[(int64_t)s * 8 + i];
+          for (int i = 0; i < kPlanRegChunks; ++i)
+            if (i == c) { r0[0] = my_head[i].x; r0[1] = my_head[i].y; r0[2] = my_head[i].z; r0[3] = my_head[i].w; }
+        } else {
+          for (int i = 0; i < 4; ++i) r0[i] = seg[(int64_t)s * 8 + i];
+        }
         const int nq = r0[3] & 0xff;
         const int nblk = (nq + g.qb - 1) / g.qb;
         rows = (nblk - 1) * kRows + min(kRows, (nq - (nblk - 1) * g.qb) * g.hb);
@@ -583,15 +592,11 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       const int seg_rows = kRows * g.rb;
       for (int i = 0; i < mcnt; ++i) {
         const int w = i / nsl, sl = i - w * nsl;
-        int* m = mrg + (int64_t)(mcarry + mex + i) * kMrgInts;
-        m[0] = r0[2];                                        // first query token
-        m[1] = r0[3] & 0xff;                                 // query tokens
-        m[2] = (r0[1] & 0xffff) * g.nw + w;                  // kv head
-        m[3] = (r0[1] >> 16) & 0x3fff;                       // head block
-        m[4] = ((carry + ex) * g.nw + w) * seg_rows;         // first partial row
-        m[5] = np;
-        m[6] = sl;
-        m[7] = rows;
+        // {first query token, query tokens, kv head, head block; first
+        // partial row, parts, slice, rows}, as two 16-byte stores
+        int4* m = reinterpret_cast<int4*>(mrg + (int64_t)(mcarry + mex + i) * kMrgInts);
+        m[0] = make_int4(r0[2], r0[3] & 0xff, (r0[1] & 0xffff) * g.nw + w, (r0[1] >> 16) & 0x3fff);
+        m[1] = make_int4(((carry + ex) * g.nw + w) * seg_rows, np, sl, rows);
       }
     }
     mcarry += mtot;
@@ -609,25 +614,26 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   __syncthreads();
 
   // 4) per-range record (see kRecInts)
+  // (records and segment records are 16-byte aligned: 16-byte stores and loads)
   auto write_rec = [&](int* out, int lo, int lo2, int t0, int t1, int j, int k) {
-    out[0] = lo; out[1] = t0; out[2] = t1; out[3] = tpw;
-    const int* r = seg + (int64_t)lo * 8;
-    int rr[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) rr[i] = r[i];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) out[4 + i] = rr[i];
-    const int b = rr[0], nq = rr[3] & 0xff, lim_base = rr[4];
+    int4* o4 = reinterpret_cast<int4*>(out);
+    const int4* r = reinterpret_cast<const int4*>(seg + (int64_t)lo * 8);
+    const int4 r0 = r[0], r1 = r[1];
+    o4[0] = make_int4(lo, t0, t1, tpw);
+    o4[1] = r0;
+    o4[2] = r1;
+    const int b = r0.x, nq = r0.w & 0xff, lim_base = r1.x;
     const int visible = max(0, lim_base + nq);
     const int nblk_vis = (visible + block_size - 1) / block_size;
-    const int blk_base = ((t0 - rr[5]) * kTile) / block_size;
-    out[12] = blk_base; out[13] = lo2; out[14] = j; out[15] = k;
+    const int blk_base = ((t0 - r1.y) * kTile) / block_size;
+    o4[3] = make_int4(blk_base, lo2, j, k);
     const int32_t* btrow = block_table + (int64_t)b * bt_stride;
     int bv[kRecBlocks];
 #pragma unroll
     for (int i = 0; i < kRecBlocks; ++i) bv[i] = blk_base + i < nblk_vis ? btrow[blk_base + i] : 0;
 #pragma unroll
-    for (int i = 0; i < kRecBlocks; ++i) out[16 + i] = bv[i];
+    for (int i = 0; i < kRecBlocks / 4; ++i)
+      o4[4 + i] = make_int4(bv[4 * i], bv[4 * i + 1], bv[4 * i + 2], bv[4 * i + 3]);
   };
   if (bal) {
     // ranges = the partial slots of the padded plan; range r is number

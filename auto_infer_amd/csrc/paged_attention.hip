@@ -451,9 +451,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     int tot;
     const int ex = block_exclusive_scan(ntiles, wave_sums, &tot);
     if (s < nseg) {
-      int* r = seg + (int64_t)s * 8;
-      r[0] = rec[0]; r[1] = rec[1]; r[2] = rec[2]; r[3] = rec[3]; r[4] = rec[4];
-      r[5] = carry + ex; r[6] = carry + ex + ntiles;
+      int4* r = reinterpret_cast<int4*>(seg + (int64_t)s * 8);   // field 7 follows in phase 3
+      r[0] = make_int4(rec[0], rec[1], rec[2], rec[3]);
+      r[1] = make_int4(rec[4], carry + ex, carry + ex + ntiles, 0);
     }
 #pragma unroll
     for (int i = 0; i < kPlanRegChunks; ++i)
@@ -516,8 +516,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       int tot;
       const int ex = block_exclusive_scan((nt + tpw - 1) / tpw * tpw, wave_sums, &tot);
       if (s < nseg) {
-        seg[(int64_t)s * 8 + 5] = carry + ex;
-        seg[(int64_t)s * 8 + 6] = carry + ex + nt;
+        *reinterpret_cast<int2*>(seg + (int64_t)s * 8 + 5) = make_int2(carry + ex, carry + ex + nt);
       }
 #pragma unroll
       for (int i = 0; i < kPlanRegChunks; ++i)
@@ -566,7 +565,12 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     int mcnt = 0, nwv = 0, nsl = 0, rows = 0;
     int r0[4] = {0, 0, 0, 0};
     if (s < nseg) {
-      for (int i = 0; i < g.nw; ++i) counters[(int64_t)s * g.nw + i] = 0;
+      if (g.nw % 4 == 0) {
+        for (int i = 0; i < g.nw; i += 4)
+          *reinterpret_cast<int4*>(counters + (int64_t)s * g.nw + i) = make_int4(0, 0, 0, 0);
+      } else {
+        for (int i = 0; i < g.nw; ++i) counters[(int64_t)s * g.nw + i] = 0;
+      }
       if (np > 1) {
         if (regs) {      // the segment's head, kept in registers since phase 2
 #pragma unroll
@@ -682,7 +686,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       const int rank = round * ncu + ((round & 1) ? ncu - 1 - cu : cu);
       if (rank >= nr) {
         int* out = wave_rec + (int64_t)w * kRecInts;
-        out[0] = -1; out[1] = 0; out[2] = 0; out[3] = tpw;
+        *reinterpret_cast<int4*>(out) = make_int4(-1, 0, 0, tpw);
       }
     }
     return;
@@ -691,7 +695,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int t0 = w * tpw;
     int* out = wave_rec + (int64_t)w * kRecInts;
     if (t0 >= total_tiles) {
-      out[0] = -1; out[1] = 0; out[2] = 0; out[3] = tpw;
+      *reinterpret_cast<int4*>(out) = make_int4(-1, 0, 0, tpw);
       continue;
     }
     const int t1 = min(total_tiles, t0 + tpw);

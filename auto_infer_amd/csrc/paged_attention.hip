@@ -1063,67 +1063,74 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
       old = __shfl(old, 0);
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       if (old == nparts - 1) {
-        // Merge, one row at a time: lane k holds part k's (m, l) (all parts
-        // requested at once), then every lane accumulates two output dims
-        // over the parts with all partial loads of a batch in flight.
-        for (int nr = 0; nr < nblk * kRows; ++nr) {
-          const int r2 = nr / kRows, n2 = nr - r2 * kRows;
-          const int t2 = n2 / a.hb, hh2 = n2 - t2 * a.hb;
-          const int qi2 = r2 * qb + t2;
-          if (t2 >= qb || qi2 >= nq) continue;
-          const int head2 = kvh * a.group + hbi * a.hb + hh2;
-          const int64_t row0 = ((int64_t)part_base * a.nw + wid) * seg_rows + nr;
-          const int64_t pstride = (int64_t)a.nw * seg_rows;   // rows between parts
-          float mx = -1e30f;
-          for (int k0 = 0; k0 < nparts; k0 += 64) {
-            const int k = k0 + lane;
-            float mk = -1e30f;
-            if (k < nparts)
-              mk = unpack_f2(__hip_atomic_load(reinterpret_cast<const uint64_t*>(
-                                                   a.part_ml + row0 + k * pstride),
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)).x;
-            mx = fmaxf(mx, mk);
-          }
+        // Merge.  This code runs once per split segment and head, cold in
+        // the instruction cache, so it is kept short.  Lane (p, c) folds
+        // parts p, p + 2, ... of output dims [4c, 4c + 4); lane k of a
+        // 64-part chunk holds part k's (m, l).  A row whose parts fit one
+        // 16-part batch costs one round trip: its (m, l) and partial loads
+        // are issued together.
+        const int64_t pstride = (int64_t)a.nw * seg_rows;   // rows between parts
+        const int64_t rbase = ((int64_t)part_base * a.nw + wid) * seg_rows;
+        const int c = lane & 31, p = lane >> 5;
+        for (int r2 = 0; r2 < nblk; ++r2)
+          for (int t2 = 0; t2 < qb && r2 * qb + t2 < nq; ++t2)
+            for (int hh2 = 0; hh2 < a.hb && hbi * a.hb + hh2 < a.group; ++hh2) {
+              const int64_t row0 = rbase + r2 * kRows + t2 * a.hb + hh2;
+              auto ml_at = [&](int k) {
+                return k < nparts ? unpack_f2(__hip_atomic_load(
+                                        reinterpret_cast<const uint64_t*>(a.part_ml + row0 + k * pstride),
+                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                                  : make_float2(-1e30f, 0.f);
+              };
+              float2 v[8][2];
+              auto fetch = [&](int kb) {
 #pragma unroll
-          for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
-          float acc0 = 0.f, acc1 = 0.f, ls = 0.f;
-          for (int k0 = 0; k0 < nparts; k0 += 64) {
-            const int k = k0 + lane;
-            float wk = 0.f, lk = 0.f;
-            if (k < nparts) {
-              const float2 ml = unpack_f2(__hip_atomic_load(
-                  reinterpret_cast<const uint64_t*>(a.part_ml + row0 + k * pstride),
-                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-              wk = __builtin_amdgcn_exp2f(ml.x - mx);
-              lk = ml.y * wk;
-            }
-            ls += lk;
-            const int kn = min(64, nparts - k0);
-            for (int j0 = 0; j0 < kn; j0 += 16) {
-              float2 v[16];
+                for (int i = 0; i < 8; ++i) {
+                  const int k = min(kb + p + 2 * i, nparts - 1);
+                  const uint64_t* src =
+                      reinterpret_cast<const uint64_t*>(a.part_o + (row0 + k * pstride) * D) + 2 * c;
+                  v[i][0] = unpack_f2(__hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+                  v[i][1] = unpack_f2(__hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+                }
+              };
+              const float2 ml0 = ml_at(lane);
+              fetch(0);
+              float mx = ml0.x;
+              for (int k0 = 64; k0 < nparts; k0 += 64) mx = fmaxf(mx, ml_at(k0 + lane).x);
 #pragma unroll
-              for (int j = 0; j < 16; ++j) {
-                const int kk = k0 + min(j0 + j, kn - 1);
-                v[j] = unpack_f2(__hip_atomic_load(
-                    reinterpret_cast<const uint64_t*>(a.part_o + (row0 + kk * pstride) * D) +
-                        lane,
-                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+              for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+              float acc[4] = {0.f, 0.f, 0.f, 0.f}, ls = 0.f;
+              for (int k0 = 0; k0 < nparts; k0 += 64) {
+                const float2 ml = k0 == 0 ? ml0 : ml_at(k0 + lane);
+                const float wk = k0 + lane < nparts ? __builtin_amdgcn_exp2f(ml.x - mx) : 0.f;
+                ls += ml.y * wk;
+                for (int kb = k0; kb < min(nparts, k0 + 64); kb += 16) {
+                  if (kb > 0) fetch(kb);
+#pragma unroll
+                  for (int i = 0; i < 8; ++i) {
+                    const int kl = kb - k0 + p + 2 * i;   // the part's lane in this chunk
+                    const float wi = kb + p + 2 * i < nparts ? __shfl(wk, kl & 63) : 0.f;
+                    acc[0] += v[i][0].x * wi;
+                    acc[1] += v[i][0].y * wi;
+                    acc[2] += v[i][1].x * wi;
+                    acc[3] += v[i][1].y * wi;
+                  }
+                }
               }
 #pragma unroll
-              for (int j = 0; j < 16; ++j) {
-                const float wj = j0 + j < kn ? __shfl(wk, j0 + j) : 0.f;
-                acc0 += v[j].x * wj;
-                acc1 += v[j].y * wj;
+              for (int d = 32; d >= 1; d >>= 1) ls += __shfl_xor(ls, d);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], 32);
+              const float inv = ls > 0.f ? 1.f / ls : 0.f;
+              if (p == 0) {
+                const int head2 = kvh * a.group + hbi * a.hb + hh2;
+                uint2 wv;
+                wv.x = aia::pack_bf16x2(acc[0] * inv, acc[1] * inv);
+                wv.y = aia::pack_bf16x2(acc[2] * inv, acc[3] * inv);
+                *reinterpret_cast<uint2*>(a.out + (int64_t)(qtok0 + r2 * qb + t2) * a.o_ts +
+                                          (int64_t)head2 * a.o_hs + 4 * c) = wv;
               }
             }
-          }
-#pragma unroll
-          for (int d = 32; d >= 1; d >>= 1) ls += __shfl_xor(ls, d);
-          const float inv = ls > 0.f ? 1.f / ls : 0.f;
-          *reinterpret_cast<uint32_t*>(a.out + (int64_t)(qtok0 + qi2) * a.o_ts +
-                                       (int64_t)head2 * a.o_hs + 2 * lane) =
-              aia::pack_bf16x2(acc0 * inv, acc1 * inv);
-        }
         if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     } else {

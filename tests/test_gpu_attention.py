@@ -407,3 +407,14 @@ def test_mixed_launch_with_fused_kv_write():
     err = (out.float().cpu() - oracle(step)).abs().max().item()
     print(f"max-abs err {err:.3e}", flush=True)
     assert err <= TOL
+
+
+
+@pytest.mark.parametrize("hq,hkv", [(40, 2), (24, 1)])
+def test_group_above_16_not_a_multiple_is_rejected(hq, hkv):
+    """Query groups above 16 split into 16-head blocks; a group that 16 does
+    not divide is refused before any launch."""
+    step = workloads.make_gqa_step(lqs=[1, 3], lks=[70, 9], num_q_heads=hq, num_kv_heads=hkv,
+                                   block_size=16, seed=1)
+    with pytest.raises(NotImplementedError, match="multiple of 16"):
+        run_gpu(step)

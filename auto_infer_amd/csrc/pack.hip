@@ -92,12 +92,13 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(PackArgs a) {
 // The whole step in one work-group, its updates and row descriptors carried
 // in the kernel arguments (the launch copies them; no staging copy): the
 // pool updates first, then, after a work-group barrier (one CU, so its
-// stores are visible to the whole group), one wave per row.
+// stores are visible to the whole group), one wave per row; 16 waves, so a
+// decode gear of up to 16 requests packs its rows in one pass.
 struct InlineBlob {
   int64_t w[AIA_PACK_INLINE_BYTES / 8];
 };
 
-__global__ __launch_bounds__(256) void pack_inline_kernel(PackArgs a, InlineBlob blob, int32_t nt,
+__global__ __launch_bounds__(1024) void pack_inline_kernel(PackArgs a, InlineBlob blob, int32_t nt,
                                                           int32_t nb, int64_t* token_pool,
                                                           int32_t* block_pool) {
   const int64_t* tidx = blob.w;
@@ -227,7 +228,7 @@ extern "C" int aia_pack_rows_inline(const void* blob, int32_t num_token_updates,
   a.block_table = block_table; a.cu_seqlens_q = cu_seqlens_q; a.seqlens_kv = seqlens_kv;
   a.last_rows = last_rows; a.sample_rows = sample_rows;
   a.sample_count = sample_count; a.sample_cap = sample_cap;
-  pack_inline_kernel<<<1, 256, 0, (hipStream_t)stream>>>(a, b, (int32_t)nt, (int32_t)nb, token_pool,
+  pack_inline_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(a, b, (int32_t)nt, (int32_t)nb, token_pool,
                                                          block_pool);
   return check_hip(hipGetLastError(), "aia_pack_rows_inline launch");
 }

@@ -39,7 +39,7 @@ constexpr int kVStride = 144;
 constexpr int kMaxBatch = 8192;   // planner keeps the request offsets in LDS
 constexpr int kDefaultWaves = 2048;
 constexpr int kMaxWaves = 16384;
-constexpr int kPlanThreads = 1024;
+constexpr int kPlanThreads = 512;
 // Per-range work record: {segment, first tile, end tile, tiles per range,
 // the segment's 8-int record, first logical block, last segment of the
 // range, 2 pad, the first 16 block ids of the range} -- everything a
@@ -226,7 +226,7 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
   return x;
 }
 
-// Exclusive scan of one value per thread across the 1024-thread block;
+// Exclusive scan of one value per thread across the planner work-group;
 // returns the exclusive prefix and writes the block total to *total.
 __device__ int block_exclusive_scan(int v, int* wave_sums, int* total) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -274,7 +274,7 @@ __device__ int2 block_exclusive_scan2(int2 v, int2* wave_sums2, int2* total) {
 // global round trip each (metadata in, block ids in) rather than one per
 // dependent lookup.
 constexpr int kPlanLds = 12288;          // ints of LDS scratch (48 KB)
-constexpr int kPlanRegChunks = 8;        // segments kept in registers: 8 x 1024
+constexpr int kPlanRegChunks = 2;        // segments kept in registers: 2 x 512
 #ifndef AIA_PAD_BELOW
 #define AIA_PAD_BELOW 16
 #endif

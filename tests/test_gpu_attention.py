@@ -418,3 +418,15 @@ def test_group_above_16_not_a_multiple_is_rejected(hq, hkv):
                                    block_size=16, seed=1)
     with pytest.raises(NotImplementedError, match="multiple of 16"):
         run_gpu(step)
+
+
+@pytest.mark.parametrize("waves", [0, 300])
+def test_more_segments_than_the_planner_keeps_in_registers(waves):
+    """1100 decode requests of one segment each: past the 1024 segments the
+    planner keeps in registers, it reads its segment records back from the
+    workspace instead."""
+    r = np.random.default_rng(5)
+    lks = r.integers(1, 200, size=1100).tolist()
+    step = workloads.make_gqa_step(lqs=[1] * 1100, lks=lks, num_q_heads=8, num_kv_heads=1,
+                                   block_size=16, seed=5)
+    check(step, waves)

@@ -180,3 +180,11 @@ def test_caller_outputs_are_checked():
     with pytest.raises(ValueError):
         ops.paged_attention_gqa(g.q.to(DEV), g.k_cache.to(DEV), g.v_cache.to(DEV), gp, g.scale,
                                 out=torch.empty(1, 8, 64, dtype=torch.bfloat16, device=DEV))
+
+
+def test_mla_more_segments_than_the_planner_keeps_in_registers():
+    """1100 requests of one segment each (past the planner's 1024 in
+    registers) through the size-dealt MLA plan."""
+    lks = torch.randint(1, 300, (1100,), generator=torch.Generator().manual_seed(9)).tolist()
+    step = workloads.make_mla_step(lqs=[1] * 1100, lks=lks, num_heads=16, block_size=64, seed=9)
+    check(step)

@@ -190,6 +190,7 @@ def cpu_baseline(step, budget_s):
         pack_build(bplan5, 128)
         pt5.append(time.perf_counter() - t0)
     pt5.sort()
+    up = upload_inclusive_packing(bplan, bs)
     return {
         "value": round(len(step.seqlens_kv) / med, 1),
         "unit": "tok/s",
@@ -202,7 +203,50 @@ def cpu_baseline(step, budget_s):
                   f"{threads} threads of {os.cpu_count()} ({cpu_model()})",
         "packing_us_per_step": round(pt[len(pt) // 2] * 1e6, 1),
         "packing_us_per_step_config5": round(pt5[len(pt5) // 2] * 1e6, 1),
+        "packing_with_upload_us_per_step": up,
+        "packing_note": "packing_us_per_step: the numpy build alone; packing_with_upload_us_per_step: "
+                        "the same build plus the reference's four copy_ calls from pinned staging "
+                        "into the device buffers (model_runner.py:170-174, blocking as there)",
     }
+
+
+def upload_inclusive_packing(bplan, bs, reps=200):
+    """The reference's whole _build on this machine: the host packing, then
+    one ``copy_`` per buffer from pinned staging into persistent device
+    buffers (model_runner.py:71-94 staging, :170-174 copies; ``copy_``
+    without non_blocking, so the host waits for each).  None without a GPU."""
+    if not torch.cuda.is_available():
+        return None
+    from oracle.pack import build as pack_build
+    d0 = pack_build(bplan, bs)
+    T, (B, W) = len(d0["token_ids"]), d0["block_table"].shape
+    dev = torch.device("cuda:0")
+    stage = [torch.empty(T, dtype=torch.int64).pin_memory(),
+             torch.empty(T, dtype=torch.int64).pin_memory(),
+             torch.empty(T, dtype=torch.int32).pin_memory(),
+             torch.empty((B, W), dtype=torch.int32).pin_memory()]
+    bufs = [torch.zeros(T, dtype=torch.int64, device=dev), torch.zeros(T, dtype=torch.int64, device=dev),
+            torch.zeros(T, dtype=torch.int32, device=dev), torch.zeros((B, W), dtype=torch.int32, device=dev)]
+    views = [t.numpy() for t in stage]
+    keys = ("token_ids", "positions", "slot_mapping", "block_table")
+
+    def one():
+        d = pack_build(bplan, bs)
+        for v, k in zip(views, keys):
+            v[...] = d[k]
+        for b, st in zip(bufs, stage):
+            b.copy_(st)
+
+    for _ in range(5):
+        one()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        one()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return round(ts[len(ts) // 2] * 1e6, 1)
 
 
 def stress_batch_plan():

@@ -299,7 +299,11 @@ def _inline_bytes(upd):
 
 
 def _launch(table, uploader, upd, *, block_size, bt_width, token_ids, positions, slot_mapping,
-            block_table, cu, kv, last_rows, sample_rows=None, sample_count=0, stream=None):
+            block_table, cu, kv, last_rows, sample_rows=None, sample_count=0, stream=None,
+            out_ptrs=None):
+    """Pack one step on the device.  ``out_ptrs`` may carry the output
+    tensors' device addresses (token_ids, positions, slot_mapping,
+    block_table, cu, kv, last_rows) when the caller keeps them."""
     cap = sample_rows.numel() if sample_rows is not None else 0
     if (_hostpack is not None and uploader.device.type == "cuda"
             and _inline_bytes(upd) <= _INLINE_BYTES):
@@ -308,13 +312,15 @@ def _launch(table, uploader, upd, *, block_size, bt_width, token_ids, positions,
         sp = (stream.cuda_stream if stream is not None
               else _raw_stream(uploader.device_index) if _raw_stream is not None
               else torch.cuda.current_stream(uploader.device).cuda_stream)
+        o = out_ptrs or (token_ids.data_ptr(), positions.data_ptr(), slot_mapping.data_ptr(),
+                         block_table.data_ptr(), cu.data_ptr(), kv.data_ptr(),
+                         last_rows.data_ptr())
+        tp, bp = table.token_pool, table.block_pool
+        tw, bw = tp.shape[1], bp.shape[1]
         rc = _hostpack.pack_inline(
-            upd, _native.address("aia_pack_rows_inline"), sp, table.token_pool.shape[1],
-            table.block_pool.shape[1], _ROW_INTS, table.token_pool.data_ptr(),
-            table.token_pool.shape[1], table.block_pool.data_ptr(), table.block_pool.shape[1],
-            block_size, bt_width, token_ids.data_ptr(), positions.data_ptr(),
-            slot_mapping.data_ptr(), block_table.data_ptr(), cu.data_ptr(), kv.data_ptr(),
-            last_rows.data_ptr(), sample_rows.data_ptr() if sample_rows is not None else 0,
+            upd, _native.address("aia_pack_rows_inline"), sp, tw, bw, _ROW_INTS,
+            tp.data_ptr(), tw, bp.data_ptr(), bw, block_size, bt_width, o[0], o[1], o[2], o[3],
+            o[4], o[5], o[6], sample_rows.data_ptr() if sample_rows is not None else 0,
             sample_count, cap)
         _native.check(rc, "aia_pack_rows_inline")
         return
@@ -442,15 +448,18 @@ class DeviceBatchPacker:
                         width * 2 if width > self._blocks else width)
         views = self._views.get((T, B, width))
         if views is None:      # steady decode steps repeat their shape
+            bt = self.block_table_buf[:B * width].view(B, width)
             views = self._views[(T, B, width)] = (
-                self.token_ids_buf[:T], self.positions_buf[:T], self.slot_mapping_buf[:T],
-                self.block_table_buf[:B * width].view(B, width), self.cu_buf[:B + 1],
-                self.kv_buf[:B])
+                self.token_ids_buf[:T], self.positions_buf[:T], self.slot_mapping_buf[:T], bt,
+                self.cu_buf[:B + 1], self.kv_buf[:B],
+                tuple(t.data_ptr() for t in (self.token_ids_buf, self.positions_buf,
+                                             self.slot_mapping_buf, bt, self.cu_buf,
+                                             self.kv_buf, self.last_buf)))
         bt = views[3]
         _launch(self.table, self._uploader, upd, block_size=bs, bt_width=width,
                 token_ids=self.token_ids_buf, positions=self.positions_buf,
                 slot_mapping=self.slot_mapping_buf, block_table=bt, cu=self.cu_buf,
-                kv=self.kv_buf, last_rows=self.last_buf)
+                kv=self.kv_buf, last_rows=self.last_buf, out_ptrs=views[6])
         ctx = ForwardContext(
             token_ids=views[0], positions=views[1], slot_mapping=views[2], block_table=bt,
             cu_seqlens_q=cu, seqlens_kv=kv, attn_mask=attn_mask, attn_backend=attn_backend,

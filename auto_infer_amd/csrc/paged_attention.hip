@@ -150,7 +150,7 @@ Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_
 
 // Workspace layout (all offsets 256-byte aligned).
 struct Layout {
-  int64_t hdr, seg, wave, part_ml, part_o, part_sc, cnt, req, mrg, pf, pfm, pf_o, pf_ml, total;
+  int64_t hdr, seg, wave, part_ml, part_o, part_sc, cnt, req, mrg, pf, pfm, pfw, pf_o, pf_ml, total;
   int64_t seg_cap, part_cap, mrg_cap, pf_cap, pf_unit_cap, pf_mrg_cap, pf_slots;
 };
 
@@ -192,6 +192,7 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
   L.pf_slots = split_units * g.hkv;             // partial row blocks
   L.pf = off;       off = align256(off + L.pf_unit_cap * 16);
   L.pfm = off;      off = align256(off + L.pf_mrg_cap * 16);
+  L.pfw = off;      off = align256(off + (g.pf ? kPfTargetWgs * 32 : 0));   // dealt work-groups
   L.pf_ml = off;    off = align256(off + L.pf_slots * kPfRows * 8);
   L.pf_o = off;     off = align256(off + L.pf_slots * kPfRows * (int64_t)kHeadDim * 4);
   L.total = off;
@@ -296,10 +297,12 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     int32_t* __restrict__ hdr, int32_t* __restrict__ seg, int32_t* __restrict__ wave_rec,
     int32_t* __restrict__ counters, int32_t* __restrict__ req_scratch,
     int32_t* __restrict__ mrg, int4* __restrict__ pf_units, int4* __restrict__ pf_mrg,
-    int32_t pf_cap, int32_t pf_unit_cap, int32_t pf_mrg_cap, int32_t seg_cap) {
+    int4* __restrict__ pf_wg, int32_t pf_cap, int32_t pf_unit_cap, int32_t pf_mrg_cap,
+    int32_t seg_cap) {
   __shared__ int lds[kPlanLds];
   __shared__ int wave_sums[kPlanThreads / 64];
   __shared__ int2 wave_sums2[kPlanThreads / 64];
+  __shared__ int pf_hist[64];
   const int tid = threadIdx.x;
   const int per_req = g.nkvg * g.nhb;
   // request metadata in LDS when it fits, else in the workspace / inputs
@@ -344,7 +347,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   // the causal mask they see the most keys).  When items x kv heads leave
   // the chip underfilled, an item's tiles are cut into k balanced chunks of
   // about `chunk` tiles; its k units write partials and get a merge record.
-  int units = 0, pmerges = 0;
+  int units = 0, pmerges = 0, dealt = 0;
   if (pcarry > 0) {
     const int* cu_p = req_lds ? cuv : cu_q;
     const int* kv_p = req_lds ? kvv : kvlen;
@@ -370,6 +373,31 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       // keeps units x kv heads within the target: one round of work-groups
       const int64_t room = kPfTargetWgs - (int64_t)pcarry * g.hkv;
       chunk = max(kPfMinChunk, (int)(((int64_t)wtot * g.hkv + room - 1) / room));
+      // That bound is loose.  In a step with no split-K segments the least
+      // chunk whose units still fit evens the work-groups out (the slowest
+      // one sets the kernel time), found by a binary search, one block
+      // reduction per probe.  Beside split-K ranges the loose bound stays:
+      // its fewer work-groups leave slots for the HBM-bound ranges.
+      const int ucap = kPfTargetWgs / g.hkv;
+      int lo = carry > 0 ? chunk : max(kPfMinChunk, (wtot + ucap - 1) / ucap);
+      while (lo < chunk) {
+        const int mid = (lo + chunk) >> 1;
+        int nu = 0;
+        for (int base = 0; base < batch; base += kPlanThreads) {
+          const int b = base + tid;
+          if (b < batch) {
+            const int lq = cu_p[b + 1] - cu_p[b], lk = kv_p[b];
+            if ((int64_t)lq * g.group >= kPfRows)
+              for (int r0 = 0; r0 < lq * g.group; r0 += kPfRows) {
+                const int nt = item_tiles(lq, lk, r0);
+                nu += nt > mid ? (nt + mid - 1) / mid : 1;
+              }
+          }
+        }
+        int utot;
+        block_exclusive_scan(nu, wave_sums, &utot);
+        if (utot <= ucap) chunk = mid; else lo = mid + 1;
+      }
     }
     int ucarry = 0, mcarry2 = 0;
     for (int base = 0; base < batch; base += kPlanThreads) {
@@ -408,6 +436,40 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     units = ucarry;
     pmerges = mcarry2;
     if (units > pf_unit_cap || pmerges > pf_mrg_cap) { units = 0; pmerges = 0; overflow = 1; }
+
+    // 1c) When a step has only prefill work-groups and they fit one round,
+    // two per CU (the hardware puts work-groups b and b + ncu on one CU
+    // then), deal them by size so every CU's pair sums evenly: the largest
+    // units alone on the CUs without a partner, then the i-th largest of the
+    // rest beside the i-th smallest.  Each dealt work-group gets its unit
+    // record and {unit, kv head} in pf_wg (two int4); hdr[9] = their number,
+    // 0 = not dealt.
+    const int jobs = units * g.hkv;
+    if (carry == 0 && jobs > g.ncu && jobs <= 2 * g.ncu && jobs <= kPfTargetWgs) {
+      if (tid < 64) pf_hist[tid] = 0;
+      __syncthreads();   // also publishes pf_units to the whole group
+      for (int p = tid; p < jobs; p += kPlanThreads) {
+        const int4 e = pf_units[p % units];
+        atomicAdd(&pf_hist[63 - min(e.w - e.z, 63)], 1);   // bucket 0: the largest
+      }
+      __syncthreads();
+      if (tid == 0) {
+        int acc = 0;
+        for (int k = 0; k < 64; ++k) { const int c = pf_hist[k]; pf_hist[k] = acc; acc += c; }
+      }
+      __syncthreads();
+      const int n2 = jobs - g.ncu, lone = g.ncu - n2;
+      for (int p = tid; p < jobs; p += kPlanThreads) {
+        const int u = p % units, kvh = p / units;
+        const int4 e = pf_units[u];
+        const int r = atomicAdd(&pf_hist[63 - min(e.w - e.z, 63)], 1);
+        const int i = r - lone;
+        const int id = r < lone ? n2 + r : i < n2 ? i : g.ncu + (jobs - 1 - r);
+        pf_wg[2 * id] = e;
+        pf_wg[2 * id + 1] = make_int4(u, kvh, 0, 0);
+      }
+      dealt = jobs;
+    }
   }
   __syncthreads();
   const int nseg = req_off[batch];
@@ -610,6 +672,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     hdr[0] = nseg; hdr[1] = total_tiles; hdr[2] = tpw; hdr[3] = carry; hdr[4] = waves;
     hdr[5] = mcarry; hdr[6] = units; hdr[7] = pmerges;
     hdr[8] = overflow ? -1 : 0;   // status: -1 = the metadata asked for more work than fits
+    hdr[9] = overflow ? 0 : dealt;
     // sentinel record so readers may look one past the end
     int* r = seg + (int64_t)nseg * 8;
     r[0] = 0; r[1] = 0; r[2] = 0; r[3] = 0; r[4] = 0;
@@ -1231,6 +1294,7 @@ struct PrefillArgs {
   uint16_t* out;
   int64_t o_ts, o_hs;
   const int4* units;         // {request, first row, first tile, end tile}
+  const int4* dealt;         // work-group b: its unit record, then {unit, kv head}
   const int32_t* hdr;
   float* part_o;             // partial row blocks of chunked items
   float2* part_ml;
@@ -1281,15 +1345,27 @@ template <bool ONE_BLOCK, bool FUSED>
 __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
                                                  uint16_t (*ks)[kPfKeys * kKStride],
                                                  uint16_t (*vs)[kPfKeys * kPfVStride]) {
-  // Work-group b takes (kv head, item) pair xcd_range(b, pairs), kv-head
-  // major: each XCD gets a contiguous run of pairs, so the items that re-read
-  // one request's keys for one kv head share an XCD's L2.
+  // Unless the planner dealt the work-groups by size (hdr[9]), work-group b
+  // takes (kv head, item) pair xcd_range(b, pairs), kv-head major: each XCD
+  // gets a contiguous run of pairs, so the items that re-read one request's
+  // keys for one kv head share an XCD's L2.
   const int count = a.hdr[6];
   const int pairs = count * a.hkv;
   if (wg >= pairs) return;
-  const int pair = xcd_range(wg, pairs);
-  const int kvh = pair / count, unit = pair - kvh * count;
-  const int4 it = a.units[unit];
+  int kvh, unit;
+  int4 it;
+  if (a.hdr[9] == pairs) {     // dealt by size (see the planner)
+    it = a.dealt[2 * wg];
+    const int4 x = a.dealt[2 * wg + 1];
+    unit = x.x;
+    kvh = x.y;
+    if (unit < 0 || unit >= count) return;
+  } else {
+    const int pair = xcd_range(wg, pairs);
+    kvh = pair / count;
+    unit = pair - kvh * count;
+    it = a.units[unit];
+  }
   const int b = it.x, row0 = it.y, t0 = it.z, t1 = it.w;
   if (b < 0 || b >= a.batch || kvh >= a.hkv) return;
   const int q_begin = a.cu_q[b], lq = a.cu_q[b + 1] - q_begin, lk = a.kvlen[b];
@@ -2190,7 +2266,8 @@ extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens
       reinterpret_cast<int32_t*>(ws + L.seg), reinterpret_cast<int32_t*>(ws + L.wave),
       reinterpret_cast<int32_t*>(ws + L.cnt), reinterpret_cast<int32_t*>(ws + L.req),
       reinterpret_cast<int32_t*>(ws + L.mrg), reinterpret_cast<int4*>(ws + L.pf),
-      reinterpret_cast<int4*>(ws + L.pfm), (int32_t)L.pf_cap, (int32_t)L.pf_unit_cap,
+      reinterpret_cast<int4*>(ws + L.pfm), reinterpret_cast<int4*>(ws + L.pfw),
+      (int32_t)L.pf_cap, (int32_t)L.pf_unit_cap,
       (int32_t)L.pf_mrg_cap, (int32_t)L.seg_cap);
   return check_hip(hipGetLastError(), "aia_attn_plan launch");
 }
@@ -2276,6 +2353,7 @@ extern "C" int aia_paged_attention_gqa(
     pa.scale_log2 = a.scale_log2;
     pa.out = a.out; pa.o_ts = a.o_ts; pa.o_hs = a.o_hs;
     pa.units = reinterpret_cast<const int4*>(ws + L.pf);
+    pa.dealt = reinterpret_cast<const int4*>(ws + L.pfw);
     pa.hdr = a.hdr;
     pa.part_o = reinterpret_cast<float*>(ws + L.pf_o);
     pa.part_ml = reinterpret_cast<float2*>(ws + L.pf_ml);

@@ -178,7 +178,7 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
   L.mrg_cap = L.seg_cap * g.nw * merge_slices(g, dv);
   L.mrg = off;      off = align256(off + L.mrg_cap * kMrgInts * 4);
   L.cnt = off;      off = align256(off + L.seg_cap * g.nw * 4);
-  L.req = off;      off = align256(off + ((int64_t)batch + 1) * 4);
+  L.req = off;      off = align256(off + ((int64_t)batch + 1) * 8);   // request and item offsets
   // prefill items: a routed request has >= kPfRows rows, so at most
   // rows / kPfRows of them, each adding at most one partial item
   const int64_t pf_rows = g.pf ? (int64_t)tokens * g.group : 0;
@@ -306,10 +306,11 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   const int tid = threadIdx.x;
   const int per_req = g.nkvg * g.nhb;
   // request metadata in LDS when it fits, else in the workspace / inputs
-  const bool req_lds = 3 * (batch + 1) <= kPlanLds;
+  const bool req_lds = 4 * (batch + 1) <= kPlanLds;
   int* req_off = req_lds ? lds : req_scratch;
   int* cuv = req_lds ? lds + (batch + 1) : nullptr;
   int* kvv = req_lds ? lds + 2 * (batch + 1) : nullptr;
+  int* item_off = req_lds ? lds + 3 * (batch + 1) : req_scratch + (batch + 1);
 
   // 1) segments per request -> request offsets; prefill-routed requests
   // get no segments and list their prefill items instead (last rows first:
@@ -332,7 +333,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     }
     int2 tot2;
     const int2 ex2 = block_exclusive_scan2(make_int2(cnt, pcnt), wave_sums2, &tot2);
-    if (b < batch) req_off[b] = carry + ex2.x;
+    if (b < batch) {
+      req_off[b] = carry + ex2.x;
+      item_off[b] = pcarry + ex2.y;
+    }
     carry += tot2.x;
     pcarry += tot2.y;
   }
@@ -347,25 +351,34 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   // the causal mask they see the most keys).  When items x kv heads leave
   // the chip underfilled, an item's tiles are cut into k balanced chunks of
   // about `chunk` tiles; its k units write partials and get a merge record.
+  // Every loop below runs over the flat item list (request-major, each
+  // request's items last rows first), one item per thread.
   int units = 0, pmerges = 0, dealt = 0;
   if (pcarry > 0) {
+    __syncthreads();   // item offsets
     const int* cu_p = req_lds ? cuv : cu_q;
     const int* kv_p = req_lds ? kvv : kvlen;
-    auto item_tiles = [&](int lq, int lk, int row0) {
-      const int last = min(lq * g.group, row0 + kPfRows) - 1;
+    // item f: its request, first row and key tiles
+    auto item_at = [&](int f, int& b, int& r0) {
+      int lo = 0, hi = batch - 1;  // last b with item_off[b] <= f
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (item_off[mid] <= f) lo = mid; else hi = mid - 1;
+      }
+      b = lo;
+      const int lq = cu_p[b + 1] - cu_p[b], lk = kv_p[b];
+      const int nitems = (lq * g.group + kPfRows - 1) / kPfRows;
+      r0 = (nitems - 1 - (f - item_off[b])) * kPfRows;
+      const int last = min(lq * g.group, r0 + kPfRows) - 1;
       const int kend = max(0, min(lk, lk - lq + last / g.group + 1));
       return (kend + kPfKeys - 1) / kPfKeys;
     };
     int chunk = 0x7fffffff;
     if ((int64_t)pcarry * g.hkv < kPfTargetWgs) {
       int mine = 0;
-      for (int base = 0; base < batch; base += kPlanThreads) {
-        const int b = base + tid;
-        if (b < batch) {
-          const int lq = cu_p[b + 1] - cu_p[b], lk = kv_p[b];
-          if ((int64_t)lq * g.group >= kPfRows)
-            for (int r0 = 0; r0 < lq * g.group; r0 += kPfRows) mine += item_tiles(lq, lk, r0);
-        }
+      for (int f = tid; f < pcarry; f += kPlanThreads) {
+        int b, r0;
+        mine += item_at(f, b, r0);
       }
       int wtot;
       block_exclusive_scan(mine, wave_sums, &wtot);
@@ -383,16 +396,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       while (lo < chunk) {
         const int mid = (lo + chunk) >> 1;
         int nu = 0;
-        for (int base = 0; base < batch; base += kPlanThreads) {
-          const int b = base + tid;
-          if (b < batch) {
-            const int lq = cu_p[b + 1] - cu_p[b], lk = kv_p[b];
-            if ((int64_t)lq * g.group >= kPfRows)
-              for (int r0 = 0; r0 < lq * g.group; r0 += kPfRows) {
-                const int nt = item_tiles(lq, lk, r0);
-                nu += nt > mid ? (nt + mid - 1) / mid : 1;
-              }
-          }
+        for (int f = tid; f < pcarry; f += kPlanThreads) {
+          int b, r0;
+          const int nt = item_at(f, b, r0);
+          nu += nt > mid ? (nt + mid - 1) / mid : 1;
         }
         int utot;
         block_exclusive_scan(nu, wave_sums, &utot);
@@ -400,35 +407,20 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       }
     }
     int ucarry = 0, mcarry2 = 0;
-    for (int base = 0; base < batch; base += kPlanThreads) {
-      const int b = base + tid;
-      int lq = 0, lk = 0, nu = 0, nm = 0;
-      bool routed = false;
-      if (b < batch) {
-        lq = cu_p[b + 1] - cu_p[b];
-        lk = kv_p[b];
-        routed = (int64_t)lq * g.group >= kPfRows;
+    for (int base = 0; base < pcarry; base += kPlanThreads) {
+      const int f = base + tid;
+      int b = 0, r0 = 0, nt = 0, k = 0;
+      if (f < pcarry) {
+        nt = item_at(f, b, r0);
+        k = nt > chunk ? (nt + chunk - 1) / chunk : 1;
       }
-      if (routed)
-        for (int r0 = 0; r0 < lq * g.group; r0 += kPfRows) {
-          const int nt = item_tiles(lq, lk, r0);
-          const int k = nt > chunk ? (nt + chunk - 1) / chunk : 1;
-          nu += k;
-          nm += k > 1 ? 1 : 0;
-        }
       int2 tot2;
-      const int2 ex2 = block_exclusive_scan2(make_int2(nu, nm), wave_sums2, &tot2);
-      if (routed && ucarry + tot2.x <= pf_unit_cap && mcarry2 + tot2.y <= pf_mrg_cap) {
-        int u = ucarry + ex2.x, mm = mcarry2 + ex2.y;
-        const int nitems = (lq * g.group + kPfRows - 1) / kPfRows;
-        for (int i = nitems - 1; i >= 0; --i) {
-          const int r0 = i * kPfRows;
-          const int nt = item_tiles(lq, lk, r0);
-          const int k = nt > chunk ? (nt + chunk - 1) / chunk : 1;
-          if (k > 1) pf_mrg[mm++] = make_int4(b, r0, u, k);
-          for (int j = 0; j < k; ++j)
-            pf_units[u++] = make_int4(b, r0, (int)((int64_t)j * nt / k), (int)((int64_t)(j + 1) * nt / k));
-        }
+      const int2 ex2 = block_exclusive_scan2(make_int2(k, k > 1 ? 1 : 0), wave_sums2, &tot2);
+      const int u = ucarry + ex2.x, mm = mcarry2 + ex2.y;
+      if (f < pcarry && u + k <= pf_unit_cap && mm + (k > 1) <= pf_mrg_cap) {
+        if (k > 1) pf_mrg[mm] = make_int4(b, r0, u, k);
+        for (int j = 0; j < k; ++j)
+          pf_units[u + j] = make_int4(b, r0, (int)((int64_t)j * nt / k), (int)((int64_t)(j + 1) * nt / k));
       }
       ucarry += tot2.x;
       mcarry2 += tot2.y;

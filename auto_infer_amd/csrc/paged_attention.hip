@@ -1755,7 +1755,10 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     int n = e / epr;
     const int c = (e - n * epr) * kMergeDims;
     const int rblk = n / kRows, t = (n - rblk * kRows) / a.hb;
-    const bool live = e < rows * epr && t < qb && rblk * qb + t < nq;
+    const int hh = n - rblk * kRows - t * a.hb;
+    // a group above 16 that 16 does not divide leaves its last head block
+    // part-filled: rows past the group hold no partials and are skipped
+    const bool live = e < rows * epr && t < qb && rblk * qb + t < nq && hbi * a.hb + hh < a.group;
     if (!live) n = 0;
     const int64_t row0 = (int64_t)row_base + n;
     float4 acc[kMergeDims / 4];
@@ -1819,7 +1822,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
         fold(sml[j][lane], x);
       }
       const float inv = ls > 0.f ? 1.f / ls : 0.f;
-      const int qi = rblk * qb + t, hh = n - rblk * kRows - t * a.hb;
+      const int qi = rblk * qb + t;
       const int head = kvh * a.group + hbi * a.hb + hh;
       uint16_t* op = a.out + (int64_t)(qtok0 + qi) * a.o_ts + (int64_t)head * a.o_hs + c;
       // 8-byte stores: the GQA output token stride need only be a multiple of 4
@@ -2210,9 +2213,6 @@ int check_heads(const char* fn, int32_t hq, int32_t hkv) {
   if (hq <= 0 || hkv <= 0 || hq % hkv != 0)
     return aia::fail(AIA_ERR_INVALID, "%s: num_q_heads %d must be a positive multiple of num_kv_heads %d",
                      fn, hq, hkv);
-  const int32_t group = hq / hkv;
-  if (group > kRows && group % kRows != 0)
-    return aia::fail(AIA_ERR_UNSUPPORTED, "%s: query group %d > 16 must be a multiple of 16", fn, group);
   return AIA_OK;
 }
 

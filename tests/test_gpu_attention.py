@@ -410,14 +410,28 @@ def test_mixed_launch_with_fused_kv_write():
 
 
 
-@pytest.mark.parametrize("hq,hkv", [(40, 2), (24, 1)])
-def test_group_above_16_not_a_multiple_is_rejected(hq, hkv):
-    """Query groups above 16 split into 16-head blocks; a group that 16 does
-    not divide is refused before any launch."""
-    step = workloads.make_gqa_step(lqs=[1, 3], lks=[70, 9], num_q_heads=hq, num_kv_heads=hkv,
-                                   block_size=16, seed=1)
-    with pytest.raises(NotImplementedError, match="multiple of 16"):
-        run_gpu(step)
+@pytest.mark.parametrize("hq,hkv", [(40, 2), (24, 1), (52, 2)])
+@pytest.mark.parametrize("waves", [7, 64, 0])
+@pytest.mark.parametrize("flags", [0, ops.ATTN_FUSED_MERGE])
+def test_group_above_16_not_a_multiple(hq, hkv, waves, flags):
+    """Groups of 20, 24 and 26 query heads: the second 16-head block of a kv
+    head is part-filled, and split rows past the group must not be merged
+    into the next kv head's outputs (the output is pre-filled with a
+    sentinel, so a stray write shows).  Decode, verify and a prefill-routed
+    request in one step."""
+    step = workloads.make_gqa_step(lqs=[1, 3, 1, 2, 40], lks=[700, 90, 1500, 33, 300],
+                                   num_q_heads=hq, num_kv_heads=hkv, block_size=16,
+                                   seed=hq + waves)
+    s = step
+    plan = ops.AttentionPlan.from_lists(s.block_table.to(DEV), s.cu_seqlens_q, s.seqlens_kv,
+                                        hq, hkv, 128, 16, num_waves=waves)
+    out = torch.full(s.q.shape, 7.0, dtype=torch.bfloat16, device=DEV)
+    ops.paged_attention_gqa(s.q.to(DEV), s.k_cache.to(DEV), s.v_cache.to(DEV), plan, s.scale,
+                            out=out, flags=flags)
+    torch.cuda.synchronize()
+    err = (out.float().cpu() - oracle(step)).abs().max().item()
+    print(f"max-abs err {err:.3e}", flush=True)
+    assert err <= TOL, err
 
 
 @pytest.mark.parametrize("waves", [0, 300])

@@ -2,7 +2,7 @@
 segments and their padding, row blocks, prefill items and their key chunks,
 merge) against the oracle, plus the fused KV write against the oracle write.
 
-Each case draws: heads (group 1..32), block size, a batch mixing decode,
+Each case draws: heads (group 1..32, 20 and 24 among them), block size, a batch mixing decode,
 verify (2-4 tokens) and prefill chunks (with and without a prefix), and
 optionally a forced range count.  Sizes keep the float32 oracle to well
 under a second per case.
@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 TOL = 2e-2
 
-HEADS = [(8, 8), (16, 8), (16, 4), (28, 4), (32, 8), (64, 4), (32, 1), (64, 2)]
+HEADS = [(8, 8), (16, 8), (16, 4), (28, 4), (32, 8), (64, 4), (32, 1), (64, 2), (40, 2), (24, 1)]
 BLOCKS = [4, 16, 32, 64, 128, 256]
 
 

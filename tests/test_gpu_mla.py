@@ -188,3 +188,12 @@ def test_mla_more_segments_than_the_planner_keeps_in_registers():
     lks = torch.randint(1, 300, (1100,), generator=torch.Generator().manual_seed(9)).tolist()
     step = workloads.make_mla_step(lqs=[1] * 1100, lks=lks, num_heads=16, block_size=64, seed=9)
     check(step)
+
+
+@pytest.mark.parametrize("waves", [5, 0])
+def test_mla_twenty_heads(waves):
+    """20 heads: the second 16-head block is part-filled; split rows past
+    the head count are neither merged nor written."""
+    step = workloads.make_mla_step(lqs=[1, 1, 2], lks=[3000, 200, 900], num_heads=20,
+                                   block_size=64, seed=20 + waves)
+    check(step, waves)

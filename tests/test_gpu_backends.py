@@ -413,3 +413,64 @@ def test_two_contexts_in_flight_on_two_streams_through_the_backends():
         assert (o.float().cpu() - ref_a).abs().max().item() <= TOL
     for o in outs["b"]:
         assert (o.float().cpu() - ref_b).abs().max().item() <= TOL
+
+
+def test_two_host_threads_gqa_and_mla_planning_every_step():
+    """Two host threads, each with its own stream, plan and run attention
+    steps at the same time (GQA in one, absorbed MLA in the other, a new
+    plan every step): the C-ABI holds no shared mutable state beyond its
+    thread-local error text, so every step of both matches the oracle."""
+    import threading
+    from auto_infer_amd import ops, workloads
+    from oracle.paged_attn import mla_absorbed_attention as mla_ref
+    ga = workloads.make_gqa_step(lqs=[1, 3, 1, 40], lks=[500, 90, 1200, 300], num_q_heads=16,
+                                 num_kv_heads=4, block_size=16, seed=71)
+    mb = workloads.make_mla_step(lqs=[1, 1, 2], lks=[2000, 300, 700], num_heads=16,
+                                 block_size=64, seed=72)
+    exp_a = paged_attention(ga.q, ga.k_cache, ga.v_cache, ga.block_table, ga.cu_seqlens_q,
+                            ga.seqlens_kv, ga.scale)
+    exp_b = mla_ref(mb.q_latent, mb.cache, mb.block_table, mb.cu_seqlens_q, mb.seqlens_kv,
+                    mb.scale, 512)
+    dev_a = {n: getattr(ga, n).to(DEV) for n in ("q", "k_cache", "v_cache", "block_table")}
+    dev_b = {n: getattr(mb, n).to(DEV) for n in ("q_latent", "cache", "block_table")}
+    torch.cuda.synchronize()
+    outs, errs = {"a": [], "b": []}, []
+
+    def run_a():
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for _ in range(20):
+                    plan = ops.AttentionPlan.from_lists(dev_a["block_table"], ga.cu_seqlens_q,
+                                                        ga.seqlens_kv, 16, 4, 128, 16)
+                    outs["a"].append(ops.paged_attention_gqa(dev_a["q"], dev_a["k_cache"],
+                                                             dev_a["v_cache"], plan, ga.scale))
+            s.synchronize()
+        except Exception as e:      # surfaced by the main thread
+            errs.append(e)
+
+    def run_b():
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for _ in range(20):
+                    plan = ops.AttentionPlan.from_lists(dev_b["block_table"], mb.cu_seqlens_q,
+                                                        mb.seqlens_kv, 16, 1, 512, 64)
+                    outs["b"].append(ops.paged_attention_mla(dev_b["q_latent"], dev_b["cache"],
+                                                             plan, mb.scale))
+            s.synchronize()
+        except Exception as e:
+            errs.append(e)
+
+    ts = [threading.Thread(target=run_a), threading.Thread(target=run_b)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(timeout=120)
+    assert not errs, errs
+    torch.cuda.synchronize()
+    assert len(outs["a"]) == 20 and len(outs["b"]) == 20
+    for o in outs["a"]:
+        assert (o.float().cpu() - exp_a).abs().max().item() <= 2e-2
+    for o in outs["b"]:
+        assert (o.float().cpu() - exp_b).abs().max().item() <= 2e-2

@@ -98,3 +98,27 @@ def test_argument_validation_of_the_fused_kernels_without_gpu():
     assert rc == _native.AIA_ERR_INVALID and "alignment" in _native.last_error()
     # no tokens: nothing to do, whatever the pointers
     assert lib.aia_mla_q_latent(None, 0, 0, 0, 16, None, None, 0, None, 0, None, 0, 0, None) == 0
+
+
+def test_error_messages_are_per_thread():
+    """aia_last_error() is thread local: two host threads failing with
+    different arguments at the same time each read their own message."""
+    import threading
+    lib = _native.load()
+    errs = []
+
+    def worker(hq):
+        out = ctypes.c_int64()
+        for _ in range(2000):
+            rc = lib.aia_attn_workspace_bytes(4, 4, hq, 2, 128, 0, ctypes.byref(out))
+            msg = _native.last_error()
+            if rc != _native.AIA_ERR_INVALID or f"num_q_heads {hq} " not in msg:
+                errs.append((hq, rc, msg))
+                return
+
+    ts = [threading.Thread(target=worker, args=(hq,)) for hq in (3, 5, 7)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errs, errs[:3]

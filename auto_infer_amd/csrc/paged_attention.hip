@@ -485,9 +485,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       }
       const int b = lo;
       const int local = s - req_off[b];
-      const int hb = local % g.nhb;
-      const int kvg = (local / g.nhb) % g.nkvg;
-      const int qblk = local / per_req;
+      // (one segment per query block in the common case: no divisions)
+      const int hb = g.nhb == 1 ? 0 : local % g.nhb;
+      const int kvg = g.nkvg == 1 ? 0 : (local / g.nhb) % g.nkvg;
+      const int qblk = per_req == 1 ? local : local / per_req;
       const int q_begin = cu_r[b];
       const int lq = cu_r[b + 1] - q_begin;
       const int lk = kv_r[b];
@@ -648,14 +649,14 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     if (bal && s < nseg) lds[pb0 + s] = carry + ex;
     if (mcnt > 0) {
       const int seg_rows = kRows * g.rb;
-      for (int i = 0; i < mcnt; ++i) {
-        const int w = i / nsl, sl = i - w * nsl;
-        // {first query token, query tokens, kv head, head block; first
-        // partial row, parts, slice, rows}, as two 16-byte stores
-        int4* m = reinterpret_cast<int4*>(mrg + (int64_t)(mcarry + mex + i) * kMrgInts);
-        m[0] = make_int4(r0[2], r0[3] & 0xff, (r0[1] & 0xffff) * g.nw + w, (r0[1] >> 16) & 0x3fff);
-        m[1] = make_int4(((carry + ex) * g.nw + w) * seg_rows, np, sl, rows);
-      }
+      int4* m = reinterpret_cast<int4*>(mrg + (int64_t)(mcarry + mex) * kMrgInts);
+      for (int w = 0; w < nwv; ++w)
+        for (int sl = 0; sl < nsl; ++sl, m += kMrgInts / 4) {
+          // {first query token, query tokens, kv head, head block; first
+          // partial row, parts, slice, rows}, as two 16-byte stores
+          m[0] = make_int4(r0[2], r0[3] & 0xff, (r0[1] & 0xffff) * g.nw + w, (r0[1] >> 16) & 0x3fff);
+          m[1] = make_int4(((carry + ex) * g.nw + w) * seg_rows, np, sl, rows);
+        }
     }
     mcarry += mtot;
     carry += tot;

@@ -1119,8 +1119,7 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
       old = __shfl(old, 0);
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       if (old == nparts - 1) {
-        // Merge.  This code runs once per split segment and head, cold in
-        // the instruction cache, so it is kept short.  Lane (p, c) folds
+        // Merge, kept to one short loop.  Lane (p, c) folds
         // parts p, p + 2, ... of output dims [4c, 4c + 4); lane k of a
         // 64-part chunk holds part k's (m, l).  A row whose parts fit one
         // 16-part batch costs one round trip: its (m, l) and partial loads

@@ -53,6 +53,38 @@ def test_config2_mixed_prefill_decode():
     check_sample(step, out, sample)
 
 
+@pytest.mark.parametrize("fused", [False, True])
+def test_config2_prefill_chunks_alone_dealt_by_size(fused):
+    """configs[1]'s three 512-token chunks alone: every request goes to the
+    prefill units, the planner takes the least chunk size whose units fit
+    one round and deals the 500 work-groups by size in CU pairs (hdr[9]).
+    Checked against the oracle, with and without the fused KV write."""
+    full = workloads.config2_mixed(seed=0)
+    sub, _ = workloads.subset(full, [0, 1, 2])
+    exp_k, exp_v = sub.k_cache.clone(), sub.v_cache.clone()
+    bs, starts = sub.k_cache.shape[1], [0] + list(sub.cu_seqlens_q[:-1])
+    slots = [int(sub.block_table[b, p // bs]) * bs + p % bs
+             for b, (c0, c1, lk) in enumerate(zip(starts, sub.cu_seqlens_q, sub.seqlens_kv))
+             for p in range(lk - (c1 - c0), lk)]
+    kv_write(sub.k_new, sub.v_new, exp_k, exp_v, slots)
+    exp = paged_attention(sub.q, exp_k, exp_v, sub.block_table, sub.cu_seqlens_q,
+                          sub.seqlens_kv, sub.scale)
+    kc, vc = (exp_k if not fused else sub.k_cache).to(DEV), (exp_v if not fused else sub.v_cache).to(DEV)
+    plan = ops.AttentionPlan.from_lists(sub.block_table.to(DEV), sub.cu_seqlens_q, sub.seqlens_kv,
+                                        28, 4, 128, sub.k_cache.shape[1])
+    kw = dict(key_new=sub.k_new.to(DEV), value_new=sub.v_new.to(DEV)) if fused else {}
+    out = ops.paged_attention_gqa(sub.q.to(DEV), kc, vc, plan, sub.scale, **kw)
+    torch.cuda.synchronize()
+    hdr = plan.workspace[:64].cpu().view(torch.int32).tolist()
+    units = hdr[6]
+    assert hdr[8] == 0 and units * 4 > 256 and hdr[9] == units * 4, hdr[:10]
+    err = (out.float().cpu() - exp).abs().max().item()
+    print(f"units {units}, max-abs err {err:.3e}", flush=True)
+    assert err <= TOL
+    if fused:
+        assert torch.equal(kc.cpu(), exp_k) and torch.equal(vc.cpu(), exp_v)
+
+
 def test_config4_mtp_verify_full():
     step = workloads.config4_mtp(seed=0, device=DEV)
     ops.write_kv(step.k_new, step.v_new, step.k_cache, step.v_cache, step.slot_mapping)

@@ -119,6 +119,7 @@ PyObject* build_rows(PyObject*, PyObject* args) {
   PyObject** items = PySequence_Fast_ITEMS(seq.get());
   long long qacc = 0, width = 0;
   bool all_decode = true;
+  Ref live_set;
 
   for (Py_ssize_t r = 0; r < count; ++r) {
     PyObject* sr = items[r];
@@ -166,6 +167,15 @@ PyObject* build_rows(PyObject*, PyObject* args) {
       PyObject* so = PyDict_GetItemWithError(slot_d.get(), rid.get());   // borrowed
       if (!so && PyErr_Occurred()) return nullptr;
       if (!so) {
+        if (live == Py_None) {   // the step's request ids, built on first need
+          live_set.p = PySet_New(nullptr);
+          if (!live_set) return nullptr;
+          for (Py_ssize_t k = 0; k < count; ++k) {
+            Ref id(PyObject_GetAttr(items[k], s_rid));
+            if (!id || PySet_Add(live_set.get(), id.get()) < 0) return nullptr;
+          }
+          live = live_set.get();
+        }
         Ref s(PyObject_CallMethodObjArgs(table, s_slot_for, rid.get(), live, nullptr));
         if (!s) return nullptr;
         slot = as_ll(s.get(), &err);
@@ -328,11 +338,25 @@ bool fill_i32(PyObject* a, int* out, Py_ssize_t n) {
   return !err;
 }
 
-PyObject* get_list(PyObject* o, const char* name) {
-  PyObject* v = PyObject_GetAttrString(o, name);
+// Interned attribute names of the per-step update lists.
+PyObject *u_ts, *u_ti, *u_tv, *u_bs, *u_bi, *u_bv, *u_rows;
+bool intern_update_names() {
+  if (u_rows) return true;
+  u_ts = PyUnicode_InternFromString("tok_slot");
+  u_ti = PyUnicode_InternFromString("tok_idx");
+  u_tv = PyUnicode_InternFromString("tok_val");
+  u_bs = PyUnicode_InternFromString("blk_slot");
+  u_bi = PyUnicode_InternFromString("blk_idx");
+  u_bv = PyUnicode_InternFromString("blk_val");
+  u_rows = PyUnicode_InternFromString("rows");
+  return u_ts && u_ti && u_tv && u_bs && u_bi && u_bv && u_rows;
+}
+
+PyObject* get_list(PyObject* o, PyObject* name) {
+  PyObject* v = PyObject_GetAttr(o, name);
   if (v && !PyList_Check(v)) {
     Py_DECREF(v);
-    PyErr_Format(PyExc_TypeError, "updates.%s must be a list", name);
+    PyErr_Format(PyExc_TypeError, "updates.%U must be a list", name);
     return nullptr;
   }
   return v;
@@ -344,9 +368,10 @@ PyObject* get_list(PyObject* o, const char* name) {
 // caller computed for these list lengths; reports the lengths.
 bool stage_impl(PyObject* upd, char* h, long long tw, long long bw, const long long (&o)[5],
                 long long row_ints, Py_ssize_t* nt_out, Py_ssize_t* nb_out, Py_ssize_t* nr_out) {
-  Ref ts(get_list(upd, "tok_slot")), ti(get_list(upd, "tok_idx")), tv(get_list(upd, "tok_val"));
-  Ref bsl(get_list(upd, "blk_slot")), bi(get_list(upd, "blk_idx")), bv(get_list(upd, "blk_val"));
-  Ref rows(get_list(upd, "rows"));
+  if (!intern_update_names()) return false;
+  Ref ts(get_list(upd, u_ts)), ti(get_list(upd, u_ti)), tv(get_list(upd, u_tv));
+  Ref bsl(get_list(upd, u_bs)), bi(get_list(upd, u_bi)), bv(get_list(upd, u_bv));
+  Ref rows(get_list(upd, u_rows));
   if (!ts || !ti || !tv || !bsl || !bi || !bv || !rows) return false;
   const Py_ssize_t nt = PyList_GET_SIZE(ti.get()), nb = PyList_GET_SIZE(bi.get());
   const Py_ssize_t nr = PyList_GET_SIZE(rows.get());
@@ -450,28 +475,45 @@ constexpr long long kInlineBytes = 3072;   // AIA_PACK_INLINE_BYTES
 // staged into a local buffer in the layout aia_pack_rows_inline takes (token
 // indices, token values, block indices, block values padded to a word, rows)
 // and handed to it, which passes them in the kernel launch.  Returns its
-// status; raises ValueError (from staging) on malformed updates.
-PyObject* pack_inline(PyObject*, PyObject* args) {
-  PyObject* upd;
-  unsigned long long fn, stream, token_pool, block_pool;
-  unsigned long long token_ids, positions, slot_mapping, block_table, cu, kv, last_rows, sample_rows;
-  long long tw, bw, row_ints, tp_stride, bp_stride;
-  int block_size, bt_width, sample_count, sample_cap;
-  if (!PyArg_ParseTuple(args, "OKKLLLKLKLiiKKKKKKKKii", &upd, &fn, &stream, &tw, &bw, &row_ints,
-                        &token_pool, &tp_stride, &block_pool, &bp_stride, &block_size, &bt_width,
-                        &token_ids, &positions, &slot_mapping, &block_table, &cu, &kv, &last_rows,
-                        &sample_rows, &sample_count, &sample_cap))
+// status, or kInlineTooLarge (nothing launched) when the step does not fit
+// kInlineBytes; raises ValueError (from staging) on malformed updates.
+// Positional arguments, taken without a format string (METH_FASTCALL): the
+// call sits on every decode step's host path.
+constexpr int kInlineTooLarge = 1;
+PyObject* pack_inline(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (nargs != 22) {
+    PyErr_SetString(PyExc_TypeError, "pack_inline takes 22 arguments");
     return nullptr;
-  Ref ti(get_list(upd, "tok_idx")), bi(get_list(upd, "blk_idx")), rows(get_list(upd, "rows"));
+  }
+  PyObject* upd = args[0];
+  long long v[21];
+  for (int i = 1; i < 22; ++i) {
+    v[i - 1] = PyLong_AsLongLong(args[i]);
+    if (v[i - 1] == -1 && PyErr_Occurred()) {
+      PyErr_Clear();      // addresses above 2^63 arrive as unsigned
+      v[i - 1] = (long long)PyLong_AsUnsignedLongLong(args[i]);
+      if (PyErr_Occurred()) return nullptr;
+    }
+  }
+  const unsigned long long fn = v[0], stream = v[1];
+  const long long tw = v[2], bw = v[3], row_ints = v[4];
+  const unsigned long long token_pool = v[5];
+  const long long tp_stride = v[6];
+  const unsigned long long block_pool = v[7];
+  const long long bp_stride = v[8];
+  const int block_size = (int)v[9], bt_width = (int)v[10];
+  const unsigned long long token_ids = v[11], positions = v[12], slot_mapping = v[13],
+                           block_table = v[14], cu = v[15], kv = v[16], last_rows = v[17],
+                           sample_rows = v[18];
+  const int sample_count = (int)v[19], sample_cap = (int)v[20];
+  if (!intern_update_names()) return nullptr;
+  Ref ti(get_list(upd, u_ti)), bi(get_list(upd, u_bi)), rows(get_list(upd, u_rows));
   if (!ti || !bi || !rows) return nullptr;
   const long long nt = PyList_GET_SIZE(ti.get()), nb = PyList_GET_SIZE(bi.get());
   const long long nr = PyList_GET_SIZE(rows.get());
   const long long o[5] = {0, 8 * nt, 16 * nt, 16 * nt + 8 * nb, 16 * nt + 8 * nb + 8 * ((nb + 1) / 2)};
   const long long total = o[4] + nr * row_ints * 4;
-  if (total > kInlineBytes) {
-    PyErr_SetString(PyExc_ValueError, "step too large for the inline pack");
-    return nullptr;
-  }
+  if (total > kInlineBytes) return PyLong_FromLong(kInlineTooLarge);
   alignas(16) char h[kInlineBytes];
   Py_ssize_t snt, snb, snr;
   if (!stage_impl(upd, h, tw, bw, o, row_ints, &snt, &snb, &snr)) return nullptr;
@@ -487,11 +529,12 @@ PyObject* pack_inline(PyObject*, PyObject* args) {
 }
 
 PyMethodDef methods[] = {
-    {"pack_inline", pack_inline, METH_VARARGS,
+    {"pack_inline", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(pack_inline)),
+     METH_FASTCALL,
      "pack_inline(updates, pack_rows_inline_fn, stream, token_width, block_width, row_ints, "
      "token_pool, token_pool_stride, block_pool, block_pool_stride, block_size, bt_width, "
      "token_ids, positions, slot_mapping, block_table, cu, kv, last_rows, sample_rows, "
-     "sample_count, sample_cap) -> status"},
+     "sample_count, sample_cap) -> status (1: the step does not fit the launch, nothing done)"},
     {"upload_pack", upload_pack, METH_VARARGS,
      "upload_pack(updates, pack_rows_fn, host, dev, wait_event, record_event, stream, token_width, "
      "block_width, total, 5 offsets, row_ints, token_pool, token_pool_stride, block_pool, "
@@ -501,7 +544,8 @@ PyMethodDef methods[] = {
      "stage(updates, host_address, token_width, block_width, off_tok_idx, off_tok_val, "
      "off_blk_idx, off_blk_val, off_rows, row_ints) -> None"},
     {"build_rows", build_rows, METH_VARARGS,
-     "build_rows(table, scheduled, get_request, block_tables, block_size, updates, live) -> "
+     "build_rows(table, scheduled, get_request, block_tables, block_size, updates, live) "
+     "(live: the step's request ids, or None to build them only if a new slot is needed) -> "
      "(cu_seqlens_q, seqlens_kv, sample_idx, decode_splice, all_decode, tokens, width)"},
     {nullptr, nullptr, 0, nullptr}};
 

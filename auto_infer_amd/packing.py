@@ -209,6 +209,7 @@ class _Uploader:
         self._dev = None
         self._turn = 0
         self._views = {}           # (turn, bytes) -> (device slice, host slice)
+        self.inline_addr = 0       # aia_pack_rows_inline, looked up on first use
 
     def reserve(self, upd):
         """Offsets and buffers of this step's upload, for the native upload
@@ -290,12 +291,11 @@ class PackedStep:
     last_rows: torch.Tensor        # (rows,) int64
 
 
-_INLINE_BYTES = 3072    # AIA_PACK_INLINE_BYTES
-
-
-def _inline_bytes(upd):
-    nt, nb, nr = len(upd.tok_idx), len(upd.blk_idx), len(upd.rows)
-    return 16 * nt + 8 * nb + 8 * ((nb + 1) // 2) + nr * _ROW_INTS * 4
+# Steps whose updates and row descriptors fit AIA_PACK_INLINE_BYTES go out in
+# the pack launch's arguments (aia_pack_rows_inline); the rest through the
+# staging copy.  (Tests switch the inline path off to cover the other.)
+_USE_INLINE = True
+_INLINE_TOO_LARGE = 1      # _hostpack.pack_inline: the step does not fit, nothing launched
 
 
 def _launch(table, uploader, upd, *, block_size, bt_width, token_ids, positions, slot_mapping,
@@ -305,10 +305,10 @@ def _launch(table, uploader, upd, *, block_size, bt_width, token_ids, positions,
     tensors' device addresses (token_ids, positions, slot_mapping,
     block_table, cu, kv, last_rows) when the caller keeps them."""
     cap = sample_rows.numel() if sample_rows is not None else 0
-    if (_hostpack is not None and uploader.device.type == "cuda"
-            and _inline_bytes(upd) <= _INLINE_BYTES):
+    if _USE_INLINE and _hostpack is not None and uploader.device.type == "cuda":
         # small step: updates and rows travel in the launch's arguments, no
-        # staging copy (aia_pack_rows_inline)
+        # staging copy (aia_pack_rows_inline); the native call stages them
+        # and says so (returns 1, nothing launched) when they do not fit
         sp = (stream.cuda_stream if stream is not None
               else _raw_stream(uploader.device_index) if _raw_stream is not None
               else torch.cuda.current_stream(uploader.device).cuda_stream)
@@ -317,13 +317,17 @@ def _launch(table, uploader, upd, *, block_size, bt_width, token_ids, positions,
                          last_rows.data_ptr())
         tp, bp = table.token_pool, table.block_pool
         tw, bw = tp.shape[1], bp.shape[1]
+        fn = uploader.inline_addr
+        if not fn:
+            fn = uploader.inline_addr = _native.address("aia_pack_rows_inline")
         rc = _hostpack.pack_inline(
-            upd, _native.address("aia_pack_rows_inline"), sp, tw, bw, _ROW_INTS,
+            upd, fn, sp, tw, bw, _ROW_INTS,
             tp.data_ptr(), tw, bp.data_ptr(), bw, block_size, bt_width, o[0], o[1], o[2], o[3],
             o[4], o[5], o[6], sample_rows.data_ptr() if sample_rows is not None else 0,
             sample_count, cap)
-        _native.check(rc, "aia_pack_rows_inline")
-        return
+        if rc != _INLINE_TOO_LARGE:
+            _native.check(rc, "aia_pack_rows_inline")
+            return
     if _hostpack is not None and uploader.device.type == "cuda":
         # one native call: event wait, staging, copy, event record, pack launch
         sp = (stream.cuda_stream if stream is not None
@@ -438,10 +442,13 @@ class DeviceBatchPacker:
         table = self.table
         upd = table.begin_step()
         scheduled = plan.scheduled
-        live = {sr.request_id for sr in scheduled}
-        rows_fn = _hostpack.build_rows if _hostpack is not None else build_rows_py
-        cu, kv, sample_idx, decode_splice, all_decode, qacc, width = rows_fn(
-            table, scheduled, plan.get_request, plan.block_tables, bs, upd, live)
+        if _hostpack is not None:     # builds the live set itself, only if a slot is needed
+            cu, kv, sample_idx, decode_splice, all_decode, qacc, width = _hostpack.build_rows(
+                table, scheduled, plan.get_request, plan.block_tables, bs, upd, None)
+        else:
+            cu, kv, sample_idx, decode_splice, all_decode, qacc, width = build_rows_py(
+                table, scheduled, plan.get_request, plan.block_tables, bs, upd,
+                {sr.request_id for sr in scheduled})
         T, B = qacc, len(plan.scheduled)
         if T > self._tokens or B > self._seqs or width > self._blocks:
             self._alloc(T * 2 if T > self._tokens else T, B * 2 if B > self._seqs else B,

@@ -221,7 +221,7 @@ def test_build_inline_and_staged_uploads_agree(inline, monkeypatch):
     (aia_pack_rows); a simulated run through either path matches the
     oracle step by step."""
     if not inline:
-        monkeypatch.setattr(packing, "_INLINE_BYTES", 0)
+        monkeypatch.setattr(packing, "_USE_INLINE", False)
     table = packing.DeviceRequestTable(DEV, max_slots=4, max_blocks=2, max_len=8)
     packer = packing.DeviceBatchPacker(16, DEV, table=table)
     n = 0

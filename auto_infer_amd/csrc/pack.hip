@@ -94,11 +94,16 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(PackArgs a) {
 // pool updates first, then, after a work-group barrier (one CU, so its
 // stores are visible to the whole group), one wave per row; 16 waves, so a
 // decode gear of up to 16 requests packs its rows in one pass.
+template <int BYTES>
 struct InlineBlob {
-  int64_t w[AIA_PACK_INLINE_BYTES / 8];
+  int64_t w[BYTES / 8];
 };
+// a smaller argument block for the common small step (a decode gear of a
+// dozen requests): the launch copies fewer argument bytes
+constexpr int kInlineSmall = 1024;
 
-__global__ __launch_bounds__(1024) void pack_inline_kernel(PackArgs a, InlineBlob blob, int32_t nt,
+template <int BYTES>
+__global__ __launch_bounds__(1024) void pack_inline_kernel(PackArgs a, InlineBlob<BYTES> blob, int32_t nt,
                                                           int32_t nb, int64_t* token_pool,
                                                           int32_t* block_pool) {
   const int64_t* tidx = blob.w;
@@ -217,8 +222,6 @@ extern "C" int aia_pack_rows_inline(const void* blob, int32_t num_token_updates,
   if (sample_cap > 0 && !sample_rows)
     return fail(AIA_ERR_INVALID, "aia_pack_rows_inline: null sample_rows");
   if (words == 0 && sample_cap == 0) return AIA_OK;
-  InlineBlob b;
-  memcpy(b.w, blob, (size_t)words * 8);
   PackArgs a;
   a.rows = nullptr; a.num_rows = (int32_t)nr;
   a.token_pool = token_pool; a.token_stride = token_pool_stride;
@@ -228,7 +231,17 @@ extern "C" int aia_pack_rows_inline(const void* blob, int32_t num_token_updates,
   a.block_table = block_table; a.cu_seqlens_q = cu_seqlens_q; a.seqlens_kv = seqlens_kv;
   a.last_rows = last_rows; a.sample_rows = sample_rows;
   a.sample_count = sample_count; a.sample_cap = sample_cap;
-  pack_inline_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(a, b, (int32_t)nt, (int32_t)nb, token_pool,
-                                                         block_pool);
+  if (words * 8 <= kInlineSmall) {
+    InlineBlob<kInlineSmall> b;
+    memcpy(b.w, blob, (size_t)words * 8);
+    pack_inline_kernel<kInlineSmall><<<1, 1024, 0, (hipStream_t)stream>>>(a, b, (int32_t)nt,
+                                                                          (int32_t)nb, token_pool,
+                                                                          block_pool);
+  } else {
+    InlineBlob<AIA_PACK_INLINE_BYTES> b;
+    memcpy(b.w, blob, (size_t)words * 8);
+    pack_inline_kernel<AIA_PACK_INLINE_BYTES><<<1, 1024, 0, (hipStream_t)stream>>>(
+        a, b, (int32_t)nt, (int32_t)nb, token_pool, block_pool);
+  }
   return check_hip(hipGetLastError(), "aia_pack_rows_inline launch");
 }

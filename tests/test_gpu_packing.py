@@ -229,3 +229,26 @@ def test_build_inline_and_staged_uploads_agree(inline, monkeypatch):
         check_build(packer, plan, 16)
         n += 1
     assert n > 20
+
+
+@pytest.mark.parametrize("batch", [16, 44, 90])
+def test_build_of_each_inline_argument_size(batch):
+    """Decode steps of 16, 44 and 90 requests growing one token a step: in
+    steady state their rows (32 B each) and new token ids (16 B each) take
+    the 1 KB inline argument block, the 3 KB one, and (90 requests) the
+    staging copy.  Every step matches the oracle."""
+    from auto_infer_amd.execution import BatchPlan, RequestView, ScheduledRequest
+    rng = np.random.default_rng(batch)
+    bs = 16
+    lens = rng.integers(5, 40, size=batch).tolist()
+    perm = rng.permutation(4 * batch).tolist()
+    packer = packing.DeviceBatchPacker(bs, DEV)
+    for k in range(4):
+        views, tables, sched = {}, {}, []
+        for i, lk in enumerate(lens):
+            lk += k
+            rid = f"q{i}"
+            tables[rid] = tuple(perm[4 * i: 4 * i + (lk + bs - 1) // bs])
+            views[rid] = RequestView(rid, tuple(range(100 + i, 100 + i + lk)), lk - 1, 1, 1, ())
+            sched.append(ScheduledRequest(rid, 1, False, tables[rid]))
+        check_build(packer, BatchPlan.make(sched, views, tables), bs)

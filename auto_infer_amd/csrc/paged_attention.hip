@@ -211,6 +211,8 @@ int32_t resolve_waves(int32_t w, const Geometry& g, int32_t dv) {
 
 // ---------------------------------------------------------------- planner
 
+constexpr int kXcdsPlan = 8;      // XCDs the hardware deals work-groups to, round-robin
+
 // Inclusive prefix sum over the 64 lanes of a wave with DPP moves (VALU
 // only, no LDS crossbar round trips): shifts by 1, 2, 4, 8 within each row of
 // 16 lanes (lanes shifted in from outside the row read 0), then row 0's last
@@ -527,11 +529,17 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   const int real_tiles = carry;
   int tpw = max(1, (real_tiles + waves - 1) / waves);
   const bool pad = 2 * nseg <= waves && tpw < kPadBelow;
+  // Padded GQA plans aim at 3/4 of the range budget: with ranges this
+  // short, fewer and slightly longer ones measured faster (config 1 22.7
+  // against 22.8 us, configs[3] 40.8 against 41.4, with the ranges spread
+  // over the XCDs as below); MLA keeps its tuned budget.
+  const int pw = (pad && dv != 512 && 2 * nseg <= waves * 3 / 4) ? waves * 3 / 4 : waves;
   if (pad) {
-    // smallest length whose padded ranges fit in `waves`: the bound
-    // ceil(tiles / (waves - nseg)) always fits, and a few block reductions
+    // smallest length whose padded ranges fit in `pw`: the bound
+    // ceil(tiles / (pw - nseg)) always fits, and a few block reductions
     // find the least one (an idle range slot is an idle work-group)
-    int hi = max(1, (real_tiles + waves - nseg - 1) / (waves - nseg));
+    tpw = max(1, (real_tiles + pw - 1) / pw);
+    int hi = max(1, (real_tiles + pw - nseg - 1) / (pw - nseg));
     while (tpw < hi) {
       const int mid = (tpw + hi) >> 1;
       int mine = 0;
@@ -550,7 +558,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       }
       int tot;
       block_exclusive_scan(mine, wave_sums, &tot);
-      if (tot <= waves) hi = mid; else tpw = mid + 1;
+      if (tot <= pw) hi = mid; else tpw = mid + 1;
     }
   }
   int total_tiles = real_tiles;
@@ -747,10 +755,23 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     }
     return;
   }
+  // GQA: work-group w runs the range in record slot w, and the hardware
+  // deals work-groups to the 8 XCDs round-robin; the used ranges go to the
+  // slots so that XCD x gets a contiguous run of about nr / 8 of them (a
+  // padded plan's unused slots no longer pile up on the last XCDs: config 1
+  // 22.8 against 23.2 us).  MLA work-groups read slot = range.
+  const bool spread = dv != 512;
+  const int nr_used = (total_tiles + tpw - 1) / tpw;
   for (int w = tid; w < waves; w += kPlanThreads) {
-    const int t0 = w * tpw;
+    int r = w;
+    if (spread) {
+      const int x = w % kXcdsPlan, i = w / kXcdsPlan;
+      const int q = nr_used / kXcdsPlan, rem = nr_used - q * kXcdsPlan;
+      r = i < q + (x < rem ? 1 : 0) ? x * q + min(x, rem) + i : waves;
+    }
+    const int t0 = r * tpw;
     int* out = wave_rec + (int64_t)w * kRecInts;
-    if (t0 >= total_tiles) {
+    if (r >= waves || t0 >= total_tiles) {
       *reinterpret_cast<int4*>(out) = make_int4(-1, 0, 0, tpw);
       continue;
     }
@@ -1221,13 +1242,13 @@ template <int NW, int RB, int D, bool FM>
 #ifndef AIA_GQA_WAVES_PER_EU
 #define AIA_GQA_WAVES_PER_EU 2
 #endif
-__device__ __forceinline__ void gqa_attn_body(const AttnArgs& a, int bid, int nblocks,
+__device__ __forceinline__ void gqa_attn_body(const AttnArgs& a, int bid,
                                               uint16_t (*vt_all)[kTile * kVStride]) {
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (bid >= a.waves) return;
-  const int w = xcd_range(bid, nblocks);
-  const int* wr = a.wave_rec + (int64_t)w * kRecInts;
+  // the planner placed the ranges in the slots, spread over the XCDs
+  const int* wr = a.wave_rec + (int64_t)bid * kRecInts;
   const int pre = wr[16 + (lane & (kRecBlocks - 1))];   // issued with the header
   const int nseg = a.hdr[0], total_tiles = a.hdr[1];
   const int ngroups = (a.hkv + NW - 1) / NW, nhb = (a.group + a.hb - 1) / a.hb;
@@ -1237,6 +1258,7 @@ __device__ __forceinline__ void gqa_attn_body(const AttnArgs& a, int bid, int nb
   if (s < 0 || s >= nseg || t < 0 || t >= t_end || t_end > total_tiles || tpw < 1 ||
       s_last < s || s_last >= nseg)
     return;
+  const int w = t / tpw;                                  // the range's index
   int rec[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) rec[i] = wr[4 + i];
@@ -1264,7 +1286,7 @@ template <int NW, int RB, int D, bool FM>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(AIA_GQA_WAVES_PER_EU, AIA_GQA_WAVES_PER_EU)))
 void gqa_attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vt_all[NW][kTile * kVStride];
-  gqa_attn_body<NW, RB, D, FM>(a, blockIdx.x, gridDim.x, vt_all);
+  gqa_attn_body<NW, RB, D, FM>(a, blockIdx.x, vt_all);
 }
 
 // ---------------------------------------------------------------- prefill
@@ -1690,7 +1712,7 @@ static_assert(kPfWaves * kTile * kVStride <= 2 * kPfKeys * kKStride,
               "decode V^T staging must fit the prefill K buffers");
 template <bool ONE_BLOCK, bool FUSED>
 __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(AIA_PF_WPE, AIA_PF_WPE)))
-void gqa_mixed_kernel(AttnArgs a, PrefillArgs pa, int npf, int ndec) {
+void gqa_mixed_kernel(AttnArgs a, PrefillArgs pa, int npf) {
   __shared__ __attribute__((aligned(16))) uint16_t ks[2][kPfKeys * kKStride];
   __shared__ __attribute__((aligned(16))) uint16_t vs[2][kPfKeys * kPfVStride];
   // Prefill units take the first npf block ids and the decode ranges the
@@ -1704,7 +1726,7 @@ void gqa_mixed_kernel(AttnArgs a, PrefillArgs pa, int npf, int ndec) {
   if (prefill)
     gqa_prefill_body<ONE_BLOCK, FUSED>(pa, idx, ks, vs);
   else
-    gqa_attn_body<kPfWaves, 1, kHeadDim, false>(a, idx, ndec,
+    gqa_attn_body<kPfWaves, 1, kHeadDim, false>(a, idx,
                                          reinterpret_cast<uint16_t(*)[kTile * kVStride]>(&ks[0][0]));
 }
 
@@ -2356,10 +2378,10 @@ extern "C" int aia_paged_attention_gqa(
       !a.fused_merge) {
     const int npf = (int)(L.pf_unit_cap * g.hkv);
     const dim3 grid((unsigned)(npf + waves));
-    if (one_block && pa.kn) gqa_mixed_kernel<true, true><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf, waves);
-    else if (one_block) gqa_mixed_kernel<true, false><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf, waves);
-    else if (pa.kn) gqa_mixed_kernel<false, true><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf, waves);
-    else gqa_mixed_kernel<false, false><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf, waves);
+    if (one_block && pa.kn) gqa_mixed_kernel<true, true><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
+    else if (one_block) gqa_mixed_kernel<true, false><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
+    else if (pa.kn) gqa_mixed_kernel<false, true><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
+    else gqa_mixed_kernel<false, false><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
     if (int rc = check_hip(hipGetLastError(), "gqa_mixed_kernel launch")) return rc;
   } else {
 #define AIA_GQA_LAUNCH_D(NW, D, FM)                                               \

@@ -761,20 +761,19 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   // padded plan's unused slots no longer pile up on the last XCDs: config 1
   // 22.8 against 23.2 us).  MLA work-groups read slot = range.
   const bool spread = dv != 512;
-  const int nr_used = (total_tiles + tpw - 1) / tpw;
-  for (int w = tid; w < waves; w += kPlanThreads) {
-    int r = w;
-    if (spread) {
-      const int x = w % kXcdsPlan, i = w / kXcdsPlan;
-      const int q = nr_used / kXcdsPlan, rem = nr_used - q * kXcdsPlan;
-      r = i < q + (x < rem ? 1 : 0) ? x * q + min(x, rem) + i : waves;
-    }
+  const int nr_used = min(waves, (total_tiles + tpw - 1) / tpw);
+  const int q8 = nr_used / kXcdsPlan, rem8 = nr_used - q8 * kXcdsPlan;
+  // Range r goes to slot (i, x) = its place i in XCD x's run; threads walk
+  // the ranges in order, so a wave's searches and record loads stay local.
+  auto slot_of = [&](int r) {
+    if (!spread) return r;
+    const int big = (q8 + 1) * rem8;          // the first rem8 runs hold q8 + 1
+    const int x = r < big ? r / (q8 + 1) : rem8 + (r - big) / q8;
+    const int i = r < big ? r - x * (q8 + 1) : r - big - (x - rem8) * q8;
+    return i * kXcdsPlan + x;
+  };
+  for (int r = tid; r < nr_used; r += kPlanThreads) {
     const int t0 = r * tpw;
-    int* out = wave_rec + (int64_t)w * kRecInts;
-    if (r >= waves || t0 >= total_tiles) {
-      *reinterpret_cast<int4*>(out) = make_int4(-1, 0, 0, tpw);
-      continue;
-    }
     const int t1 = min(total_tiles, t0 + tpw);
     int lo = 0, hi = nseg - 1;  // last s with tile_begin <= t0
     while (lo < hi) {
@@ -788,7 +787,14 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       const int tb = tb_lds ? lds[mid] : seg[(int64_t)mid * 8 + 5];
       if (tb < t1) lo2 = mid; else hi2 = mid - 1;
     }
-    write_rec(out, lo, lo2, t0, t1, 0, 0);
+    write_rec(wave_rec + (int64_t)slot_of(r) * kRecInts, lo, lo2, t0, t1, 0, 0);
+  }
+  // slots no range maps to
+  for (int w = tid; w < waves; w += kPlanThreads) {
+    const int x = w % kXcdsPlan, i = w / kXcdsPlan;
+    const bool used = spread ? i < q8 + (x < rem8 ? 1 : 0) : w < nr_used;
+    if (!used)
+      *reinterpret_cast<int4*>(wave_rec + (int64_t)w * kRecInts) = make_int4(-1, 0, 0, tpw);
   }
 }
 

@@ -529,11 +529,12 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   const int real_tiles = carry;
   int tpw = max(1, (real_tiles + waves - 1) / waves);
   const bool pad = 2 * nseg <= waves && tpw < kPadBelow;
-  // Padded GQA plans aim at 3/4 of the range budget: with ranges this
+  // Padded GQA plans aim at 7/8 of the range budget: with ranges this
   // short, fewer and slightly longer ones measured faster (config 1 22.7
-  // against 22.8 us, configs[3] 40.8 against 41.4, with the ranges spread
-  // over the XCDs as below); MLA keeps its tuned budget.
-  const int pw = (pad && dv != 512 && 2 * nseg <= waves * 3 / 4) ? waves * 3 / 4 : waves;
+  // against 23.1 us, configs[3] 40.7 against 41.0; 3/4 measured the same
+  // on config 1, 5/8 and 1/2 slower), with the ranges spread over the XCDs
+  // as below; MLA keeps its tuned budget.
+  const int pw = (pad && dv != 512 && 2 * nseg <= waves * 7 / 8) ? waves * 7 / 8 : waves;
   if (pad) {
     // smallest length whose padded ranges fit in `pw`: the bound
     // ceil(tiles / (pw - nseg)) always fits, and a few block reductions

@@ -1231,12 +1231,14 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   }
 }
 
-// XCD-aware range order.  The hardware deals work-groups to the 8 XCDs
-// round-robin by id; mapping work-group b to range x q + min(x, r) + b / 8
-// (x = b % 8, n = 8 q + r) gives each XCD a contiguous run of ranges, so
-// the requests it serves -- and the keys their query blocks re-read -- stay
-// in its own L2.
+// XCD-aware order of the prefill work items.  The hardware deals
+// work-groups to the 8 XCDs round-robin by id; mapping work-group b to item
+// x q + min(x, r) + b / 8 (x = b % 8, n = 8 q + r) gives each XCD a
+// contiguous run of items, so the requests it serves -- and the keys their
+// query blocks re-read -- stay in its own L2.  (The split-K ranges get the
+// same order from the planner, which writes them into their slots.)
 constexpr int kXcds = 8;
+static_assert(kXcds == kXcdsPlan, "one XCD count for the planner and the kernels");
 __device__ __forceinline__ int xcd_range(int b, int n) {
   const int q = n / kXcds, r = n - q * kXcds;
   const int x = b % kXcds, i = b / kXcds;

@@ -444,3 +444,38 @@ def test_more_segments_than_the_planner_keeps_in_registers(waves):
     step = workloads.make_gqa_step(lqs=[1] * 1100, lks=lks, num_q_heads=8, num_kv_heads=1,
                                    block_size=16, seed=5)
     check(step, waves)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_gqa_plan_ranges_spread_over_the_xcds(seed):
+    """Read a config-1 plan back.  The planner writes every range it uses
+    into a record slot so that slot b (run by work-group b, dealt to XCD
+    b % 8) holds XCD b % 8's next range: every range start appears exactly
+    once, each XCD's ranges are consecutive, and the XCDs' counts differ by
+    at most one; unused slots hold empty records."""
+    step = workloads.config1_decode(seed=seed)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, 16, 8, 128, 128)
+    torch.cuda.synchronize()
+    ws = plan.workspace.cpu().view(torch.int32)
+    hdr = ws[:64].tolist()
+    total, tpw, waves = hdr[1], hdr[2], hdr[4]
+    # layout for Hq 16 / Hkv 8, one query token per request: 18 segment slots
+    seg_cap = 16 + 2
+    rec_off = (256 + (seg_cap + 1) * 32 + 255) // 256 * 256
+    recs = ws[rec_off // 4: rec_off // 4 + waves * 32].view(waves, 32)
+    nr = -(-total // tpw)
+    assert tpw >= 1 and nr <= waves
+    starts = {}
+    for b in range(waves):
+        r = recs[b].tolist()
+        if r[0] < 0:
+            continue
+        assert r[1] % tpw == 0 and r[2] == min(total, r[1] + tpw)
+        starts.setdefault(b % 8, []).append(r[1] // tpw)
+    got = sorted(i for v in starts.values() for i in v)
+    assert got == list(range(nr))
+    counts = [len(starts.get(x, [])) for x in range(8)]
+    assert max(counts) - min(counts) <= 1
+    for x, v in starts.items():
+        assert v == list(range(v[0], v[0] + len(v)))

@@ -1324,12 +1324,11 @@ struct PrefillArgs {
   int32_t part_units;        // units the partial buffer holds
 };
 
-// LDS row strides (elements) of the staged K and V tiles: 272 bytes puts the
-// 16 keys of a K fragment read in distinct banks; V keeps the transposing
-// read's 288 bytes.  (Measured on the configs[1] prefill chunks: 288-byte K
-// rows are as fast, unpadded 256-byte rows 25% slower, 264-byte rows 75%.)
-constexpr int kKStride = 136;
-constexpr int kPfVStride = kVStride;
+// LDS rows of the staged K and V tiles are 256 bytes, unpadded: the direct
+// loads write whole 1 KB runs, so the chunks of each row are swizzled
+// instead (see the loader).
+constexpr int kKStride = kHeadDim;
+constexpr int kPfVStride = kHeadDim;
 constexpr int kPfDtBatch = 4;      // V^T fragments read ahead of their MFMAs
 // Wave priority raised around each MFMA block, so a wave entering its MFMA
 // phase issues ahead of the co-resident wave, which runs its softmax VALU
@@ -1346,7 +1345,7 @@ constexpr float kLazyLog2 = AIA_PF_LAZY;              // max growth (log2) befor
 // kPfRows consecutive rows of one request's (query token, group head) row
 // list, row = token * group + head-in-group; each of the 4 waves owns 32
 // rows (two 16-row MFMA tiles).  The work-group walks the keys its rows can
-// see in tiles of 64: every K/V tile is loaded once (registers, then one of
+// see in tiles of 64: every K/V tile is loaded once (straight into one of
 // two LDS buffers, one barrier per tile) and used by all 128 rows.
 //   S^T = K Q^T   v_mfma_f32_16x16x32_bf16, K fragments ds_read_b128 from LDS
 //                 (lane (key n, group g) reads dims 32 j + 8 g of key n), Q^T
@@ -1366,8 +1365,8 @@ constexpr float kLazyLog2 = AIA_PF_LAZY;              // max growth (log2) befor
 #endif
 template <bool ONE_BLOCK, bool FUSED>
 __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
-                                                 uint16_t (*ks)[kPfKeys * kKStride],
-                                                 uint16_t (*vs)[kPfKeys * kPfVStride]) {
+                                                 uint16_t* k0, uint16_t* k1,
+                                                 uint16_t* v0, uint16_t* v1) {
   // Unless the planner dealt the work-groups by size (hdr[9]), work-group b
   // takes (kv head, item) pair xcd_range(b, pairs), kv-head major: each XCD
   // gets a contiguous run of pairs, so the items that re-read one request's
@@ -1462,13 +1461,19 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
   const bool whole = t0 == 0 && t1 == ntiles;
   if (!whole && unit >= a.part_units) return;
 
-  // loader: thread tid moves 16-byte chunk (tid % 16) of keys kLdKeys i + tid / 16.
+  // Loader: thread tid moves 16-byte chunk (tid % 16) of keys kLdKeys i + tid / 16
+  // straight from global memory into LDS (no registers, no LDS stores).  Each
+  // wave's load writes one 1 KB run, four key rows of 256 bytes with lane l at
+  // byte 16 l; lane l fetches the chunk whose swizzled place that is: K chunk
+  // c of key r sits at c ^ (r % 16) and V chunk c at c ^ 2 (r % 8), so the K
+  // fragment reads (16 keys, one chunk each) and the V^T transposing reads (8
+  // keys, 32 bytes each) hit distinct banks without padded rows.
   // Block ids are fetched one tile ahead (their loads are in flight during a
-  // tile's math), so a tile's K/V loads never wait on a table lookup.  When
-  // the block size is a multiple of the tile, a tile lies in one block: its
-  // id is one scalar load and a key's address one multiply-add.  Keys past
-  // the last visible one re-read it (never a slot that may hold stale
-  // bytes); keys at this step's new positions come from the new rows.
+  // tile's math), so a tile's loads never wait on a table lookup.  When the
+  // block size is a multiple of the tile, a tile lies in one block: its id is
+  // one scalar load and a key's address one multiply-add.  Keys past the last
+  // visible one re-read it (never a slot that may hold stale bytes); keys at
+  // this step's new positions come from the new rows.
   const int lkey = tid >> 4, lc = tid & 15;
   const int64_t kvoff = (int64_t)kvh * kHeadDim;
   const uint16_t* kcb = a.kc + kvoff;
@@ -1477,7 +1482,6 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
   const uint16_t* vnb = FUSED ? a.vn + kvoff : nullptr;
   constexpr int kLdKeys = kPfWaves * 4;                // keys per loader round
   constexpr int kLdRounds = kPfKeys / kLdKeys;
-  uint4 kr[kLdRounds], vr[kLdRounds];
   int bid[kLdRounds];
   auto fetch_ids = [&](int t) {
     if (ONE_BLOCK) {
@@ -1487,44 +1491,43 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
       for (int i = 0; i < kLdRounds; ++i) bid[i] = btrow[min(t * kPfKeys + kLdKeys * i + lkey, kend - 1) / a.bs];
     }
   };
-  auto fetch_row = [&](int i, int p, int slot) {
+  auto load_row = [&](int i, int p, int slot, uint16_t* kdst, uint16_t* vdst) {
     const int64_t e = (int64_t)slot * row_elems;
-    const uint4* kp = reinterpret_cast<const uint4*>(kcb + e);
-    const uint4* vp = reinterpret_cast<const uint4*>(vcb + e);
+    const uint16_t* kp = kcb + e;
+    const uint16_t* vp = vcb + e;
     if (FUSED) {
       const bool fresh = p >= ctx0;
       const int64_t tok = q_begin + (p - ctx0);
-      kp = fresh ? reinterpret_cast<const uint4*>(knb + tok * a.kn_ts) : kp;
-      vp = fresh ? reinterpret_cast<const uint4*>(vnb + tok * a.vn_ts) : vp;
+      kp = fresh ? knb + tok * a.kn_ts : kp;
+      vp = fresh ? vnb + tok * a.vn_ts : vp;
     }
-    kr[i] = kp[lc];
-    vr[i] = vp[lc];
+    const int rb = (kLdKeys * i + 4 * wid) * kHeadDim;     // the wave's first row
+    __builtin_amdgcn_global_load_lds(kp + 8 * (lc ^ lkey),
+                                     (__attribute__((address_space(3))) void*)(kdst + rb), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(vp + 8 * (lc ^ (2 * (lkey & 7))),
+                                     (__attribute__((address_space(3))) void*)(vdst + rb), 16, 0, 0);
   };
-  auto load = [&](int t) {
-    const int k0 = t * kPfKeys;
+  auto load = [&](int t, auto buf_tag) {
+    constexpr int B = decltype(buf_tag)::value;
+    uint16_t* kdst = B ? k1 : k0;
+    uint16_t* vdst = B ? v1 : v0;
+    const int kb = t * kPfKeys;
     if (ONE_BLOCK) {
       const int blk = min(max(bid[0], 0), a.nb - 1);
-      const int slot0 = blk * a.bs + k0 % a.bs;
-      const int last = kend - 1 - k0;
+      const int slot0 = blk * a.bs + kb % a.bs;
+      const int last = kend - 1 - kb;
 #pragma unroll
       for (int i = 0; i < kLdRounds; ++i) {
         const int off = min(kLdKeys * i + lkey, last);
-        fetch_row(i, k0 + off, slot0 + off);
+        load_row(i, kb + off, slot0 + off, kdst, vdst);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < kLdRounds; ++i) {
-        const int p = min(k0 + kLdKeys * i + lkey, kend - 1);
+        const int p = min(kb + kLdKeys * i + lkey, kend - 1);
         const int blk = min(max(bid[i], 0), a.nb - 1);
-        fetch_row(i, p, blk * a.bs + p % a.bs);
+        load_row(i, p, blk * a.bs + p % a.bs, kdst, vdst);
       }
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < kLdRounds; ++i) {
-      *reinterpret_cast<u32x4_t*>(&ks[buf][(kLdKeys * i + lkey) * kKStride + 8 * lc]) = as_u4(kr[i]);
-      *reinterpret_cast<u32x4_t*>(&vs[buf][(kLdKeys * i + lkey) * kPfVStride + 8 * lc]) = as_u4(vr[i]);
     }
   };
 
@@ -1538,12 +1541,13 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     lsum[rt] = 0.f;
   }
 
-  auto compute = [&](int t, int buf, auto mask_tag) {
+  auto compute = [&](int t, auto buf_tag, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
+    constexpr int B = decltype(buf_tag)::value;
     const int kbase = t * kPfKeys;
     if (MASK && kbase > wlim_hi) return;         // no row of this wave sees these keys
-    const uint16_t* kt = ks[buf];
-    const uint16_t* vt = vs[buf];
+    const uint16_t* kt = B ? k1 : k0;
+    const uint16_t* vt = B ? v1 : v0;
     constexpr int kSt = kPfKeys / 16;      // 16-key sub-tiles
     float4_t acc[kPfRt][kSt];
 #if AIA_PF_PRIO
@@ -1554,7 +1558,7 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
       uint4 kf[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        kf[j] = *reinterpret_cast<const uint4*>(kt + (16 * st + n) * kKStride + 32 * j + 8 * g);
+        kf[j] = *reinterpret_cast<const uint4*>(kt + (16 * st + n) * kKStride + 8 * ((4 * j + g) ^ n));
 #pragma unroll
       for (int rt = 0; rt < kPfRt; ++rt) {
         // (a row tile with no valid row computes rows that are never written)
@@ -1626,7 +1630,10 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     __builtin_amdgcn_s_setprio(1);
 #endif
     // V^T fragments of half the dims at a time are read before their MFMAs,
-    // so the transposing reads overlap instead of waiting one by one
+    // so the transposing reads overlap instead of waiting one by one.  Lane
+    // (n, g) reads keys 4 g + n / 4 (+ 16), dims 16 dt + 4 (n % 4), at their
+    // swizzled place (the transposing read as in vt_frag).
+    const int vrow = 4 * g + (n >> 2);
 #pragma unroll
     for (int pp = 0; pp < kSt / 2; ++pp) {
 #pragma unroll
@@ -1634,9 +1641,11 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
         bf16x8_t va[kPfDtBatch];
 #pragma unroll
         for (int d = 0; d < kPfDtBatch; ++d) {
-          const short4_t v0 = vt_frag<kPfVStride>(vt + (32 * pp) * kPfVStride, n, g, dh + d);
-          const short4_t v1 = vt_frag<kPfVStride>(vt + (32 * pp + 16) * kPfVStride, n, g, dh + d);
-          va[d] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+          const short4_t x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_short4_t*)(vt + (32 * pp + vrow) * kPfVStride + 16 * ((dh + d) ^ (vrow & 7)) + 4 * (n & 3)));
+          const short4_t x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_short4_t*)(vt + (32 * pp + 16 + vrow) * kPfVStride + 16 * ((dh + d) ^ (vrow & 7)) + 4 * (n & 3)));
+          va[d] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
         }
 #pragma unroll
         for (int d = 0; d < kPfDtBatch; ++d)
@@ -1652,27 +1661,48 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
   };
 
   if (t1 > t0) {
+    using buf0 = std::integral_constant<int, 0>;
+    using buf1 = std::integral_constant<int, 1>;
     fetch_ids(t0);
-    load(t0);
+    load(t0, buf0{});
     fetch_ids(t0 + 1);
-    store(0);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
-    // tiles below the wave's smallest row limit need no mask; the two runs
-    // together take every tile, so all waves pass the same barriers
+    // Tiles below the wave's smallest row limit need no mask; the two runs
+    // together take every tile, so all waves pass the same barriers.  The
+    // buffer of each step is a compile-time choice (separate LDS arrays), so
+    // the compiler sees that a step's reads and the next tile's direct loads
+    // touch different memory and holds no read back for those loads; with a
+    // buffer index chosen at run time it waits for the loads before each read.
+    // The loop keeps one copy of each buffer's step (unrolled copies cost more
+    // in instruction fetch than they save).
     const int t_um = max(t0, min(t1, (wlim_lo + 1) / kPfKeys));
-    auto step = [&](int t, auto mask_tag) {
-      const int buf = (t - t0) & 1;
+    auto step = [&](int t, auto buf_tag, auto mask_tag) {
+      constexpr int B = decltype(buf_tag)::value;
+      using other = std::integral_constant<int, B ^ 1>;
       if (t + 1 < t1) {
-        load(t + 1);
+        load(t + 1, other{});
         fetch_ids(t + 2);
       }
-      compute(t, buf, mask_tag);
-      if (t + 1 < t1) store(buf ^ 1);
+      compute(t, buf_tag, mask_tag);
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
       __syncthreads();
     };
-    int t = t0;
-    for (; t < t_um; ++t) step(t, std::false_type{});
-    for (; t < t1; ++t) step(t, std::true_type{});
+    auto run = [&](int t, int t_end, auto mask_tag) {
+      bool odd = ((t - t0) & 1) != 0;
+#pragma clang loop unroll(disable)
+      while (t < t_end) {
+        if (!odd) {
+          step(t, buf0{}, mask_tag);
+          if (++t >= t_end) break;
+        }
+        step(t, buf1{}, mask_tag);
+        ++t;
+        odd = false;
+      }
+    };
+    run(t0, t_um, std::false_type{});
+    run(t_um, t1, std::true_type{});
   }
 
 #pragma unroll
@@ -1702,28 +1732,33 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
 template <bool ONE_BLOCK, bool FUSED>
 __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(AIA_PF_WPE, AIA_PF_WPE)))
 void gqa_prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kPfKeys * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vs[2][kPfKeys * kPfVStride];
-  gqa_prefill_body<ONE_BLOCK, FUSED>(a, blockIdx.x, ks, vs);
+  __shared__ __attribute__((aligned(16))) uint16_t k0[kPfKeys * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t k1[kPfKeys * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t v0[kPfKeys * kPfVStride];
+  __shared__ __attribute__((aligned(16))) uint16_t v1[kPfKeys * kPfVStride];
+  gqa_prefill_body<ONE_BLOCK, FUSED>(a, blockIdx.x, k0, k1, v0, v1);
 }
 
 // Mixed steps (prefill items beside split-K decode ranges) in one grid, for
 // kPfWaves-wave decode groups (Hkv = kPfWaves).  Launched separately, the
-// two kernels cannot share a CU: VGPRs are allocated in blocks of 8, so one
-// prefill wave (232) plus two decode waves (2 x 144) exceed a SIMD's 512, and
-// the second kernel waits for the first to drain.  In one grid every
+// two kernels barely share a CU: one prefill wave (212-232 VGPRs, allocated
+// in blocks of 8) plus two decode waves (2 x 144) fill or exceed a SIMD's
+// 512, so the second kernel mostly waits for the first to drain.  In one grid every
 // work-group gets the prefill budget and does one job or the other, so the
 // compute-bound prefill runs while the HBM-bound decode streams beside it.
 #ifndef AIA_MIXED
 #define AIA_MIXED 1
 #endif
-static_assert(kPfWaves * kTile * kVStride <= 2 * kPfKeys * kKStride,
-              "decode V^T staging must fit the prefill K buffers");
+// The decode role stages its V^T tiles in the first K buffer.
+constexpr int kMixedK0 = kPfWaves * kTile * kVStride > kPfKeys * kKStride
+                             ? kPfWaves * kTile * kVStride : kPfKeys * kKStride;
 template <bool ONE_BLOCK, bool FUSED>
 __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(AIA_PF_WPE, AIA_PF_WPE)))
 void gqa_mixed_kernel(AttnArgs a, PrefillArgs pa, int npf) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kPfKeys * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vs[2][kPfKeys * kPfVStride];
+  __shared__ __attribute__((aligned(16))) uint16_t k0[kMixedK0];
+  __shared__ __attribute__((aligned(16))) uint16_t k1[kPfKeys * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t v0[kPfKeys * kPfVStride];
+  __shared__ __attribute__((aligned(16))) uint16_t v1[kPfKeys * kPfVStride];
   // Prefill units take the first npf block ids and the decode ranges the
   // rest: the units are dealt out first, one or two per CU, and the ranges
   // fill the remaining slots and every slot a unit frees.  (Alternating the
@@ -1733,10 +1768,10 @@ void gqa_mixed_kernel(AttnArgs a, PrefillArgs pa, int npf) {
   const bool prefill = b < npf;
   const int idx = prefill ? b : b - npf;
   if (prefill)
-    gqa_prefill_body<ONE_BLOCK, FUSED>(pa, idx, ks, vs);
+    gqa_prefill_body<ONE_BLOCK, FUSED>(pa, idx, k0, k1, v0, v1);
   else
     gqa_attn_body<kPfWaves, 1, kHeadDim, false>(a, idx,
-                                         reinterpret_cast<uint16_t(*)[kTile * kVStride]>(&ks[0][0]));
+                                         reinterpret_cast<uint16_t(*)[kTile * kVStride]>(&k0[0]));
 }
 
 struct MergeArgs {

@@ -1329,7 +1329,6 @@ struct PrefillArgs {
 // instead (see the loader).
 constexpr int kKStride = kHeadDim;
 constexpr int kPfVStride = kHeadDim;
-constexpr int kPfDtBatch = 4;      // V^T fragments read ahead of their MFMAs
 // Wave priority raised around each MFMA block, so a wave entering its MFMA
 // phase issues ahead of the co-resident wave, which runs its softmax VALU
 // meanwhile (measured about 3% faster on the configs[1] prefill chunks).
@@ -1339,6 +1338,29 @@ constexpr int kPfDtBatch = 4;      // V^T fragments read ahead of their MFMAs
 #ifndef AIA_PF_LAZY
 #define AIA_PF_LAZY 8.0f
 #endif
+// Instruction order of the QK^T and PV blocks (sched_group_barrier): LDS
+// reads kept kPfQkAhead 16-key sub-tiles (QK^T) and kPfPvAhead V^T fragments
+// (PV) ahead of their MFMAs.  Left to itself the scheduler reuses one V^T
+// fragment's registers and waits for each batch of reads before two MFMAs.
+// (configs[1] prefill chunks, µs per call: 48.2 unordered; QK 2 / PV 4 46.0;
+// PV 2, 6 or 8 and QK 3 or 4 the same within 0.1; QK 1 46.9; PV 16 46.6.)
+constexpr int kPfQkAhead = 2;
+constexpr int kPfPvAhead = 4;
+constexpr int kSgMfma = 0x008, kSgDsRead = 0x100;    // sched_group_barrier masks
+// One 16-byte direct load from global memory into LDS at byte lds + 16 lane
+// (lds wave-uniform).  Issued as inline assembly on purpose: the compiler's
+// counter-wait pass tracks the builtin form as an outstanding LDS access and
+// then waits for the LDS counter to drain completely (lgkmcnt(0)) before
+// every LDS read, which exposes each read's full latency (48.2 against 49.3
+// µs per call, and it defeats the read-ahead order above: 47.6-47.9 against
+// 46.0).  Completion is explicit instead: every step waits vmcnt(0) before its
+// barrier.  Loads the compiler does not see can only make its own vmcnt waits
+// stricter, never too weak (the counter retires in order).
+__device__ __forceinline__ void lds_load16(const uint16_t* src, uint16_t* lds) {
+  const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(la), "v"(src) : "memory", "m0");
+}
 constexpr float kLazyLog2 = AIA_PF_LAZY;              // max growth (log2) before a rescale
 
 // Prefill attention: one work-group per (prefill item, kv head).  An item is
@@ -1502,10 +1524,8 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
       vp = fresh ? vnb + tok * a.vn_ts : vp;
     }
     const int rb = (kLdKeys * i + 4 * wid) * kHeadDim;     // the wave's first row
-    __builtin_amdgcn_global_load_lds(kp + 8 * (lc ^ lkey),
-                                     (__attribute__((address_space(3))) void*)(kdst + rb), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(vp + 8 * (lc ^ (2 * (lkey & 7))),
-                                     (__attribute__((address_space(3))) void*)(vdst + rb), 16, 0, 0);
+    lds_load16(kp + 8 * (lc ^ lkey), kdst + rb);
+    lds_load16(vp + 8 * (lc ^ (2 * (lkey & 7))), vdst + rb);
   };
   auto load = [&](int t, auto buf_tag) {
     constexpr int B = decltype(buf_tag)::value;
@@ -1566,6 +1586,12 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[rt][st] = qk_step(kf[j], qf[rt][j], acc[rt][st]);
       }
+    }
+    __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4 * kPfQkAhead, 0);
+#pragma unroll
+    for (int st = 0; st < kSt; ++st) {
+      __builtin_amdgcn_sched_group_barrier(kSgMfma, 4 * kPfRt, 0);
+      if (st + kPfQkAhead < kSt) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4, 0);
     }
 #if AIA_PF_PRIO
     __builtin_amdgcn_s_setprio(0);
@@ -1629,31 +1655,28 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
 #if AIA_PF_PRIO
     __builtin_amdgcn_s_setprio(1);
 #endif
-    // V^T fragments of half the dims at a time are read before their MFMAs,
-    // so the transposing reads overlap instead of waiting one by one.  Lane
-    // (n, g) reads keys 4 g + n / 4 (+ 16), dims 16 dt + 4 (n % 4), at their
-    // swizzled place (the transposing read as in vt_frag).
+    // PV over V^T fragments f = (32-key pair pp, 16 dims dt), read kPfPvAhead
+    // fragments ahead of their MFMAs.  Lane (n, g) reads keys 4 g + n / 4
+    // (+ 16), dims 16 dt + 4 (n % 4), at their swizzled place (the
+    // transposing read as in vt_frag).
     const int vrow = 4 * g + (n >> 2);
 #pragma unroll
-    for (int pp = 0; pp < kSt / 2; ++pp) {
+    for (int f = 0; f < kSt / 2 * 8; ++f) {
+      const int pp = f >> 3, dt = f & 7;
+      const short4_t x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_short4_t*)(vt + (32 * pp + vrow) * kPfVStride + 16 * (dt ^ (vrow & 7)) + 4 * (n & 3)));
+      const short4_t x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_short4_t*)(vt + (32 * pp + 16 + vrow) * kPfVStride + 16 * (dt ^ (vrow & 7)) + 4 * (n & 3)));
+      const bf16x8_t va = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-      for (int dh = 0; dh < 8; dh += kPfDtBatch) {
-        bf16x8_t va[kPfDtBatch];
+      for (int rt = 0; rt < kPfRt; ++rt)
+        o[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, as_b8(pb[rt][pp]), o[rt][dt], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2 * kPfPvAhead, 0);
 #pragma unroll
-        for (int d = 0; d < kPfDtBatch; ++d) {
-          const short4_t x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_short4_t*)(vt + (32 * pp + vrow) * kPfVStride + 16 * ((dh + d) ^ (vrow & 7)) + 4 * (n & 3)));
-          const short4_t x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_short4_t*)(vt + (32 * pp + 16 + vrow) * kPfVStride + 16 * ((dh + d) ^ (vrow & 7)) + 4 * (n & 3)));
-          va[d] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
-        }
-#pragma unroll
-        for (int d = 0; d < kPfDtBatch; ++d)
-#pragma unroll
-          for (int rt = 0; rt < kPfRt; ++rt)
-            o[rt][dh + d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[d], as_b8(pb[rt][pp]),
-                                                                     o[rt][dh + d], 0, 0, 0);
-      }
+    for (int f = 0; f < kSt / 2 * 8; ++f) {
+      __builtin_amdgcn_sched_group_barrier(kSgMfma, kPfRt, 0);
+      if (f + kPfPvAhead < kSt / 2 * 8) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
     }
 #if AIA_PF_PRIO
     __builtin_amdgcn_s_setprio(0);

@@ -1329,12 +1329,6 @@ struct PrefillArgs {
 // instead (see the loader).
 constexpr int kKStride = kHeadDim;
 constexpr int kPfVStride = kHeadDim;
-// Wave priority raised around each MFMA block, so a wave entering its MFMA
-// phase issues ahead of the co-resident wave, which runs its softmax VALU
-// meanwhile (measured about 3% faster on the configs[1] prefill chunks).
-#ifndef AIA_PF_PRIO
-#define AIA_PF_PRIO 1
-#endif
 #ifndef AIA_PF_LAZY
 #define AIA_PF_LAZY 8.0f
 #endif
@@ -1490,12 +1484,15 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
   // c of key r sits at c ^ (r % 16) and V chunk c at c ^ 2 (r % 8), so the K
   // fragment reads (16 keys, one chunk each) and the V^T transposing reads (8
   // keys, 32 bytes each) hit distinct banks without padded rows.
-  // Block ids are fetched one tile ahead (their loads are in flight during a
-  // tile's math), so a tile's loads never wait on a table lookup.  When the
-  // block size is a multiple of the tile, a tile lies in one block: its id is
-  // one scalar load and a key's address one multiply-add.  Keys past the last
-  // visible one re-read it (never a slot that may hold stale bytes); keys at
-  // this step's new positions come from the new rows.
+  // When the block size is a multiple of the tile, a tile lies in one block
+  // and a key's address is one multiply-add: lane l of every wave holds the
+  // block id of tile tb + l, fetched 64 tiles at a time, and a tile takes its
+  // id with one readlane.  (Fetched per tile, the id's load was waited for at
+  // once to move it into a scalar register: a memory round trip every tile.)
+  // Other block sizes fetch each key's id one tile ahead, so those loads are
+  // in flight during a tile's math.  Keys past the last visible one re-read
+  // it (never a slot that may hold stale bytes); keys at this step's new
+  // positions come from the new rows.
   const int lkey = tid >> 4, lc = tid & 15;
   const int64_t kvoff = (int64_t)kvh * kHeadDim;
   const uint16_t* kcb = a.kc + kvoff;
@@ -1505,13 +1502,19 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
   constexpr int kLdKeys = kPfWaves * 4;                // keys per loader round
   constexpr int kLdRounds = kPfKeys / kLdKeys;
   int bid[kLdRounds];
+  int tb = -64, vbid = 0;
   auto fetch_ids = [&](int t) {
-    if (ONE_BLOCK) {
-      bid[0] = btrow[min(t * kPfKeys, kend - 1) / a.bs];
-    } else {
+    if (!ONE_BLOCK) {
 #pragma unroll
       for (int i = 0; i < kLdRounds; ++i) bid[i] = btrow[min(t * kPfKeys + kLdKeys * i + lkey, kend - 1) / a.bs];
     }
+  };
+  auto tile_bid = [&](int t) {
+    if (t - tb >= 64) {
+      tb = t;
+      vbid = btrow[min((t + lane) * kPfKeys, kend - 1) / a.bs];
+    }
+    return __builtin_amdgcn_readlane(vbid, t - tb);
   };
   auto load_row = [&](int i, int p, int slot, uint16_t* kdst, uint16_t* vdst) {
     const int64_t e = (int64_t)slot * row_elems;
@@ -1533,7 +1536,7 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     uint16_t* vdst = B ? v1 : v0;
     const int kb = t * kPfKeys;
     if (ONE_BLOCK) {
-      const int blk = min(max(bid[0], 0), a.nb - 1);
+      const int blk = min(max(tile_bid(t), 0), a.nb - 1);
       const int slot0 = blk * a.bs + kb % a.bs;
       const int last = kend - 1 - kb;
 #pragma unroll
@@ -1561,18 +1564,24 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     lsum[rt] = 0.f;
   }
 
-  auto compute = [&](int t, auto buf_tag, auto mask_tag) {
+  // issue_next() issues the next tile's loads after the QK^T MFMAs, so that
+  // the load addresses and issue overlap the MFMAs' execution: 0-1% faster
+  // than issuing them first.  (A raised wave priority around each MFMA block,
+  // 3% faster with register-staged loads, made this order 1-2% slower, and
+  // either order is as fast without it, so no priority is set.)
+  auto compute = [&](int t, auto buf_tag, auto mask_tag, auto issue_next) {
     constexpr bool MASK = decltype(mask_tag)::value;
     constexpr int B = decltype(buf_tag)::value;
     const int kbase = t * kPfKeys;
-    if (MASK && kbase > wlim_hi) return;         // no row of this wave sees these keys
+    if (MASK && kbase > wlim_hi) {               // no row of this wave sees these keys
+      issue_next();
+      return;
+    }
     const uint16_t* kt = B ? k1 : k0;
     const uint16_t* vt = B ? v1 : v0;
     constexpr int kSt = kPfKeys / 16;      // 16-key sub-tiles
     float4_t acc[kPfRt][kSt];
-#if AIA_PF_PRIO
-    __builtin_amdgcn_s_setprio(1);
-#endif
+    __builtin_amdgcn_sched_barrier(0);     // the block below is scheduled on its own
 #pragma unroll
     for (int st = 0; st < kSt; ++st) {
       uint4 kf[4];
@@ -1593,9 +1602,8 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
       __builtin_amdgcn_sched_group_barrier(kSgMfma, 4 * kPfRt, 0);
       if (st + kPfQkAhead < kSt) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4, 0);
     }
-#if AIA_PF_PRIO
-    __builtin_amdgcn_s_setprio(0);
-#endif
+    __builtin_amdgcn_sched_barrier(0);
+    issue_next();
     uint4 pb[kPfRt][kSt / 2];
 #pragma unroll
     for (int rt = 0; rt < kPfRt; ++rt) {
@@ -1652,9 +1660,7 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
         pb[rt][pp].w = aia::pack_bf16x2(p[2 * pp + 1][2], p[2 * pp + 1][3]);
       }
     }
-#if AIA_PF_PRIO
-    __builtin_amdgcn_s_setprio(1);
-#endif
+    __builtin_amdgcn_sched_barrier(0);     // the block below is scheduled on its own
     // PV over V^T fragments f = (32-key pair pp, 16 dims dt), read kPfPvAhead
     // fragments ahead of their MFMAs.  Lane (n, g) reads keys 4 g + n / 4
     // (+ 16), dims 16 dt + 4 (n % 4), at their swizzled place (the
@@ -1678,9 +1684,7 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
       __builtin_amdgcn_sched_group_barrier(kSgMfma, kPfRt, 0);
       if (f + kPfPvAhead < kSt / 2 * 8) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
     }
-#if AIA_PF_PRIO
-    __builtin_amdgcn_s_setprio(0);
-#endif
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   if (t1 > t0) {
@@ -1703,11 +1707,13 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     auto step = [&](int t, auto buf_tag, auto mask_tag) {
       constexpr int B = decltype(buf_tag)::value;
       using other = std::integral_constant<int, B ^ 1>;
-      if (t + 1 < t1) {
-        load(t + 1, other{});
-        fetch_ids(t + 2);
-      }
-      compute(t, buf_tag, mask_tag);
+      auto issue_next = [&]() {
+        if (t + 1 < t1) {
+          load(t + 1, other{});
+          fetch_ids(t + 2);
+        }
+      };
+      compute(t, buf_tag, mask_tag, issue_next);
       __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
       __syncthreads();
     };

@@ -306,6 +306,20 @@ def test_prefill_route(lqs, lks, hq, hkv, bs):
     check(step)
 
 
+def test_prefill_whole_items_past_64_tiles():
+    """63 items of 128 rows x 8 kv heads = 504 work-groups fit one round, so
+    no item is cut and each unit walks all of its 65-72 key tiles: the block
+    ids (one per 64-key tile, fetched 64 tiles at a time) are fetched again
+    past tile 64.  Against the oracle."""
+    step = workloads.make_gqa_step(lqs=[504], lks=[4600], num_q_heads=128, num_kv_heads=8,
+                                   block_size=128, seed=59)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, 128, 8, 128, 128)
+    torch.cuda.synchronize()
+    assert plan.workspace[:64].cpu().view(torch.int32)[6].item() == 63   # units: whole items
+    check(step)
+
+
 def test_prefill_route_repeated_and_deterministic():
     """The prefill kernel has no split: repeated calls on one plan are
     bit-identical, with a decode batch beside it on split-K."""

@@ -420,7 +420,13 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       const int2 ex2 = block_exclusive_scan2(make_int2(k, k > 1 ? 1 : 0), wave_sums2, &tot2);
       const int u = ucarry + ex2.x, mm = mcarry2 + ex2.y;
       if (f < pcarry && u + k <= pf_unit_cap && mm + (k > 1) <= pf_mrg_cap) {
-        if (k > 1) pf_mrg[mm] = make_int4(b, r0, u, k);
+        if (k > 1) {
+          // {first query token, first row, first unit, units | item rows << 16}
+          const int c0 = req_lds ? cuv[b] : cu_q[b];
+          const int c1 = req_lds ? cuv[b + 1] : cu_q[b + 1];
+          const int rows = min(kPfRows, (c1 - c0) * g.group - r0);
+          pf_mrg[mm] = make_int4(c0, r0, u, k | (rows << 16));
+        }
         for (int j = 0; j < k; ++j)
           pf_units[u + j] = make_int4(b, r0, (int)((int64_t)j * nt / k), (int)((int64_t)(j + 1) * nt / k));
       }
@@ -1319,7 +1325,7 @@ struct PrefillArgs {
   const int4* units;         // {request, first row, first tile, end tile}
   const int4* dealt;         // work-group b: its unit record, then {unit, kv head}
   const int32_t* hdr;
-  float* part_o;             // partial row blocks of chunked items
+  uint16_t* part_o;          // partial row blocks of chunked items (fp16, scaled per row)
   float2* part_ml;
   int32_t part_units;        // units the partial buffer holds
 };
@@ -1737,13 +1743,32 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
 #pragma unroll
   for (int rt = 0; rt < kPfRt; ++rt) {
     lsum[rt] = aia::group4_sum(lsum[rt]);
-    if (!rv[rt]) continue;
-    if (!whole) {   // partial (O, m, l) of the unit's rows
-      const int64_t prow = ((int64_t)unit * a.hkv + kvh) * kPfRows + (wid * kPfRt + rt) * kRows + n;
-      float* pp = a.part_o + prow * kHeadDim;
+    // a unit that does not cover all of its item's keys writes a partial:
+    // y = O / c in fp16, c = the row's largest |O| (1 for an all-zero row),
+    // with (m + log2 c, l / c) in place of (m, l).  The merge's log-sum-exp
+    // rule then folds c back exactly (its weights are exp2(m - M)), and the
+    // partials take half the bytes of fp32 ones.
+    float cmax = 0.f;
+    if (!whole) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * g) = o[rt][dt];
-      if (g == 0) a.part_ml[prow] = make_float2(m[rt], lsum[rt]);
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) cmax = fmaxf(cmax, fabsf(o[rt][dt][v]));
+      cmax = aia::group4_max(cmax);
+    }
+    if (!rv[rt]) continue;
+    if (!whole) {
+      const float c = cmax > 0.f ? cmax : 1.f, ic = 1.f / c;
+      const int64_t prow = ((int64_t)unit * a.hkv + kvh) * kPfRows + (wid * kPfRt + rt) * kRows + n;
+      uint16_t* pp = a.part_o + prow * kHeadDim;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        uint2 hv;
+        hv.x = pack_f16x2(o[rt][dt][0] * ic, o[rt][dt][1] * ic);
+        hv.y = pack_f16x2(o[rt][dt][2] * ic, o[rt][dt][3] * ic);
+        *reinterpret_cast<uint2*>(pp + 16 * dt + 4 * g) = hv;
+      }
+      if (g == 0) a.part_ml[prow] = make_float2(m[rt] + __log2f(c), lsum[rt] * ic);
       continue;
     }
     const float inv = lsum[rt] > 0.f ? 1.f / lsum[rt] : 0.f;
@@ -1815,11 +1840,12 @@ struct MergeArgs {
   int64_t mrg_cap;
   int32_t part_f16;          // split-K partials stored as fp16 scaled by part_sc
   const float* part_sc;
-  // prefill chunk merges: records {request, first row, first unit, units}
+  // prefill chunk merges: records {first query token, first row, first
+  // unit, units | item rows << 16}
   const int4* pf_mrg;
-  const float* pf_o;
+  int64_t pf_items_cap;     // work items the records can hold
+  const uint16_t* pf_o;
   const float2* pf_ml;
-  const int32_t* cu_q;
 };
 
 // Merge of split partials.  The planner lists the merge work: one record per
@@ -1840,6 +1866,16 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int seg_rows = kRows * a.rb;
   const int qb = kRows / a.hb;
   const int64_t pstride = (int64_t)a.nw * seg_rows;
+  // the first prefill record and the count go out with the first split-K
+  // record, so a prefill work-group's chain is record, then partials
+  constexpr int kSlices = kPfRows / 16;
+  const int per_rec = a.hkv * kSlices;
+  int4 pr0 = make_int4(0, 0, 0, 0);
+  int npm = 0;
+  if (a.pf_mrg) {
+    if (blockIdx.x < a.pf_items_cap) pr0 = a.pf_mrg[blockIdx.x / per_rec];
+    npm = a.hdr[7];
+  }
   for (int64_t item = blockIdx.x; item < a.mrg_cap; item += gridDim.x) {
     const int4 m0 = *reinterpret_cast<const int4*>(a.mrg + item * kMrgInts);
     const int4 m1 = *reinterpret_cast<const int4*>(a.mrg + item * kMrgInts + 4);
@@ -1933,35 +1969,47 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   }
 
   // Prefill chunk merges, one work item per (record, kv head, 16 rows):
-  // thread (row r, 8 dims) folds the record's partials with the same rule.
-  const int npm = a.pf_mrg ? a.hdr[7] : 0;
-  constexpr int kSlices = kPfRows / 16;
-  const int64_t pitems = (int64_t)npm * a.hkv * kSlices;
+  // thread (row r, 8 dims) folds the record's fp16 partials (scaled per row,
+  // see the prefill kernel) with the same rule, 8 at a time so a batch costs
+  // one round trip.
+  const int64_t pitems = (int64_t)npm * per_rec;
   for (int64_t it = blockIdx.x; it < pitems; it += gridDim.x) {
-    const int rec = (int)(it / (a.hkv * kSlices));
-    const int rem = (int)(it - (int64_t)rec * a.hkv * kSlices);
+    const int rec = (int)(it / per_rec);
+    const int rem = (int)(it - (int64_t)rec * per_rec);
     const int kvh = rem / kSlices, slice = rem - kvh * kSlices;
-    const int4 r = a.pf_mrg[rec];
-    const int b = r.x, row0 = r.y, u0 = r.z, k = r.w;
-    const int q_begin = a.cu_q[b], lq = a.cu_q[b + 1] - q_begin;
+    const int4 r = it == blockIdx.x ? pr0 : a.pf_mrg[rec];
+    const int q_begin = r.x, row0 = r.y, u0 = r.z, k = r.w & 0xffff, rows = r.w >> 16;
     const int rl = slice * 16 + (threadIdx.x >> 4), c = (threadIdx.x & 15) * 8;
     const int row = row0 + rl;
-    if (row >= lq * a.group) continue;
+    if (rl >= rows) continue;
     float4 acc[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
     float mx = -1e30f, ls = 0.f;
-    for (int j = 0; j < k; ++j) {
-      const int64_t prow = ((int64_t)(u0 + j) * a.hkv + kvh) * kPfRows + rl;
-      const float2 ml = a.pf_ml[prow];
-      const float4* src = reinterpret_cast<const float4*>(a.pf_o + prow * kHeadDim + c);
-      const float4 x0 = src[0], x1 = src[1];
-      const float mn = fmaxf(mx, ml.x);
-      const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
-      ls = ls * sa + ml.y * sb;
-      acc[0].x = acc[0].x * sa + x0.x * sb; acc[0].y = acc[0].y * sa + x0.y * sb;
-      acc[0].z = acc[0].z * sa + x0.z * sb; acc[0].w = acc[0].w * sa + x0.w * sb;
-      acc[1].x = acc[1].x * sa + x1.x * sb; acc[1].y = acc[1].y * sa + x1.y * sb;
-      acc[1].z = acc[1].z * sa + x1.z * sb; acc[1].w = acc[1].w * sa + x1.w * sb;
-      mx = mn;
+    for (int j0 = 0; j0 < k; j0 += 8) {
+      float2 ml[8];
+      float4 x[8][2];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j0 + j >= k) break;                    // k is the same for the whole work-group
+        const int64_t prow = ((int64_t)(u0 + j0 + j) * a.hkv + kvh) * kPfRows + rl;
+        ml[j] = a.pf_ml[prow];
+        const uint4 h = *reinterpret_cast<const uint4*>(a.pf_o + prow * kHeadDim + c);
+        const half2_t h0 = __builtin_bit_cast(half2_t, h.x), h1 = __builtin_bit_cast(half2_t, h.y);
+        const half2_t h2 = __builtin_bit_cast(half2_t, h.z), h3 = __builtin_bit_cast(half2_t, h.w);
+        x[j][0] = make_float4((float)h0[0], (float)h0[1], (float)h1[0], (float)h1[1]);
+        x[j][1] = make_float4((float)h2[0], (float)h2[1], (float)h3[0], (float)h3[1]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j0 + j >= k) break;
+        const float mn = fmaxf(mx, ml[j].x);
+        const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml[j].x - mn);
+        ls = ls * sa + ml[j].y * sb;
+        acc[0].x = acc[0].x * sa + x[j][0].x * sb; acc[0].y = acc[0].y * sa + x[j][0].y * sb;
+        acc[0].z = acc[0].z * sa + x[j][0].z * sb; acc[0].w = acc[0].w * sa + x[j][0].w * sb;
+        acc[1].x = acc[1].x * sa + x[j][1].x * sb; acc[1].y = acc[1].y * sa + x[j][1].y * sb;
+        acc[1].z = acc[1].z * sa + x[j][1].z * sb; acc[1].w = acc[1].w * sa + x[j][1].w * sb;
+        mx = mn;
+      }
     }
     const float inv = ls > 0.f ? 1.f / ls : 0.f;
     const int tok = row / a.group, head = kvh * a.group + (row - tok * a.group);
@@ -2282,7 +2330,7 @@ void mla_attn_kernel(MlaArgs a) {
 int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32_t dv,
                  const float* part_o,
                  const float2* part_ml, const int32_t* seg, uint16_t* out, int64_t o_ts,
-                 int64_t o_hs, const int32_t* cu_q, hipStream_t s) {
+                 int64_t o_hs, hipStream_t s) {
   MergeArgs mg;
   mg.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
   mg.seg = seg; mg.part_o = part_o; mg.part_ml = part_ml;
@@ -2293,9 +2341,9 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
   mg.part_sc = reinterpret_cast<const float*>(ws + L.part_sc);
   const bool pf = L.pf_mrg_cap > 0;
   mg.pf_mrg = pf ? reinterpret_cast<const int4*>(ws + L.pfm) : nullptr;
-  mg.pf_o = reinterpret_cast<const float*>(ws + L.pf_o);
+  mg.pf_items_cap = L.pf_mrg_cap * g.hkv * (kPfRows / 16);
+  mg.pf_o = reinterpret_cast<const uint16_t*>(ws + L.pf_o);
   mg.pf_ml = reinterpret_cast<const float2*>(ws + L.pf_ml);
-  mg.cu_q = cu_q;
   const int64_t pitems = pf ? L.pf_mrg_cap * g.hkv * (kPfRows / 16) : 0;
   const int64_t items = L.mrg_cap > pitems ? L.mrg_cap : pitems;
   int64_t mgrid = items < 2048 ? items : 2048;
@@ -2442,7 +2490,7 @@ extern "C" int aia_paged_attention_gqa(
     pa.units = reinterpret_cast<const int4*>(ws + L.pf);
     pa.dealt = reinterpret_cast<const int4*>(ws + L.pfw);
     pa.hdr = a.hdr;
-    pa.part_o = reinterpret_cast<float*>(ws + L.pf_o);
+    pa.part_o = reinterpret_cast<uint16_t*>(ws + L.pf_o);
     pa.part_ml = reinterpret_cast<float2*>(ws + L.pf_ml);
     pa.part_units = (int32_t)(L.pf_slots / g.hkv);
   }
@@ -2488,7 +2536,7 @@ extern "C" int aia_paged_attention_gqa(
   }
   if (a.fused_merge) return AIA_OK;
   return launch_merge(ws, L, g, g.nw, head_dim, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
-                      cu_seqlens_q, s);
+                      s);
 }
 
 extern "C" int aia_paged_attention_mla(
@@ -2546,7 +2594,7 @@ extern "C" int aia_paged_attention_mla(
   else mla_attn_kernel<1><<<waves, 256, 0, s>>>(a);
   if (int rc = check_hip(hipGetLastError(), "mla_attn_kernel launch")) return rc;
   return launch_merge(ws, L, g, 1, kMlaV, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
-                      cu_seqlens_q, s);
+                      s);
 }
 
 // ------------------------------------------------- allocation-free variant

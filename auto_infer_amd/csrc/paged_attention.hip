@@ -101,12 +101,16 @@ constexpr int kPfWaves = AIA_PF_WAVES;       // waves per prefill work-group
 constexpr int kPfRt = AIA_PF_RT;             // 16-row MFMA tiles per wave
 constexpr int kPfRows = 16 * kPfRt * kPfWaves;   // rows per prefill work item
 constexpr int kPfKeys = AIA_PF_KEYS;         // keys per staged K/V tile (32 or 64)
-// Items alone fill the chip when items x kv heads reach kPfTargetWgs (two
-// resident work-groups per CU); below that, each item's key tiles are cut
-// into chunks of at least kPfMinChunk tiles, sized so all units still fit in
-// one round (fp32 partials, merged with the split-K partials' rule).
+// Items alone fill the chip when items x kv heads reach kPfTargetWgs (a
+// little under two resident work-groups per CU); below that, each item's key
+// tiles are cut into chunks of at least kPfMinChunk tiles, sized so all units
+// still fit in one round (fp16 partials scaled per row, merged with the
+// split-K partials' rule).  448 rather than 512: fewer, longer chunks write
+// fewer partials, and the CUs left with one work-group take the largest
+// units (configs[1] prefill chunks, us per call: 43.1 at 448 or 416, 44.6 at
+// 512, 44.1-44.5 at 384, 49.6-49.9 at 256-320; 416 is slower at 32K keys).
 #ifndef AIA_PF_TARGET
-#define AIA_PF_TARGET 512
+#define AIA_PF_TARGET 448
 #endif
 constexpr int kPfTargetWgs = AIA_PF_TARGET;
 constexpr int kPfMinChunk = 8;

@@ -57,7 +57,7 @@ def test_config2_mixed_prefill_decode():
 def test_config2_prefill_chunks_alone_dealt_by_size(fused):
     """configs[1]'s three 512-token chunks alone: every request goes to the
     prefill units, the planner takes the least chunk size whose units fit
-    one round and deals the 500 work-groups by size in CU pairs (hdr[9]).
+    one round and deals the work-groups by size in CU pairs (hdr[9]).
     Checked against the oracle, with and without the fused KV write."""
     full = workloads.config2_mixed(seed=0)
     sub, _ = workloads.subset(full, [0, 1, 2])

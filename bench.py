@@ -598,11 +598,14 @@ def main():
 
     def layer_steps(start, n):
         """n layer-steps from layer-step index `start`: the planner at every
-        model-step boundary (its plan serves the L layers), then each layer's
-        attention with the KV write of the 16 new rows fused into it."""
+        model-step boundary (layer 0; its plan serves the L layers), then each
+        layer's attention with the KV write of the 16 new rows fused into it.
+        A window that starts mid-step uses the plan its step's layer 0 made
+        (the warmup's, or the previous replay's last boundary), so the planner
+        runs exactly once per L layer-steps of the timed region."""
         for i in range(start, start + n):
             layer = i % L
-            if layer == 0 or i == start:
+            if layer == 0:
                 plan.replan()
             ops.paged_attention_gqa(q, kcs[layer], vcs[layer], plan, step.scale, out=out,
                                     key_new=k_new, value_new=v_new)

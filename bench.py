@@ -299,7 +299,7 @@ def other_configs(stream, only=None):
     with enough rotating caches to exceed the Infinity Cache, and the fused
     kernels either side of the path.  `only` selects one entry (its key:
     configs[1] .. configs[4], configs[1]_prefill, configs[1]_decode,
-    pre_attention, mla_pre_attention, mla_v_up, mtp_compaction)."""
+    prefill_long, pre_attention, mla_pre_attention, mla_v_up, mtp_compaction)."""
     import time as _time
     import numpy as np
     from auto_infer_amd import ops, packing, workloads
@@ -365,6 +365,14 @@ def other_configs(stream, only=None):
             gqa("configs[1]_decode_only",
                 on_device(workloads.subset(full, list(range(3, 515)))[0]), 1)
         del full
+    if want("prefill_long"):
+        # not a BASELINE config: one 512-token chunk behind a 32K-key context
+        # with configs[1]'s heads, where the prefill units run long enough
+        # for their ramp and tail not to dominate
+        note("prefill chunk at 32K keys")
+        gqa("prefill_512_tokens_at_32K_keys",
+            on_device(workloads.make_gqa_step(lqs=[512], lks=[32768], num_q_heads=28,
+                                              num_kv_heads=4, block_size=128, seed=3)), 1)
     if want("configs[3]"):
         note("configs[3] MTP verify (with the KV write of both query tokens)")
         gqa("configs[3]_mtp_verify", workloads.config4_mtp(seed=0, device=dev), 3, write=True)

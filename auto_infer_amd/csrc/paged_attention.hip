@@ -1,22 +1,31 @@
-// Split-K paged attention for gfx950 (GQA, head_dim 128).
+// Paged attention for gfx950: GQA (head_dim 128 and 64) and absorbed MLA.
 //
-// Three kernels:
-//   plan_kernel   one work-group; turns (cu_seqlens_q, seqlens_kv) into a flat
-//                 list of segments (request, kv head, head block, query
-//                 block) with their key tiles (16 keys each), then cuts the
-//                 concatenated tile list into equal contiguous ranges, one
-//                 per wave (balanced split-K: every wave streams the same
-//                 number of KV bytes whatever the context-length mix).
-//   gqa_attn      one wave per range.  Per 16-key tile: K rows go straight
-//                 from HBM into MFMA A-fragments (S^T = K Q^T on
-//                 v_mfma_f32_16x16x16_bf16, the 16 query rows of a segment
-//                 are the N dimension), online softmax on the S^T fragment
-//                 (row max over the 4 lane groups with two xor shuffles),
-//                 V is transposed through LDS and O^T += V^T P^T runs on the
-//                 same MFMA with P^T taken directly from the S^T registers.
-//                 A wave that covers a whole segment writes bf16 output;
-//                 otherwise it writes an fp32 partial (O, m, l).
-//   gqa_merge     log-sum-exp merge of the partials of each split segment.
+// Kernels:
+//   plan_kernel         one work-group per step.  Turns (cu_seqlens_q,
+//                       seqlens_kv) into segments (request, kv-head group,
+//                       head block, query block) with their 16-key tiles and
+//                       cuts the concatenated tile list into equal contiguous
+//                       ranges (balanced split-K: every range streams the same
+//                       number of KV bytes whatever the context-length mix).
+//                       Requests whose query rows fill 128-row items go to the
+//                       prefill units instead.  It also lists the merge work.
+//   gqa_attn_kernel     split-K decode and verify rows, one wave per (range,
+//                       kv head).  K rows go straight from HBM into MFMA
+//                       fragments (S^T = K Q^T), online softmax on the S^T
+//                       registers, V^T through LDS, O^T += V^T P^T with P^T
+//                       taken from the S^T registers.  A wave that covers a
+//                       whole segment writes bf16 output, otherwise an fp32
+//                       partial (O, m, l).
+//   gqa_prefill_kernel  prefill units: 128 query rows per work-group, 64-key
+//                       K/V tiles loaded straight into LDS and used by all of
+//                       them, QK^T and PV on MFMA.  A unit that covers only
+//                       part of its item's keys writes an fp16 partial scaled
+//                       per row.
+//   gqa_mixed_kernel    both roles in one grid (Hkv = 4), so the compute-bound
+//                       units run beside the HBM-bound ranges.
+//   mla_attn_kernel     absorbed MLA over one latent cache (576-wide keys, V =
+//                       their first 512 dims), four waves per range.
+//   merge_kernel        log-sum-exp merge of the split segments and cut items.
 #include <math.h>
 
 #include <atomic>

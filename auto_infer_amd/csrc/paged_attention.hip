@@ -163,7 +163,7 @@ Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_
 
 // Workspace layout (all offsets 256-byte aligned).
 struct Layout {
-  int64_t hdr, seg, wave, part_ml, part_o, part_sc, cnt, req, mrg, pf, pfm, pfw, pf_o, pf_ml, total;
+  int64_t hdr, seg, wave, part_ml, part_o, cnt, req, mrg, pf, pfm, pfw, pf_o, pf_ml, total;
   int64_t seg_cap, part_cap, mrg_cap, pf_cap, pf_unit_cap, pf_mrg_cap, pf_slots;
 };
 
@@ -187,7 +187,6 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
   L.wave = off;     off = align256(off + (int64_t)waves * kRecInts * 4);
   L.part_ml = off;  off = align256(off + L.part_cap * g.nw * kRows * g.rb * 8);
   L.part_o = off;   off = align256(off + L.part_cap * g.nw * kRows * g.rb * (int64_t)dv * 4);
-  L.part_sc = off;  off = align256(off + L.part_cap * g.nw * kRows * g.rb * 4);
   L.mrg_cap = L.seg_cap * g.nw * merge_slices(g, dv);
   L.mrg = off;      off = align256(off + L.mrg_cap * kMrgInts * 4);
   L.cnt = off;      off = align256(off + L.seg_cap * g.nw * 4);
@@ -1851,8 +1850,7 @@ struct MergeArgs {
   int32_t group, hb, dv, nw, hkv, rb;
   const int32_t* mrg;
   int64_t mrg_cap;
-  int32_t part_f16;          // split-K partials stored as fp16 scaled by part_sc
-  const float* part_sc;
+  int32_t part_f16;          // split-K partials stored as fp16, scaled per row
   // prefill chunk merges: records {first query token, first row, first
   // unit, units | item rows << 16}
   const int4* pf_mrg;
@@ -1920,12 +1918,11 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
       }
       mx = mn;
     };
-    if (live && a.part_f16) {    // scaled fp16 partials: x = y * c
+    if (live && a.part_f16) {    // fp16 partials y = O / c, with (m + log2 c, l / c)
 #pragma unroll 2
       for (int k = kg; k < np; k += kMergeGroups) {
         const int64_t pr = row0 + k * pstride;
         const float2 ml = a.part_ml[pr];
-        const float sc = a.part_sc[pr];
         const uint4* src = reinterpret_cast<const uint4*>(
             reinterpret_cast<const uint16_t*>(a.part_o) + pr * a.dv + c);
         const uint4 h0 = src[0], h1 = src[1];
@@ -1935,7 +1932,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
         for (int i = 0; i < kMergeDims / 4; ++i) {
           const half2_t a2 = __builtin_bit_cast(half2_t, hw[2 * i]);
           const half2_t b2 = __builtin_bit_cast(half2_t, hw[2 * i + 1]);
-          x[i] = make_float4((float)a2[0] * sc, (float)a2[1] * sc, (float)b2[0] * sc, (float)b2[1] * sc);
+          x[i] = make_float4((float)a2[0], (float)a2[1], (float)b2[0], (float)b2[1]);
         }
         fold(ml, x);
       }
@@ -2067,7 +2064,6 @@ struct MlaArgs {
   const int32_t* wave_rec;
   float* part_o;
   float2* part_ml;
-  float* part_sc;
   uint16_t* out;
   int64_t o_ts, o_hs;
   int32_t waves;
@@ -2274,7 +2270,7 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
       const float c = fmaxf(fmaxf(smax[r * kRows + n], smax[(RB + r) * kRows + n]),
                             fmaxf(smax[(2 * RB + r) * kRows + n], smax[(3 * RB + r) * kRows + n]));
       if (!rv[r]) continue;
-      const float inv = c > 0.f ? 1.f / c : 0.f;
+      const float cc = c > 0.f ? c : 1.f, inv = 1.f / cc;
       const int64_t prow = (int64_t)part * seg_rows + r * kRows + n;
       uint16_t* pp = reinterpret_cast<uint16_t*>(a.part_o) + prow * kMlaV + d0;
 #pragma unroll
@@ -2284,10 +2280,9 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
         wv.y = pack_f16x2(o[r][dt][2] * inv, o[r][dt][3] * inv);
         *reinterpret_cast<uint2*>(pp + 16 * dt + 4 * g) = wv;
       }
-      if (g == 0 && wid == 0) {
-        a.part_ml[prow] = make_float2(m[r], lsum[r]);
-        a.part_sc[prow] = c;
-      }
+      // the scale goes into the weights: (m + log2 c, l / c), so the merge
+      // folds y = O / c exactly as it folds O
+      if (g == 0 && wid == 0) a.part_ml[prow] = make_float2(m[r] + __log2f(cc), lsum[r] * inv);
     }
   }
 }
@@ -2351,7 +2346,6 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
   mg.nw = nw; mg.hkv = g.hkv; mg.rb = g.rb;
   mg.mrg = reinterpret_cast<const int32_t*>(ws + L.mrg); mg.mrg_cap = L.mrg_cap;
   mg.part_f16 = dv == kMlaV ? 1 : 0;
-  mg.part_sc = reinterpret_cast<const float*>(ws + L.part_sc);
   const bool pf = L.pf_mrg_cap > 0;
   mg.pf_mrg = pf ? reinterpret_cast<const int4*>(ws + L.pfm) : nullptr;
   mg.pf_items_cap = L.pf_mrg_cap * g.hkv * (kPfRows / 16);
@@ -2596,7 +2590,6 @@ extern "C" int aia_paged_attention_mla(
   a.wave_rec = reinterpret_cast<const int32_t*>(ws + L.wave);
   a.part_o = reinterpret_cast<float*>(ws + L.part_o);
   a.part_ml = reinterpret_cast<float2*>(ws + L.part_ml);
-  a.part_sc = reinterpret_cast<float*>(ws + L.part_sc);
   a.out = static_cast<uint16_t*>(out);
   a.o_ts = out_token_stride; a.o_hs = out_head_stride;
   a.waves = waves;

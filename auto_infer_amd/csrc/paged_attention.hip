@@ -202,9 +202,9 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
   L.pf_unit_cap = L.pf_cap > split_units ? L.pf_cap : split_units;
   L.pf_mrg_cap = g.pf ? (kPfTargetWgs + g.hkv - 1) / g.hkv : 0;
   L.pf_slots = split_units * g.hkv;             // partial row blocks
-  L.pf = off;       off = align256(off + L.pf_unit_cap * 16);
+  L.pf = off;       off = align256(off + L.pf_unit_cap * 32);              // two int4 per unit
   L.pfm = off;      off = align256(off + L.pf_mrg_cap * 16);
-  L.pfw = off;      off = align256(off + (g.pf ? kPfTargetWgs * 32 : 0));   // dealt work-groups
+  L.pfw = off;      off = align256(off + (g.pf ? kPfTargetWgs * 48 : 0));   // dealt work-groups
   L.pf_ml = off;    off = align256(off + L.pf_slots * kPfRows * 8);
   L.pf_o = off;     off = align256(off + L.pf_slots * kPfRows * (int64_t)kHeadDim * 4);
   L.total = off;
@@ -439,8 +439,18 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
           const int rows = min(kPfRows, (c1 - c0) * g.group - r0);
           pf_mrg[mm] = make_int4(c0, r0, u, k | (rows << 16));
         }
-        for (int j = 0; j < k; ++j)
-          pf_units[u + j] = make_int4(b, r0, (int)((int64_t)j * nt / k), (int)((int64_t)(j + 1) * nt / k));
+        // unit record: {request, first row, first tile, end tile}, then
+        // {first query token, query tokens, keys, block id of the first
+        // tile}, so a work-group starts its Q and first-tile loads as soon
+        // as its record arrives (the id serves block sizes that are a
+        // multiple of the tile)
+        const int c0 = cu_p[b], lqb = cu_p[b + 1] - c0, lkb = kv_p[b];
+        const int32_t* btr = block_table + (int64_t)b * bt_stride;
+        for (int j = 0; j < k; ++j) {
+          const int tj = (int)((int64_t)j * nt / k);
+          pf_units[2 * (u + j)] = make_int4(b, r0, tj, (int)((int64_t)(j + 1) * nt / k));
+          pf_units[2 * (u + j) + 1] = make_int4(c0, lqb, lkb, btr[(tj * kPfKeys) / block_size]);
+        }
       }
       ucarry += tot2.x;
       mcarry2 += tot2.y;
@@ -449,19 +459,36 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     pmerges = mcarry2;
     if (units > pf_unit_cap || pmerges > pf_mrg_cap) { units = 0; pmerges = 0; overflow = 1; }
 
-    // 1c) When a step has only prefill work-groups and they fit one round,
-    // two per CU (the hardware puts work-groups b and b + ncu on one CU
-    // then), deal them by size so every CU's pair sums evenly: the largest
-    // units alone on the CUs without a partner, then the i-th largest of the
-    // rest beside the i-th smallest.  Each dealt work-group gets its unit
-    // record and {unit, kv head} in pf_wg (two int4); hdr[9] = their number,
-    // 0 = not dealt.
+    // 1c) Work-group b's record at pf_wg[b]: its unit record (two int4),
+    // then {unit, kv head}, so a work-group loads it beside the header
+    // instead of after it; hdr[9] = the number written (0: too many
+    // work-groups, they read the unit list).  When a step has only prefill
+    // work-groups and they fit one round, two per CU (the hardware puts
+    // work-groups b and b + ncu on one CU then), they are dealt by size so
+    // every CU's pair sums evenly: the largest units alone on the CUs
+    // without a partner, then the i-th largest of the rest beside the i-th
+    // smallest.  Otherwise b takes (kv head, unit) pair xcd_range(b, pairs):
+    // each XCD gets a contiguous run of pairs, kv-head major, so the items
+    // that re-read one request's keys for one kv head share an XCD's L2.
     const int jobs = units * g.hkv;
+    if (jobs <= kPfTargetWgs && !(carry == 0 && jobs > g.ncu && jobs <= 2 * g.ncu)) {
+      __syncthreads();   // publishes pf_units to the whole group
+      const int q = jobs / kXcdsPlan, r = jobs - q * kXcdsPlan;
+      for (int id = tid; id < jobs; id += kPlanThreads) {
+        const int x = id % kXcdsPlan, i = id / kXcdsPlan;
+        const int pair = x * q + min(x, r) + i;          // xcd_range(id, jobs)
+        const int kvh = pair / units, u = pair - kvh * units;
+        pf_wg[3 * id] = pf_units[2 * u];
+        pf_wg[3 * id + 1] = pf_units[2 * u + 1];
+        pf_wg[3 * id + 2] = make_int4(u, kvh, 0, 0);
+      }
+      dealt = jobs;
+    }
     if (carry == 0 && jobs > g.ncu && jobs <= 2 * g.ncu && jobs <= kPfTargetWgs) {
       if (tid < 64) pf_hist[tid] = 0;
       __syncthreads();   // also publishes pf_units to the whole group
       for (int p = tid; p < jobs; p += kPlanThreads) {
-        const int4 e = pf_units[p % units];
+        const int4 e = pf_units[2 * (p % units)];
         atomicAdd(&pf_hist[63 - min(e.w - e.z, 63)], 1);   // bucket 0: the largest
       }
       __syncthreads();
@@ -473,12 +500,13 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       const int n2 = jobs - g.ncu, lone = g.ncu - n2;
       for (int p = tid; p < jobs; p += kPlanThreads) {
         const int u = p % units, kvh = p / units;
-        const int4 e = pf_units[u];
+        const int4 e = pf_units[2 * u];
         const int r = atomicAdd(&pf_hist[63 - min(e.w - e.z, 63)], 1);
         const int i = r - lone;
         const int id = r < lone ? n2 + r : i < n2 ? i : g.ncu + (jobs - 1 - r);
-        pf_wg[2 * id] = e;
-        pf_wg[2 * id + 1] = make_int4(u, kvh, 0, 0);
+        pf_wg[3 * id] = e;
+        pf_wg[3 * id + 1] = pf_units[2 * u + 1];
+        pf_wg[3 * id + 2] = make_int4(u, kvh, 0, 0);
       }
       dealt = jobs;
     }
@@ -1334,8 +1362,10 @@ struct PrefillArgs {
   float scale_log2;
   uint16_t* out;
   int64_t o_ts, o_hs;
-  const int4* units;         // {request, first row, first tile, end tile}
-  const int4* dealt;         // work-group b: its unit record, then {unit, kv head}
+  const int4* units;         // per unit: {request, first row, first tile, end tile},
+                             // {first query token, query tokens, keys, first tile's block id}
+  const int4* dealt;         // work-group b: its unit record (two int4), then {unit, kv head}
+                             // (written when the work-groups fit kPfTargetWgs, hdr[9])
   const int32_t* hdr;
   uint16_t* part_o;          // partial row blocks of chunked items (fp16, scaled per row)
   float2* part_ml;
@@ -1401,30 +1431,40 @@ template <bool ONE_BLOCK, bool FUSED>
 __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
                                                  uint16_t* k0, uint16_t* k1,
                                                  uint16_t* v0, uint16_t* v1) {
-  // Unless the planner dealt the work-groups by size (hdr[9]), work-group b
-  // takes (kv head, item) pair xcd_range(b, pairs), kv-head major: each XCD
-  // gets a contiguous run of pairs, so the items that re-read one request's
-  // keys for one kv head share an XCD's L2.
+  // The planner writes work-group b's record at dealt[b] when the
+  // work-groups fit the fill target (hdr[9] = their number; dealt by size, or
+  // in xcd_range order); it is loaded beside the header rather than after
+  // it.  Past the target, work-group b takes (kv head, item) pair
+  // xcd_range(b, pairs), kv-head major: each XCD gets a contiguous run of
+  // pairs, so the items that re-read one request's keys for one kv head
+  // share an XCD's L2.
+  int4 w0 = make_int4(0, 0, 0, 0), w1 = w0, w2 = w0;
+  if (wg < kPfTargetWgs) {
+    w0 = a.dealt[3 * wg];
+    w1 = a.dealt[3 * wg + 1];
+    w2 = a.dealt[3 * wg + 2];
+  }
   const int count = a.hdr[6];
   const int pairs = count * a.hkv;
   if (wg >= pairs) return;
   int kvh, unit;
-  int4 it;
-  if (a.hdr[9] == pairs) {     // dealt by size (see the planner)
-    it = a.dealt[2 * wg];
-    const int4 x = a.dealt[2 * wg + 1];
-    unit = x.x;
-    kvh = x.y;
+  int4 it, iq;
+  if (a.hdr[9] == pairs) {     // this work-group's record (see the planner)
+    it = w0;
+    iq = w1;
+    unit = w2.x;
+    kvh = w2.y;
     if (unit < 0 || unit >= count) return;
   } else {
     const int pair = xcd_range(wg, pairs);
     kvh = pair / count;
     unit = pair - kvh * count;
-    it = a.units[unit];
+    it = a.units[2 * unit];
+    iq = a.units[2 * unit + 1];
   }
   const int b = it.x, row0 = it.y, t0 = it.z, t1 = it.w;
   if (b < 0 || b >= a.batch || kvh >= a.hkv) return;
-  const int q_begin = a.cu_q[b], lq = a.cu_q[b + 1] - q_begin, lk = a.kvlen[b];
+  const int q_begin = iq.x, lq = iq.y, lk = iq.z, bid0 = iq.w;
   const int G = a.group;
   const int nrows = lq * G;
   if (row0 < 0 || row0 >= nrows || q_begin < 0 || q_begin + lq > a.tokens) return;
@@ -1528,6 +1568,7 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     }
   };
   auto tile_bid = [&](int t) {
+    if (t == t0) return bid0;      // from the unit record
     if (t - tb >= 64) {
       tb = t;
       vbid = btrow[min((t + lane) * kPfKeys, kend - 1) / a.bs];
@@ -1708,6 +1749,10 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
   if (t1 > t0) {
     using buf0 = std::integral_constant<int, 0>;
     using buf1 = std::integral_constant<int, 1>;
+    if (ONE_BLOCK) {   // the next 64 tiles' ids, in flight beside the first tile
+      tb = t0;
+      vbid = btrow[min((t0 + lane) * kPfKeys, kend - 1) / a.bs];
+    }
     fetch_ids(t0);
     load(t0, buf0{});
     fetch_ids(t0 + 1);

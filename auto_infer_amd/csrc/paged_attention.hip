@@ -1559,6 +1559,8 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
   const uint16_t* vnb = FUSED ? a.vn + kvoff : nullptr;
   constexpr int kLdKeys = kPfWaves * 4;                // keys per loader round
   constexpr int kLdRounds = kPfKeys / kLdKeys;
+  static_assert(kLdKeys % 16 == 0 && kPfKeys % kLdKeys == 0,
+                "loader rounds of whole 16-key swizzle groups");
   int bid[kLdRounds];
   int tb = -64, vbid = 0;
   auto fetch_ids = [&](int t) {
@@ -1586,7 +1588,7 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
       vp = fresh ? vnb + tok * a.vn_ts : vp;
     }
     const int rb = (kLdKeys * i + 4 * wid) * kHeadDim;     // the wave's first row
-    lds_load16(kp + 8 * (lc ^ lkey), kdst + rb);
+    lds_load16(kp + 8 * (lc ^ (lkey & 15)), kdst + rb);   // rounds start at multiples of 16 keys
     lds_load16(vp + 8 * (lc ^ (2 * (lkey & 7))), vdst + rb);
   };
   auto load = [&](int t, auto buf_tag) {

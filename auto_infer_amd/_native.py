@@ -40,6 +40,7 @@ SIGNATURES = {
                                         c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                                         c_f32, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64,
                                         c_i32, c_i32, c_vp],
+    "aia_noalloc_scratch_bytes": [ctypes.POINTER(c_i64)],
     "aia_paged_attention_mla": [c_vp, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp, c_vp, c_i32,
                                 c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp,
                                 c_i64, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp],

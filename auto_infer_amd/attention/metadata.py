@@ -8,7 +8,17 @@ split-K plan; both depend only on the step, so they are built once per
 as ``ctx.aia_cu_seqlens_q`` / ``ctx.aia_seqlens_kv``) and cached on it.
 Every context's plan owns its workspace, so steps in flight on different
 streams do not share scratch memory.
+
+Device metadata attached by a packer is not checked on the host.  Query
+lengths that do not add up to the step's token count make the planner plan
+nothing (status -1); the attention call then fills its output with NaN.
+With ``AIA_CHECK_PLAN=1`` in the environment, ``step_plan`` also reads the
+status back after planning (one device synchronisation per step) and raises
+the ValueError of the reference's stager contract
+(prefill_input_stager.py:77-81).
 """
+import os
+
 import torch
 
 from auto_infer_amd import ops
@@ -45,5 +55,8 @@ def step_plan(ctx, num_q_heads, num_kv_heads, head_dim_v, block_size):
     # out again while a step on another stream still reads it
     plan = ops.AttentionPlan(bt, cu, kv, T, num_q_heads, num_kv_heads, head_dim_v, block_size,
                              owned=owned)
+    if not owned and os.environ.get("AIA_CHECK_PLAN", "0") == "1" and \
+            not torch.cuda.is_current_stream_capturing():
+        plan.status()
     plans[key] = plan
     return plan

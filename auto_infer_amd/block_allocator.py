@@ -146,7 +146,9 @@ class KVCacheManager:
             chunk = tuple(token_ids[start:start + bs])
             h = hash((prev, chunk))
             b = self._owner.get(h)
-            if b is None or self._chunk_of[b] != chunk or state[b] == _UNUSED:
+            # an id outside the pool (registered by the caller) never matches
+            if b is None or not 0 <= b < self.num_blocks or self._chunk_of[b] != chunk \
+                    or state[b] == _UNUSED:
                 break
             if state[b] == _CACHED:
                 self._ring_unlink(b)
@@ -168,8 +170,13 @@ class KVCacheManager:
             chunk = tuple(token_ids[i * bs:(i + 1) * bs])
             h = hash((prev, chunk))
             b = block_ids[i]
+            # An id outside the pool still claims the hash (as a dict keyed by
+            # block id would), but has no per-block state to update and is
+            # never matched: negative ids must not alias the pool's last
+            # blocks.
             self._owner.setdefault(h, b)
-            if self._hash_of[b] is None:
-                self._hash_of[b] = h
-            self._chunk_of[b] = chunk
+            if 0 <= b < self.num_blocks:
+                if self._hash_of[b] is None:
+                    self._hash_of[b] = h
+                self._chunk_of[b] = chunk
             prev = h

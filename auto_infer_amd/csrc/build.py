@@ -14,7 +14,8 @@ PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
 OUT_DIR = os.path.join(PKG, "_lib")
 LIB = os.path.join(OUT_DIR, "libautoinfer_amd.so")
-SOURCES = ["core.hip", "kv_write.hip", "paged_attention.hip", "pack.hip", "qk_rope.hip", "mtp_compact.hip", "mla_pre.hip"]
+SOURCES = ["core.hip", "kv_write.hip", "paged_attention.hip", "noalloc.hip", "pack.hip", "qk_rope.hip",
+           "mtp_compact.hip", "mla_pre.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",

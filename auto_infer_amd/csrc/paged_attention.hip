@@ -163,7 +163,7 @@ Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_
 
 // Workspace layout (all offsets 256-byte aligned).
 struct Layout {
-  int64_t hdr, seg, wave, part_ml, part_o, cnt, req, mrg, pf, pfm, pfw, pf_o, pf_ml, total;
+  int64_t hdr, seg, wave, part_ml, part_o, req, mrg, pf, pfm, pfw, pf_o, pf_ml, total;
   int64_t seg_cap, part_cap, mrg_cap, pf_cap, pf_unit_cap, pf_mrg_cap, pf_slots;
 };
 
@@ -186,10 +186,10 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
   L.seg = off;      off = align256(off + (L.seg_cap + 1) * 8 * 4);
   L.wave = off;     off = align256(off + (int64_t)waves * kRecInts * 4);
   L.part_ml = off;  off = align256(off + L.part_cap * g.nw * kRows * g.rb * 8);
-  L.part_o = off;   off = align256(off + L.part_cap * g.nw * kRows * g.rb * (int64_t)dv * 4);
+  // split partials are fp16, scaled per row
+  L.part_o = off;   off = align256(off + L.part_cap * g.nw * kRows * g.rb * (int64_t)dv * 2);
   L.mrg_cap = L.seg_cap * g.nw * merge_slices(g, dv);
   L.mrg = off;      off = align256(off + L.mrg_cap * kMrgInts * 4);
-  L.cnt = off;      off = align256(off + L.seg_cap * g.nw * 4);
   L.req = off;      off = align256(off + ((int64_t)batch + 1) * 8);   // request and item offsets
   // prefill items: a routed request has >= kPfRows rows, so at most
   // rows / kPfRows of them, each adding at most one partial item
@@ -206,7 +206,7 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
   L.pfm = off;      off = align256(off + L.pf_mrg_cap * 16);
   L.pfw = off;      off = align256(off + (g.pf ? kPfTargetWgs * 48 : 0));   // dealt work-groups
   L.pf_ml = off;    off = align256(off + L.pf_slots * kPfRows * 8);
-  L.pf_o = off;     off = align256(off + L.pf_slots * kPfRows * (int64_t)kHeadDim * 4);
+  L.pf_o = off;     off = align256(off + L.pf_slots * kPfRows * (int64_t)kHeadDim * 2);
   L.total = off;
   return L;
 }
@@ -309,7 +309,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ block_table, int64_t bt_stride, int32_t block_size,
     int32_t batch, Geometry g, int32_t waves, int32_t dv,
     int32_t* __restrict__ hdr, int32_t* __restrict__ seg, int32_t* __restrict__ wave_rec,
-    int32_t* __restrict__ counters, int32_t* __restrict__ req_scratch,
+    int32_t* __restrict__ req_scratch,
     int32_t* __restrict__ mrg, int4* __restrict__ pf_units, int4* __restrict__ pf_mrg,
     int4* __restrict__ pf_wg, int32_t pf_cap, int32_t pf_unit_cap, int32_t pf_mrg_cap,
     int32_t seg_cap) {
@@ -675,12 +675,6 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     int mcnt = 0, nwv = 0, nsl = 0, rows = 0;
     int r0[4] = {0, 0, 0, 0};
     if (s < nseg) {
-      if (g.nw % 4 == 0) {
-        for (int i = 0; i < g.nw; i += 4)
-          *reinterpret_cast<int4*>(counters + (int64_t)s * g.nw + i) = make_int4(0, 0, 0, 0);
-      } else {
-        for (int i = 0; i < g.nw; ++i) counters[(int64_t)s * g.nw + i] = 0;
-      }
       if (np > 1) {
         if (regs) {      // the segment's head, kept in registers since phase 2
 #pragma unroll
@@ -863,10 +857,8 @@ struct AttnArgs {
   float scale_log2;
   const int32_t* seg;
   const int32_t* wave_rec;
-  float* part_o;
+  uint16_t* part_o;          // split partials (fp16, scaled per row)
   float2* part_ml;
-  int32_t* counters;
-  int32_t fused_merge;
   uint16_t* out;
   int64_t o_ts, o_hs;
   int32_t waves;
@@ -885,13 +877,6 @@ __device__ __forceinline__ bool rec_ok(const int* r, int nseg_tiles, int batch, 
 
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima), gfx9 encoding.
 constexpr int kWaitVmcnt0 = 0x0F70;
-
-__device__ __forceinline__ uint64_t pack_f2(float x, float y) {
-  return (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
-}
-__device__ __forceinline__ float2 unpack_f2(uint64_t v) {
-  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
-}
 
 __device__ __forceinline__ short4_t as_s4(uint32_t a, uint32_t b) {
   short4_t r;
@@ -955,9 +940,7 @@ constexpr int kPipe = AIA_PIPE;
 // (qb = 16 / hb).  Every K/V tile is loaded once and used by all blocks, so a
 // prefill chunk reads its keys 1/RB as often; blocks past the segment's last
 // token are skipped (a uniform branch), so a decode segment costs one block.
-// FM: the optional in-kernel merge is compiled in (its own instantiation,
-// so the default kernel carries none of its code).
-template <int RB, int D, bool FM>
+template <int RB, int D>
 __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, int s, int lt0,
                                             int lt1, int w, int tpw, uint16_t* vt, int lane,
                                             int wid, bool use_pre, int pre) {
@@ -1159,120 +1142,31 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
       }
     }
   } else {
+    // fp16 partial y = O / c, c = the row's largest |O| (1 for a zero row),
+    // with (m + log2 c, l / c) in place of (m, l): the merge's weights
+    // exp2(m - M) carry c back, so y folds exactly as O would
     const int part = part_base + (w - first_wave);
-    if (FM && D == 128) {   // lanes x 2 dims cover a 128-wide row
-      // In-kernel merge.  Partials go out with agent-coherent stores (sc1,
-      // written through past the per-XCD L2), the wave waits for them to
-      // complete, then bumps the segment's per-head counter; the wave that
-      // sees the last count reads the partials back with agent-coherent
-      // loads, merges, and resets the counter for the next call on this
-      // plan.  No L2 write-back / invalidate is needed.
 #pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        if (!rv[r]) continue;
-        const int64_t prow = ((int64_t)part * a.nw + wid) * seg_rows + r * kRows + n;
-        uint64_t* pp = reinterpret_cast<uint64_t*>(a.part_o + prow * D);
+    for (int r = 0; r < RB; ++r) {
+      float cmax = 0.f;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const int e = (16 * dt + 4 * g) / 2;
-          __hip_atomic_store(pp + e, pack_f2(o[r][dt][0], o[r][dt][1]), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(pp + e + 1, pack_f2(o[r][dt][2], o[r][dt][3]), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-        }
-        if (g == 0)
-          __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_ml + prow), pack_f2(m[r], lsum[r]),
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, fabsf(o[r][dt][i]));
+      cmax = aia::group4_max(cmax);
+      if (!rv[r]) continue;
+      const float c = cmax > 0.f ? cmax : 1.f;
+      const float inv = 1.f / c;
+      const int64_t prow = ((int64_t)part * a.nw + wid) * seg_rows + r * kRows + n;
+      uint16_t* pp = a.part_o + prow * D;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        uint2 hv;
+        hv.x = pack_f16x2(o[r][dt][0] * inv, o[r][dt][1] * inv);
+        hv.y = pack_f16x2(o[r][dt][2] * inv, o[r][dt][3] * inv);
+        *reinterpret_cast<uint2*>(pp + 16 * dt + 4 * g) = hv;
       }
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      int* cnt = a.counters + (int64_t)s * a.nw + wid;
-      int old = 0;
-      if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      old = __shfl(old, 0);
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      if (old == nparts - 1) {
-        // Merge, kept to one short loop.  Lane (p, c) folds
-        // parts p, p + 2, ... of output dims [4c, 4c + 4); lane k of a
-        // 64-part chunk holds part k's (m, l).  A row whose parts fit one
-        // 16-part batch costs one round trip: its (m, l) and partial loads
-        // are issued together.
-        const int64_t pstride = (int64_t)a.nw * seg_rows;   // rows between parts
-        const int64_t rbase = ((int64_t)part_base * a.nw + wid) * seg_rows;
-        const int c = lane & 31, p = lane >> 5;
-        for (int r2 = 0; r2 < nblk; ++r2)
-          for (int t2 = 0; t2 < qb && r2 * qb + t2 < nq; ++t2)
-            for (int hh2 = 0; hh2 < a.hb && hbi * a.hb + hh2 < a.group; ++hh2) {
-              const int64_t row0 = rbase + r2 * kRows + t2 * a.hb + hh2;
-              auto ml_at = [&](int k) {
-                return k < nparts ? unpack_f2(__hip_atomic_load(
-                                        reinterpret_cast<const uint64_t*>(a.part_ml + row0 + k * pstride),
-                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-                                  : make_float2(-1e30f, 0.f);
-              };
-              float2 v[8][2];
-              auto fetch = [&](int kb) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                  const int k = min(kb + p + 2 * i, nparts - 1);
-                  const uint64_t* src =
-                      reinterpret_cast<const uint64_t*>(a.part_o + (row0 + k * pstride) * D) + 2 * c;
-                  v[i][0] = unpack_f2(__hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-                  v[i][1] = unpack_f2(__hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-                }
-              };
-              const float2 ml0 = ml_at(lane);
-              fetch(0);
-              float mx = ml0.x;
-              for (int k0 = 64; k0 < nparts; k0 += 64) mx = fmaxf(mx, ml_at(k0 + lane).x);
-#pragma unroll
-              for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
-              float acc[4] = {0.f, 0.f, 0.f, 0.f}, ls = 0.f;
-              for (int k0 = 0; k0 < nparts; k0 += 64) {
-                const float2 ml = k0 == 0 ? ml0 : ml_at(k0 + lane);
-                const float wk = k0 + lane < nparts ? __builtin_amdgcn_exp2f(ml.x - mx) : 0.f;
-                ls += ml.y * wk;
-                for (int kb = k0; kb < min(nparts, k0 + 64); kb += 16) {
-                  if (kb > 0) fetch(kb);
-#pragma unroll
-                  for (int i = 0; i < 8; ++i) {
-                    const int kl = kb - k0 + p + 2 * i;   // the part's lane in this chunk
-                    const float wi = kb + p + 2 * i < nparts ? __shfl(wk, kl & 63) : 0.f;
-                    acc[0] += v[i][0].x * wi;
-                    acc[1] += v[i][0].y * wi;
-                    acc[2] += v[i][1].x * wi;
-                    acc[3] += v[i][1].y * wi;
-                  }
-                }
-              }
-#pragma unroll
-              for (int d = 32; d >= 1; d >>= 1) ls += __shfl_xor(ls, d);
-#pragma unroll
-              for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], 32);
-              const float inv = ls > 0.f ? 1.f / ls : 0.f;
-              if (p == 0) {
-                const int head2 = kvh * a.group + hbi * a.hb + hh2;
-                uint2 wv;
-                wv.x = aia::pack_bf16x2(acc[0] * inv, acc[1] * inv);
-                wv.y = aia::pack_bf16x2(acc[2] * inv, acc[3] * inv);
-                *reinterpret_cast<uint2*>(a.out + (int64_t)(qtok0 + r2 * qb + t2) * a.o_ts +
-                                          (int64_t)head2 * a.o_hs + 4 * c) = wv;
-              }
-            }
-        if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        if (!rv[r]) continue;
-        const int64_t prow = ((int64_t)part * a.nw + wid) * seg_rows + r * kRows + n;
-        float* pp = a.part_o + prow * D;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-          *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * g) = o[r][dt];
-        if (g == 0) a.part_ml[prow] = make_float2(m[r], lsum[r]);
-      }
+      if (g == 0) a.part_ml[prow] = make_float2(m[r] + __log2f(c), lsum[r] * inv);
     }
   }
 }
@@ -1292,8 +1186,8 @@ __device__ __forceinline__ int xcd_range(int b, int n) {
 }
 
 // One work-group per key range, one wave per kv head of the segment's group.
-// D: head dim, 128 or 64; FM: the in-kernel merge variant.
-template <int NW, int RB, int D, bool FM>
+// D: head dim, 128 or 64.
+template <int NW, int RB, int D>
 #ifndef AIA_GQA_WAVES_PER_EU
 #define AIA_GQA_WAVES_PER_EU 2
 #endif
@@ -1324,7 +1218,7 @@ __device__ __forceinline__ void gqa_attn_body(const AttnArgs& a, int bid,
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
       if ((rec[1] & 0xffff) * NW + wid < a.hkv)
-        gqa_segment<RB, D, FM>(a, rec, s, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane, wid, first,
+        gqa_segment<RB, D>(a, rec, s, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane, wid, first,
                         pre);
       first = false;
       t = chunk_end;
@@ -1337,11 +1231,11 @@ __device__ __forceinline__ void gqa_attn_body(const AttnArgs& a, int bid,
   }
 }
 
-template <int NW, int RB, int D, bool FM>
+template <int NW, int RB, int D>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(AIA_GQA_WAVES_PER_EU, AIA_GQA_WAVES_PER_EU)))
 void gqa_attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vt_all[NW][kTile * kVStride];
-  gqa_attn_body<NW, RB, D, FM>(a, blockIdx.x, vt_all);
+  gqa_attn_body<NW, RB, D>(a, blockIdx.x, vt_all);
 }
 
 // ---------------------------------------------------------------- prefill
@@ -1883,27 +1777,27 @@ void gqa_mixed_kernel(AttnArgs a, PrefillArgs pa, int npf) {
   if (prefill)
     gqa_prefill_body<ONE_BLOCK, FUSED>(pa, idx, k0, k1, v0, v1);
   else
-    gqa_attn_body<kPfWaves, 1, kHeadDim, false>(a, idx,
+    gqa_attn_body<kPfWaves, 1, kHeadDim>(a, idx,
                                          reinterpret_cast<uint16_t(*)[kTile * kVStride]>(&k0[0]));
 }
 
 struct MergeArgs {
   const int32_t* hdr;
   const int32_t* seg;
-  const float* part_o;
+  const uint16_t* part_o;
   const float2* part_ml;
   uint16_t* out;
   int64_t o_ts, o_hs;
   int32_t group, hb, dv, nw, hkv, rb;
   const int32_t* mrg;
   int64_t mrg_cap;
-  int32_t part_f16;          // split-K partials stored as fp16, scaled per row
   // prefill chunk merges: records {first query token, first row, first
   // unit, units | item rows << 16}
   const int4* pf_mrg;
   int64_t pf_items_cap;     // work items the records can hold
   const uint16_t* pf_o;
   const float2* pf_ml;
+  int32_t tokens;           // output rows (query tokens); heads = group x hkv
 };
 
 // Merge of split partials.  The planner lists the merge work: one record per
@@ -1928,6 +1822,8 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   // record, so a prefill work-group's chain is record, then partials
   constexpr int kSlices = kPfRows / 16;
   const int per_rec = a.hkv * kSlices;
+  // planner status, read now and used at the end (no extra round trip)
+  const int status = a.hdr[8];
   int4 pr0 = make_int4(0, 0, 0, 0);
   int npm = 0;
   if (a.pf_mrg) {
@@ -1965,13 +1861,13 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
       }
       mx = mn;
     };
-    if (live && a.part_f16) {    // fp16 partials y = O / c, with (m + log2 c, l / c)
+    if (live) {    // fp16 partials y = O / c, with (m + log2 c, l / c)
 #pragma unroll 2
       for (int k = kg; k < np; k += kMergeGroups) {
         const int64_t pr = row0 + k * pstride;
         const float2 ml = a.part_ml[pr];
         const uint4* src = reinterpret_cast<const uint4*>(
-            reinterpret_cast<const uint16_t*>(a.part_o) + pr * a.dv + c);
+            a.part_o + pr * a.dv + c);
         const uint4 h0 = src[0], h1 = src[1];
         const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
         float4 x[kMergeDims / 4];
@@ -1981,17 +1877,6 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
           const half2_t b2 = __builtin_bit_cast(half2_t, hw[2 * i + 1]);
           x[i] = make_float4((float)a2[0], (float)a2[1], (float)b2[0], (float)b2[1]);
         }
-        fold(ml, x);
-      }
-    } else if (live) {
-#pragma unroll 2
-      for (int k = kg; k < np; k += kMergeGroups) {
-        const int64_t pr = row0 + k * pstride;
-        const float2 ml = a.part_ml[pr];
-        const float4* src = reinterpret_cast<const float4*>(a.part_o + pr * a.dv + c);
-        float4 x[kMergeDims / 4];
-#pragma unroll
-        for (int i = 0; i < kMergeDims / 4; ++i) x[i] = src[i];
         fold(ml, x);
       }
     }
@@ -2079,6 +1964,22 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
       *reinterpret_cast<uint2*>(op + 4 * i) = wv;
     }
   }
+
+  // A plan whose metadata asked for more work than the workspace holds
+  // planned nothing (status -1): no kernel wrote the output, so it is filled
+  // with NaN rather than left holding whatever the memory held.
+  if (status < 0) {
+    const int hq = a.group * a.hkv, per_row = a.dv / 4;   // 4 elements per 8-byte store
+    const int64_t n = (int64_t)a.tokens * hq * per_row;
+    const uint2 nan2 = make_uint2(0x7fc07fc0u, 0x7fc07fc0u);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+      const int64_t row = i / per_row;
+      const int tok = (int)(row / hq), h = (int)(row - (int64_t)tok * hq);
+      const int d = (int)(i - row * per_row) * 4;
+      *reinterpret_cast<uint2*>(a.out + (int64_t)tok * a.o_ts + (int64_t)h * a.o_hs + d) = nan2;
+    }
+  }
 }
 
 // ---------------------------------------------------------------- absorbed MLA
@@ -2109,7 +2010,7 @@ struct MlaArgs {
   float scale_log2;
   const int32_t* seg;
   const int32_t* wave_rec;
-  float* part_o;
+  uint16_t* part_o;          // split partials (fp16, scaled per row)
   float2* part_ml;
   uint16_t* out;
   int64_t o_ts, o_hs;
@@ -2319,7 +2220,7 @@ __device__ __forceinline__ void mla_segment(const MlaArgs& a, const int* rec, in
       if (!rv[r]) continue;
       const float cc = c > 0.f ? c : 1.f, inv = 1.f / cc;
       const int64_t prow = (int64_t)part * seg_rows + r * kRows + n;
-      uint16_t* pp = reinterpret_cast<uint16_t*>(a.part_o) + prow * kMlaV + d0;
+      uint16_t* pp = a.part_o + prow * kMlaV + d0;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         uint2 wv;
@@ -2382,17 +2283,16 @@ void mla_attn_kernel(MlaArgs a) {
   }
 }
 
-int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32_t dv,
-                 const float* part_o,
+int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32_t dv, int32_t tokens,
+                 const uint16_t* part_o,
                  const float2* part_ml, const int32_t* seg, uint16_t* out, int64_t o_ts,
                  int64_t o_hs, hipStream_t s) {
   MergeArgs mg;
   mg.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
   mg.seg = seg; mg.part_o = part_o; mg.part_ml = part_ml;
   mg.out = out; mg.o_ts = o_ts; mg.o_hs = o_hs; mg.group = g.group; mg.hb = g.hb; mg.dv = dv;
-  mg.nw = nw; mg.hkv = g.hkv; mg.rb = g.rb;
+  mg.nw = nw; mg.hkv = g.hkv; mg.rb = g.rb; mg.tokens = tokens;
   mg.mrg = reinterpret_cast<const int32_t*>(ws + L.mrg); mg.mrg_cap = L.mrg_cap;
-  mg.part_f16 = dv == kMlaV ? 1 : 0;
   const bool pf = L.pf_mrg_cap > 0;
   mg.pf_mrg = pf ? reinterpret_cast<const int4*>(ws + L.pfm) : nullptr;
   mg.pf_items_cap = L.pf_mrg_cap * g.hkv * (kPfRows / 16);
@@ -2453,7 +2353,7 @@ extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens
       cu_seqlens_q, seqlens_kv, block_table, block_table_stride, block_size, batch, g, waves,
       head_dim_v, reinterpret_cast<int32_t*>(ws + L.hdr),
       reinterpret_cast<int32_t*>(ws + L.seg), reinterpret_cast<int32_t*>(ws + L.wave),
-      reinterpret_cast<int32_t*>(ws + L.cnt), reinterpret_cast<int32_t*>(ws + L.req),
+      reinterpret_cast<int32_t*>(ws + L.req),
       reinterpret_cast<int32_t*>(ws + L.mrg), reinterpret_cast<int4*>(ws + L.pf),
       reinterpret_cast<int4*>(ws + L.pfm), reinterpret_cast<int4*>(ws + L.pfw),
       (int32_t)L.pf_cap, (int32_t)L.pf_unit_cap,
@@ -2479,8 +2379,8 @@ extern "C" int aia_paged_attention_gqa(
   if (block_size <= 0 || num_blocks <= 0)
     return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: block_size %d / num_blocks %d",
                 block_size, num_blocks);
-  if (flags & ~AIA_ATTN_FUSED_MERGE)
-    return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: unknown flags 0x%x", flags);
+  if (flags != 0)
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: flags must be 0 (got 0x%x)", flags);
   if (num_tokens == 0 || batch == 0) return AIA_OK;    // empty step (zero-size tensors)
   if (!query || !key_cache || !value_cache || !block_table || !out || !workspace || !cu_seqlens_q ||
       !seqlens_kv)
@@ -2519,17 +2419,13 @@ extern "C" int aia_paged_attention_gqa(
   a.scale_log2 = scale * 1.4426950408889634f;
   a.seg = reinterpret_cast<const int32_t*>(ws + L.seg);
   a.wave_rec = reinterpret_cast<const int32_t*>(ws + L.wave);
-  a.part_o = reinterpret_cast<float*>(ws + L.part_o);
+  a.part_o = reinterpret_cast<uint16_t*>(ws + L.part_o);
   a.part_ml = reinterpret_cast<float2*>(ws + L.part_ml);
   a.out = static_cast<uint16_t*>(out);
   a.o_ts = out_token_stride; a.o_hs = out_head_stride;
   a.waves = waves;
   a.hdr = reinterpret_cast<const int32_t*>(ws + L.hdr);
   a.batch = batch; a.tokens = num_tokens;
-  a.counters = reinterpret_cast<int32_t*>(ws + L.cnt);
-  // (the in-kernel merge exists for head_dim 128; 64 always merges in its own pass)
-  a.fused_merge =
-      (flags & AIA_ATTN_FUSED_MERGE) && head_dim == kHeadDim;
   hipStream_t s = (hipStream_t)stream;
   PrefillArgs pa = {};
   if (L.pf_cap > 0) {
@@ -2549,8 +2445,7 @@ extern "C" int aia_paged_attention_gqa(
     pa.part_units = (int32_t)(L.pf_slots / g.hkv);
   }
   const bool one_block = block_size % kPfKeys == 0;
-  if (AIA_MIXED && L.pf_cap > 0 && g.nw == kPfWaves && g.rb == 1 && head_dim == kHeadDim &&
-      !a.fused_merge) {
+  if (AIA_MIXED && L.pf_cap > 0 && g.nw == kPfWaves && g.rb == 1 && head_dim == kHeadDim) {
     const int npf = (int)(L.pf_unit_cap * g.hkv);
     const dim3 grid((unsigned)(npf + waves));
     if (one_block && pa.kn) gqa_mixed_kernel<true, true><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
@@ -2559,13 +2454,11 @@ extern "C" int aia_paged_attention_gqa(
     else gqa_mixed_kernel<false, false><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
     if (int rc = check_hip(hipGetLastError(), "gqa_mixed_kernel launch")) return rc;
   } else {
-#define AIA_GQA_LAUNCH_D(NW, D, FM)                                               \
-  (g.rb == 2 ? gqa_attn_kernel<NW, 2, D, FM><<<waves, 64 * NW, 0, s>>>(a)        \
-             : gqa_attn_kernel<NW, 1, D, FM><<<waves, 64 * NW, 0, s>>>(a))
+#define AIA_GQA_LAUNCH_D(NW, D)                                                   \
+  (g.rb == 2 ? gqa_attn_kernel<NW, 2, D><<<waves, 64 * NW, 0, s>>>(a)            \
+             : gqa_attn_kernel<NW, 1, D><<<waves, 64 * NW, 0, s>>>(a))
 #define AIA_GQA_LAUNCH(NW)                                                        \
-  (head_dim == 64 ? AIA_GQA_LAUNCH_D(NW, 64, false)                               \
-   : a.fused_merge ? AIA_GQA_LAUNCH_D(NW, kHeadDim, true)                         \
-                   : AIA_GQA_LAUNCH_D(NW, kHeadDim, false))
+  (head_dim == 64 ? AIA_GQA_LAUNCH_D(NW, 64) : AIA_GQA_LAUNCH_D(NW, kHeadDim))
     switch (g.nw) {
       case 1: AIA_GQA_LAUNCH(1); break;
       case 2: AIA_GQA_LAUNCH(2); break;
@@ -2588,8 +2481,7 @@ extern "C" int aia_paged_attention_gqa(
       if (int rc = check_hip(hipGetLastError(), "gqa_prefill_kernel launch")) return rc;
     }
   }
-  if (a.fused_merge) return AIA_OK;
-  return launch_merge(ws, L, g, g.nw, head_dim, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
+  return launch_merge(ws, L, g, g.nw, head_dim, num_tokens, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
                       s);
 }
 
@@ -2635,7 +2527,7 @@ extern "C" int aia_paged_attention_mla(
   a.scale_log2 = scale * 1.4426950408889634f;
   a.seg = reinterpret_cast<const int32_t*>(ws + L.seg);
   a.wave_rec = reinterpret_cast<const int32_t*>(ws + L.wave);
-  a.part_o = reinterpret_cast<float*>(ws + L.part_o);
+  a.part_o = reinterpret_cast<uint16_t*>(ws + L.part_o);
   a.part_ml = reinterpret_cast<float2*>(ws + L.part_ml);
   a.out = static_cast<uint16_t*>(out);
   a.o_ts = out_token_stride; a.o_hs = out_head_stride;
@@ -2646,74 +2538,6 @@ extern "C" int aia_paged_attention_mla(
   if (g.rb == 2) mla_attn_kernel<2><<<waves, 256, 0, s>>>(a);
   else mla_attn_kernel<1><<<waves, 256, 0, s>>>(a);
   if (int rc = check_hip(hipGetLastError(), "mla_attn_kernel launch")) return rc;
-  return launch_merge(ws, L, g, 1, kMlaV, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
+  return launch_merge(ws, L, g, 1, kMlaV, num_tokens, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
                       s);
-}
-
-// ------------------------------------------------- allocation-free variant
-
-// Scratch of the allocation-free entry point: plan + partials in one
-// file-scope device array (every GPU the library runs on holds its own copy
-// until the process ends).  Host code uses the per-device address that
-// hipGetSymbolAddress returns, never the array's name.
-namespace {
-constexpr int64_t kScratchBytes = 256ll << 20;
-constexpr int kMaxScratchDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxScratchDevices];
-}  // namespace
-
-static __device__ __align__(256) char scratch[kScratchBytes];
-
-static int scratch_address(void** out) {
-  int dev = 0;
-  if (int rc = aia::check_hip(hipGetDevice(&dev), "aia_paged_attention_gqa_noalloc: hipGetDevice"))
-    return rc;
-  if (dev < 0 || dev >= kMaxScratchDevices)
-    return aia::fail(AIA_ERR_UNSUPPORTED, "aia_paged_attention_gqa_noalloc: device %d", dev);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
-    void* p = nullptr;
-    if (int rc = aia::check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
-                                "aia_paged_attention_gqa_noalloc: scratch address"))
-      return rc;
-    g_scratch_ptr[dev] = p;
-  }
-  *out = g_scratch_ptr[dev];
-  return AIA_OK;
-}
-
-extern "C" int aia_paged_attention_gqa_noalloc(
-    const void* query, int64_t q_token_stride, int64_t q_head_stride, const void* key_cache,
-    const void* value_cache, const int32_t* block_table, int32_t block_table_stride,
-    const int32_t* cu_seqlens_q, const int32_t* seqlens_kv, int32_t batch, int32_t num_tokens,
-    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-    int32_t num_blocks, float scale, void* out, int64_t out_token_stride, int64_t out_head_stride,
-    const void* key_new, const void* value_new, int64_t new_key_token_stride,
-    int64_t new_value_token_stride, int32_t num_waves, int32_t flags, void* stream) {
-  using namespace aia;
-  if (int rc = check_heads("aia_paged_attention_gqa_noalloc", num_q_heads, num_kv_heads)) return rc;
-  if (batch < 0 || num_tokens < 0)
-    return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa_noalloc: bad sizes");
-  if (num_tokens == 0 || batch == 0) return AIA_OK;
-  int64_t need = 0;
-  if (int rc = aia_attn_workspace_bytes(batch, num_tokens, num_q_heads, num_kv_heads, head_dim,
-                                        num_waves, &need))
-    return rc;
-  if (need > kScratchBytes)
-    return fail(AIA_ERR_CAPACITY,
-                "aia_paged_attention_gqa_noalloc: step needs %lld bytes of scratch, the static "
-                "scratch holds %lld", (long long)need, (long long)kScratchBytes);
-  void* ws = nullptr;
-  if (int rc = scratch_address(&ws)) return rc;
-  if (int rc = aia_attn_plan(cu_seqlens_q, seqlens_kv, block_table, block_table_stride,
-                             block_size, batch, num_tokens, num_q_heads, num_kv_heads, head_dim,
-                             num_waves, ws, kScratchBytes, stream))
-    return rc;
-  return aia_paged_attention_gqa(query, q_token_stride, q_head_stride, key_cache, value_cache,
-                                 block_table, block_table_stride, cu_seqlens_q, seqlens_kv, batch,
-                                 num_tokens, num_q_heads, num_kv_heads, head_dim, block_size,
-                                 num_blocks, scale, out, out_token_stride, out_head_stride,
-                                 key_new, value_new, new_key_token_stride, new_value_token_stride,
-                                 num_waves, flags, ws, kScratchBytes, stream);
 }

@@ -329,7 +329,8 @@ class AttentionPlan:
         """Synchronising check of the last plan: raises ValueError if the
         planner found more work than the workspace was sized for (query
         lengths that do not add up to ``num_tokens``); the kernels then ran
-        an empty plan and left the output unwritten."""
+        an empty plan and the attention calls filled their outputs with
+        NaN."""
         code = int(self.workspace[32:36].view(torch.int32).item())
         if code != 0:
             raise ValueError(f"attention planner overflow (status {code}): cu_seqlens_q does "
@@ -389,9 +390,6 @@ def _check_out(out, name, shape, device):
     if out.dim() == 3:
         _require(out.stride(1) >= out.shape[2] and out.stride(0) >= out.shape[1] * out.stride(1),
                  f"{name} rows must not overlap")
-
-
-ATTN_FUSED_MERGE = 2        # merge split rows inside the split kernel (default: 2nd kernel)
 
 
 def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None, flags=0,

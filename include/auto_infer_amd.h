@@ -97,7 +97,7 @@ int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
  * hidden 896 over 14 heads), AIA_ERR_UNSUPPORTED otherwise; scale must be
  * positive (AIA_ERR_INVALID otherwise).  Prefill items exist for head_dim
  * 128; at 64 every row runs on the split-K kernel (two query blocks per key
- * tile for prefill chunks) and AIA_ATTN_FUSED_MERGE is ignored.
+ * tile for prefill chunks).
  * The workspace must hold a plan made by
  * aia_attn_plan with the same metadata, head counts and num_waves.
  * key_new / value_new (optional, both or neither): this step's new K/V rows
@@ -106,12 +106,13 @@ int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
  * rows (what aia_kv_write would do, at slot block_table[b, pos / bs] * bs +
  * pos % bs -- the slot_mapping every packer produces) and reads the new keys
  * from the rows themselves, saving the separate write launch.
- * Rows whose keys were split over several work-groups are merged from fp32
- * (O, max, sum) partials by log-sum-exp, by default in a second kernel.
- * flags: AIA_ATTN_FUSED_MERGE merges in the split kernel instead (the last
- * work-group of a split row to finish merges it, via agent-coherent partial
- * stores and a per-segment counter).  Other bits must be 0. */
-#define AIA_ATTN_FUSED_MERGE 2
+ * Rows whose keys were split over several work-groups are merged by
+ * log-sum-exp in a second kernel, from fp16 partials y = O / c scaled per
+ * row (c = the row's largest |O|) with fp32 (max + log2 c, sum / c).
+ * If the plan overflowed (query lengths that do not add up to num_tokens:
+ * the planner plans nothing and sets status -1 in the workspace header), the
+ * output is filled with NaN.
+ * flags must be 0. */
 int aia_paged_attention_gqa(const void* query, int64_t q_token_stride,
                             int64_t q_head_stride,
                             const void* key_cache, const void* value_cache,
@@ -130,14 +131,17 @@ int aia_paged_attention_gqa(const void* query, int64_t q_token_stride,
                             void* stream);
 
 /* Allocation-free paged GQA attention: aia_attn_plan + aia_paged_attention_gqa
- * in one call, with the plan and the split partials in a static 256 MiB
- * device array of the library (one per GPU, held until the process ends)
- * instead of a caller workspace.  No counterpart in the reference: it is for
- * callers that cannot allocate device memory (code under HIP graph capture,
- * tight serving loops, harnesses that forbid allocation).  Same arguments as
+ * in one call, with the plan and the split partials in a static device array
+ * of the library (aia_noalloc_scratch_bytes: 96 MiB; one per GPU, held until
+ * the process ends) instead of a caller workspace.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  The array sits in its own code object, which the runtime
+ * loads onto a GPU only on the first call there: processes that never call
+ * this entry point do not hold it.  Same arguments as
  * aia_paged_attention_gqa without the workspace; steps whose plan needs
- * more than 256 MiB (aia_attn_workspace_bytes; every BASELINE config needs
- * at most 132 MiB) fail with AIA_ERR_CAPACITY.
+ * more than the array (aia_attn_workspace_bytes) fail with
+ * AIA_ERR_CAPACITY.  It plans on every call (one planner launch per call).
  * All calls on one GPU share the array: calls that overlap on one GPU (two
  * streams, two host threads) race and must be ordered by the caller. */
 int aia_paged_attention_gqa_noalloc(const void* query, int64_t q_token_stride,
@@ -155,6 +159,10 @@ int aia_paged_attention_gqa_noalloc(const void* query, int64_t q_token_stride,
                                     int64_t new_key_token_stride,
                                     int64_t new_value_token_stride, int32_t num_waves,
                                     int32_t flags, void* stream);
+
+/* Size in bytes of the allocation-free entry point's static array.  No
+ * counterpart in the reference (see aia_paged_attention_gqa_noalloc). */
+int aia_noalloc_scratch_bytes(int64_t* bytes);
 
 /* Absorbed-MLA paged attention over a planned step.  Replaces the FIA call of
  * mla_paged_absorbed (reference auto_infer/layers/attention/mla.py:76-122,

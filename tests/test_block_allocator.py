@@ -155,3 +155,31 @@ def test_config5_fragmentation_trace_matches_oracle():
     want, _ = workloads.fragmented_block_tables(lks, num_blocks=8192, block_size=128, ops=1500,
                                                 allocator=RefKVCacheManager)
     assert got == want
+
+
+@pytest.mark.parametrize("cls", [KVCacheManager, RefKVCacheManager], ids=["product", "oracle"])
+def test_out_of_range_ids_in_register_prefix(cls):
+    """Block ids outside the pool handed to register_prefix claim their
+    hashes (as the reference's dicts keyed by block id do) but never match,
+    and a negative id does not alias the pool's last block: the same log
+    from the product and the oracle."""
+    def drive(m):
+        log = []
+        toks = [1, 2, 3, 4, 5, 6]
+        m.register_prefix(toks[:2], [-1])
+        m.register_prefix(toks, [-1, m.num_blocks, m.num_blocks + 3])
+        a = m.allocate(2)                  # the highest id: the slot -1 would alias
+        log.append(a)
+        m.register_prefix([9, 9], a)
+        log.append(m.match_prefix(toks))   # hashes held by foreign ids: no hit
+        m.free(a)
+        b = m.allocate(6)
+        log.append(b)
+        m.register_prefix(toks, b)
+        log.append(m.match_prefix(toks))
+        m.free(b)
+        log.append(m.allocate(8))
+        log.append(m.num_free_blocks())
+        return log
+    got = drive(cls(8, 2))
+    assert got == drive(RefKVCacheManager(8, 2))

@@ -14,13 +14,13 @@ DEV = "cuda:0"
 TOL = 2e-2
 
 
-def run_gpu(step, num_waves=0, flags=0):
+def run_gpu(step, num_waves=0):
     s = step
     plan = ops.AttentionPlan.from_lists(s.block_table.to(DEV), s.cu_seqlens_q, s.seqlens_kv,
                                         s.q.shape[1], s.k_cache.shape[2], s.q.shape[2],
                                         s.k_cache.shape[1], num_waves=num_waves)
     out = ops.paged_attention_gqa(s.q.to(DEV), s.k_cache.to(DEV), s.v_cache.to(DEV), plan,
-                                  s.scale, flags=flags)
+                                  s.scale)
     torch.cuda.synchronize()
     return out.float().cpu()
 
@@ -30,8 +30,8 @@ def oracle(step):
                            step.cu_seqlens_q, step.seqlens_kv, step.scale)
 
 
-def check(step, num_waves=0, flags=0):
-    got = run_gpu(step, num_waves, flags)
+def check(step, num_waves=0):
+    got = run_gpu(step, num_waves)
     exp = oracle(step)
     err = (got - exp).abs().max().item()
     print(f"max-abs err {err:.3e}", flush=True)
@@ -39,23 +39,20 @@ def check(step, num_waves=0, flags=0):
     return got
 
 
-@pytest.mark.parametrize("flags", [0, ops.ATTN_FUSED_MERGE])
-def test_config1_decode_shape(flags):
-    check(workloads.config1_decode(seed=3), flags=flags)
+def test_config1_decode_shape():
+    check(workloads.config1_decode(seed=3))
 
 
 @pytest.mark.parametrize("waves", [1, 7, 64, 0])
-@pytest.mark.parametrize("flags", [0, ops.ATTN_FUSED_MERGE])
-def test_split_count_invariance(waves, flags):
-    """The result does not depend on how the key range is split, nor on
-    whether split rows are merged in the kernel or by a second pass."""
+def test_split_count_invariance(waves):
+    """The result does not depend on how the key range is split."""
     step = workloads.make_gqa_step(lqs=[1, 1, 1], lks=[300, 17, 1000], num_q_heads=8,
                                    num_kv_heads=2, block_size=16, seed=11)
-    check(step, waves, flags)
+    check(step, waves)
 
 
 def test_repeated_calls_on_one_plan():
-    """The in-kernel merge resets its counters: many layers on one plan."""
+    """Many layers on one plan give the same result (the plan is read-only)."""
     step = workloads.make_gqa_step(lqs=[1, 2, 1], lks=[900, 40, 2000], num_q_heads=16,
                                    num_kv_heads=8, block_size=128, seed=13)
     plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
@@ -100,14 +97,13 @@ def test_chunked_prefill_and_decode_mixed():
     ([40, 3], [400, 3], 64, 2, 128),                        # group 32: head blocks
 ])
 @pytest.mark.parametrize("waves", [1, 7, 64, 0])
-@pytest.mark.parametrize("flags", [0, ops.ATTN_FUSED_MERGE])
-def test_two_row_blocks(lqs, lks, hq, hkv, bs, waves, flags):
+def test_two_row_blocks(lqs, lks, hq, hkv, bs, waves):
     """Launches whose requests average more query tokens than a 16-row block
     holds run segments of two row blocks (every K/V tile feeds both); the
-    result does not depend on it, nor on the split count or merge path."""
+    result does not depend on it, nor on the split count."""
     step = workloads.make_gqa_step(lqs=lqs, lks=lks, num_q_heads=hq, num_kv_heads=hkv,
                                    block_size=bs, seed=41)
-    check(step, waves, flags)
+    check(step, waves)
 
 
 def test_block_size_not_multiple_of_tile():
@@ -426,8 +422,7 @@ def test_mixed_launch_with_fused_kv_write():
 
 @pytest.mark.parametrize("hq,hkv", [(40, 2), (24, 1), (52, 2)])
 @pytest.mark.parametrize("waves", [7, 64, 0])
-@pytest.mark.parametrize("flags", [0, ops.ATTN_FUSED_MERGE])
-def test_group_above_16_not_a_multiple(hq, hkv, waves, flags):
+def test_group_above_16_not_a_multiple(hq, hkv, waves):
     """Groups of 20, 24 and 26 query heads: the second 16-head block of a kv
     head is part-filled, and split rows past the group must not be merged
     into the next kv head's outputs (the output is pre-filled with a
@@ -441,7 +436,7 @@ def test_group_above_16_not_a_multiple(hq, hkv, waves, flags):
                                         hq, hkv, 128, 16, num_waves=waves)
     out = torch.full(s.q.shape, 7.0, dtype=torch.bfloat16, device=DEV)
     ops.paged_attention_gqa(s.q.to(DEV), s.k_cache.to(DEV), s.v_cache.to(DEV), plan, s.scale,
-                            out=out, flags=flags)
+                            out=out)
     torch.cuda.synchronize()
     err = (out.float().cpu() - oracle(step)).abs().max().item()
     print(f"max-abs err {err:.3e}", flush=True)

@@ -474,3 +474,71 @@ def test_two_host_threads_gqa_and_mla_planning_every_step():
         assert (o.float().cpu() - exp_a).abs().max().item() <= 2e-2
     for o in outs["b"]:
         assert (o.float().cpu() - exp_b).abs().max().item() <= 2e-2
+
+
+def _overflow_ctx(backend, caches, bs):
+    """A context whose device metadata (as a packer attaches it) does not add
+    up: cu_seqlens_q describes 100 query tokens in a 10-token step."""
+    rows = [(0, 5, [3]), (0, 5, [7, 1])]
+    ctx, positions = make_ctx(backend, caches, rows, bs, derived=False)
+    ctx.aia_cu_seqlens_q = torch.tensor([0, 5, 100], dtype=torch.int32, device=DEV)
+    ctx.aia_seqlens_kv = torch.tensor([5, 100], dtype=torch.int32, device=DEV)
+    cos, sin = rope_tables(positions, 128)
+    ctx.cos, ctx.sin = cos.to(DEV), sin.to(DEV)
+    return ctx
+
+
+def _small_gqa(seed):
+    g = torch.Generator().manual_seed(seed)
+    hq, hkv, d, hidden = 4, 2, 128, 256
+    p = "model.layers.0.self_attn."
+    w = {p + "qkv_proj.weight": (torch.randn((hq + 2 * hkv) * d, hidden, generator=g) / 16).bfloat16(),
+         p + "o_proj.weight": (torch.randn(hidden, hq * d, generator=g) / 23).bfloat16()}
+    w = {k: v.to(DEV) for k, v in w.items()}
+    return GqaHipBackend(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, scale=d ** -0.5,
+                         num_layers=1, device=DEV, dtype=torch.bfloat16, w=w), hidden
+
+
+def test_gqa_backend_planner_overflow_is_visible(monkeypatch):
+    """Device metadata that overflows the planner: the attention op's output
+    is all NaN (not uninitialised memory), and with AIA_CHECK_PLAN=1 the
+    step's planning raises the stager contract's ValueError
+    (prefill_input_stager.py:77-81)."""
+    bs = 16
+    hip, hidden = _small_gqa(3)
+    caches = hip.alloc_kv_caches(12, bs)
+    x = (torch.randn(10, hidden) * 0.5).bfloat16().to(DEV)
+    ctx = _overflow_ctx(hip, caches, bs)
+    got = []
+    orig = hip._attn
+
+    def spy(*a, **k):
+        o = orig(*a, **k)
+        got.append(o)
+        return o
+    hip._attn = spy
+    monkeypatch.delenv("AIA_CHECK_PLAN", raising=False)
+    hip.attention(0, x, ctx)
+    torch.cuda.synchronize()
+    assert got[0].shape == (10, 4, 128)
+    assert torch.isnan(got[0].float()).all(), "overflowed plan left output values"
+    hip._attn = orig
+    monkeypatch.setenv("AIA_CHECK_PLAN", "1")
+    ctx2 = _overflow_ctx(hip, caches, bs)
+    with pytest.raises(ValueError, match="overflow"):
+        hip.attention(0, x, ctx2)
+
+
+def test_mla_planner_overflow_fills_nan():
+    """The same for the absorbed-MLA call: its merge pass fills the latent
+    output with NaN when the plan overflowed."""
+    from auto_infer_amd import ops
+    bt = torch.arange(8, dtype=torch.int32, device=DEV).view(2, 4)
+    cu = torch.tensor([0, 5, 100], dtype=torch.int32, device=DEV)
+    kv = torch.tensor([5, 100], dtype=torch.int32, device=DEV)
+    plan = ops.AttentionPlan(bt, cu, kv, 10, 16, 1, 512, 64)
+    q = torch.randn(10, 16, 576, device=DEV).bfloat16()
+    cache = torch.randn(8, 64, 1, 576, device=DEV).bfloat16()
+    out = ops.paged_attention_mla(q, cache, plan, 0.1)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()

@@ -19,12 +19,11 @@ DEV = torch.device("cuda:0")
 TOL = 2e-2
 
 
-def attend(step, flags=0):
+def attend(step):
     plan = ops.AttentionPlan.from_lists(step.block_table, step.cu_seqlens_q, step.seqlens_kv,
                                         step.q.shape[1], step.k_cache.shape[2], step.q.shape[2],
                                         step.k_cache.shape[1])
-    out = ops.paged_attention_gqa(step.q, step.k_cache, step.v_cache, plan, step.scale,
-                                  flags=flags)
+    out = ops.paged_attention_gqa(step.q, step.k_cache, step.v_cache, plan, step.scale)
     torch.cuda.synchronize()
     return out
 
@@ -89,10 +88,26 @@ def test_config2_prefill_chunks_alone_dealt_by_size(fused):
         assert torch.equal(kc.cpu(), exp_k) and torch.equal(vc.cpu(), exp_v)
 
 
-def test_config4_mtp_verify_full():
+@pytest.mark.parametrize("fused", [False, True])
+def test_config4_mtp_verify_full(fused):
+    """configs[3] at full size, with the separate KV write or with the write
+    fused into the attention kernel (the bench's and the backend's default):
+    the caches are bit-exact against the separate write at slot_mapping, and
+    the output within 2e-2 of the oracle on every request."""
     step = workloads.config4_mtp(seed=0, device=DEV)
-    ops.write_kv(step.k_new, step.v_new, step.k_cache, step.v_cache, step.slot_mapping)
-    out = attend(step)
+    if not fused:
+        ops.write_kv(step.k_new, step.v_new, step.k_cache, step.v_cache, step.slot_mapping)
+        out = attend(step)
+    else:
+        ek, ev = step.k_cache.clone(), step.v_cache.clone()
+        ops.write_kv(step.k_new, step.v_new, ek, ev, step.slot_mapping)
+        plan = ops.AttentionPlan.from_lists(step.block_table, step.cu_seqlens_q, step.seqlens_kv,
+                                            32, 8, 128, step.k_cache.shape[1])
+        out = ops.paged_attention_gqa(step.q, step.k_cache, step.v_cache, plan, step.scale,
+                                      key_new=step.k_new, value_new=step.v_new)
+        torch.cuda.synchronize()
+        assert torch.equal(step.k_cache, ek) and torch.equal(step.v_cache, ev), \
+            "fused KV write differs from the write at slot_mapping"
     check_sample(step, out, list(range(16)))
 
 

@@ -1,8 +1,10 @@
 """Compile the gfx950 HIP sources into the package's C-ABI shared library.
 
 Usage: ``python -m auto_infer_amd.csrc.build`` (or ``build()`` from Python).
-Output: ``auto_infer_amd/_lib/libautoinfer_amd.so`` and the packer's host
-extension ``auto_infer_amd/_hostpack*.so``.  Always recompiles.
+Output: ``auto_infer_amd/_lib/libautoinfer_amd.so``, the packer's host
+extension ``auto_infer_amd/_hostpack*.so`` and the bench's HBM probes
+``auto_infer_amd/_lib/libaia_probes.so`` (not part of the product ABI).
+Always recompiles.
 """
 import os
 import subprocess
@@ -14,6 +16,7 @@ PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
 OUT_DIR = os.path.join(PKG, "_lib")
 LIB = os.path.join(OUT_DIR, "libautoinfer_amd.so")
+PROBES = os.path.join(OUT_DIR, "libaia_probes.so")
 SOURCES = ["core.hip", "kv_write.hip", "paged_attention.hip", "noalloc.hip", "pack.hip", "qk_rope.hip",
            "mtp_compact.hip", "mla_pre.hip"]
 
@@ -62,6 +65,12 @@ def build(verbose=False):
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
+    tmp = PROBES + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, os.path.join(HERE, "probes.hip"), "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, PROBES)
     return LIB
 
 

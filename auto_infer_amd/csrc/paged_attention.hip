@@ -897,6 +897,7 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
 
 
 __device__ __forceinline__ u32x4_t as_u4(uint4 v) { return u32x4_t{v.x, v.y, v.z, v.w}; }
+
 __device__ __forceinline__ bf16x8_t as_b8(uint4 v) { return __builtin_bit_cast(bf16x8_t, as_u4(v)); }
 
 // S^T tile (16 keys x 16 rows) += K (16 keys x 32 dims) . Q^T: lane (key n,
@@ -1836,7 +1837,14 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     if (item >= a.hdr[5]) break;                           // uniform over the group
     const int qtok0 = m0.x, nq = m0.y, kvh = m0.z, hbi = m0.w;
     const int row_base = m1.x, np = m1.y, sl = m1.z, rows = m1.w;
-    const int e = sl * 64 + lane;
+    // A slice of fewer than 64 elements (a decode segment's few rows) takes
+    // the smallest power-of-two lane group that holds it, and the wave's
+    // other lane groups fold other partials: all of an item's partial loads
+    // then go out in one round (config 1: 16 elements, 16 partials at once).
+    const int span = rows * epr - sl * 64;
+    const int pw = span > 32 ? 64 : span > 16 ? 32 : span > 8 ? 16 : 8;
+    const int pg = lane / pw, ng = 64 / pw;
+    const int e = sl * 64 + (lane & (pw - 1));
     int n = e / epr;
     const int c = (e - n * epr) * kMergeDims;
     const int rblk = n / kRows, t = (n - rblk * kRows) / a.hb;
@@ -1863,7 +1871,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     };
     if (live) {    // fp16 partials y = O / c, with (m + log2 c, l / c)
 #pragma unroll 2
-      for (int k = kg; k < np; k += kMergeGroups) {
+      for (int k = kg * ng + pg; k < np; k += kMergeGroups * ng) {
         const int64_t pr = row0 + k * pstride;
         const float2 ml = a.part_ml[pr];
         const uint4* src = reinterpret_cast<const uint4*>(
@@ -1880,13 +1888,24 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
         fold(ml, x);
       }
     }
+    // fold the wave's lane groups together (every lane of an element's
+    // groups ends with the wave's result)
+    for (int d = pw; d < 64; d <<= 1) {
+      const float2 oml = make_float2(__shfl_xor(mx, d), __shfl_xor(ls, d));
+      float4 ox[kMergeDims / 4];
+#pragma unroll
+      for (int i = 0; i < kMergeDims / 4; ++i)
+        ox[i] = make_float4(__shfl_xor(acc[i].x, d), __shfl_xor(acc[i].y, d),
+                            __shfl_xor(acc[i].z, d), __shfl_xor(acc[i].w, d));
+      fold(oml, ox);
+    }
     if (kg > 0) {
 #pragma unroll
       for (int i = 0; i < kMergeDims / 4; ++i) sacc[kg - 1][i][lane] = acc[i];
       sml[kg - 1][lane] = make_float2(mx, ls);
     }
     __syncthreads();
-    if (kg == 0 && live) {
+    if (kg == 0 && live && pg == 0) {
 #pragma unroll
       for (int j = 0; j < kMergeGroups - 1; ++j) {
         float4 x[kMergeDims / 4];

@@ -116,7 +116,108 @@ def hbm_sweep():
                     "copy_TBps": round(by / us_copy / 1e6, 2), "rowsum_read_us": round(us_sum, 2),
                     "rowsum_TBps": round(by / us_sum / 1e6, 2)})
         del srcs, dsts
-    print(json.dumps({"hbm_sweep": out}))
+    print(json.dumps({"hbm_sweep": out}), flush=True)
+    print(json.dumps({"hbm_probes": probe_sweep(timeit, L)}), flush=True)
+
+
+def _probe_lib():
+    import ctypes
+    path = os.path.join(ROOT, "auto_infer_amd", "_lib", "libaia_probes.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: run __graft_entry__.build() first")
+    lib = ctypes.CDLL(path)
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    lib.aia_probe_stream_read.argtypes = [vp, i64, i32, i32, i32, vp, vp]
+    lib.aia_probe_paged_gather.argtypes = [vp, vp, vp, i32, vp, i64, i32, i32, i32, i32, i32,
+                                           vp, vp]
+    return lib
+
+
+def config1_ranges(plan, seg_cap):
+    """The key ranges of a config-1 plan, read back from its workspace in
+    work-group order: {request, first key, end key, 0} per record slot
+    (empty slots read nothing).  Record slot layout: int4 {segment, first
+    tile, end tile, tiles per range}, then the segment's 8-int record
+    {request, .., .., .., lim_base, tile_begin, tile_end, ..}."""
+    torch.cuda.synchronize()
+    ws = plan.workspace.cpu().view(torch.int32)
+    waves = int(ws[4])
+    rec_off = (256 + (seg_cap + 1) * 32 + 255) // 256 * 256 // 4
+    recs = ws[rec_off: rec_off + waves * 32].view(waves, 32).tolist()
+    out = []
+    for r in recs:
+        if r[0] < 0:
+            out.append((0, 0, 0, 0))
+            continue
+        t0, t1, b, nq, lim_base, tb = r[1], r[2], r[4], r[7] & 0xff, r[8], r[9]
+        visible = lim_base + nq
+        out.append((b, (t0 - tb) * 16, min((t1 - tb) * 16, visible), 0))
+    return out
+
+
+def probe_sweep(timeit, L):
+    """Hand-written gfx950 read probes (auto_infer_amd/csrc/probes.hip) that
+    set the ceilings the config-1 decode kernel is compared with:
+    - stream_read: a plain read of N bytes with 16-byte loads over all CUs,
+      L rotating buffers past the Infinity Cache, at several grid sizes;
+    - paged_gather: config 1's exact key ranges (read back from a real
+      plan, in work-group order), K and V rows of all 8 kv heads at the
+      block table's slots, no math, no output; and the same keys as one
+      work-group per (request, kv head).
+    Times are per launch (HIP graph of L launches, HIP events, median of 5)."""
+    from auto_infer_amd import ops, workloads
+    dev = torch.device("cuda:0")
+    lib = _probe_lib()
+    stream_ptr = lambda: torch.cuda.current_stream(dev).cuda_stream   # noqa: E731
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+    res = {"stream_read": [], "paged_gather": []}
+    for mb in (72, 288):
+        n = mb << 20
+        bufs = [torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev) for _ in range(L)]
+        for grid, threads, variant in ((512, 512, 0), (1024, 512, 0), (2048, 512, 0),
+                                       (256, 1024, 1), (512, 1024, 1), (512, 512, 1),
+                                       (512, 512, 2), (512, 512, 3), (1024, 256, 1)):
+            def fn():
+                for b in bufs:
+                    rc = lib.aia_probe_stream_read(b.data_ptr(), n, grid, threads, variant,
+                                                   sink.data_ptr(), stream_ptr())
+                    assert rc == 0, rc
+            us = timeit(fn)
+            res["stream_read"].append({"MiB": mb, "work_groups": grid, "threads": threads,
+                                       "loads_in_flight": 16 if variant & 1 else 8,
+                                       "nontemporal": bool(variant & 2), "us": round(us, 2),
+                                       "TBps": round(n / us / 1e6, 3),
+                                       "frac_of_peak": round(n / us / 1e6 / 8.0, 4)})
+        del bufs
+    step = workloads.config1_decode(seed=0)
+    hkv, d, bs = 8, 128, step.k_cache.shape[1]
+    bt = step.block_table.to(dev)
+    cu = torch.tensor([0, *step.cu_seqlens_q], dtype=torch.int32, device=dev)
+    kvl = torch.tensor(step.seqlens_kv, dtype=torch.int32, device=dev)
+    plan = ops.AttentionPlan(bt, cu, kvl, step.num_tokens, 16, hkv, d, bs)
+    ranges = config1_ranges(plan, seg_cap=16 + 2)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    kcs = [torch.randn(step.k_cache.shape, generator=gen, device=dev).bfloat16() for _ in range(L)]
+    vcs = [torch.randn(step.v_cache.shape, generator=gen, device=dev).bfloat16() for _ in range(L)]
+    nbytes = sum(step.seqlens_kv) * hkv * d * 2 * 2
+    per_head = [(b, 0, lk, h) for b, lk in enumerate(step.seqlens_kv) for h in range(hkv)]
+    for name, recs, heads, threads in (
+            ("config-1 ranges, 8 kv heads per work-group", ranges, hkv, 512),
+            ("one work-group per (request, kv head)", per_head, 1, 1024),
+            ("one work-group per (request, kv head), 256 threads", per_head, 1, 256)):
+        rt = torch.tensor(recs, dtype=torch.int32, device=dev)
+        def fn():
+            for i in range(L):
+                rc = lib.aia_probe_paged_gather(kcs[i].data_ptr(), vcs[i].data_ptr(), rt.data_ptr(),
+                                                len(recs), bt.data_ptr(), bt.stride(0), bs, hkv,
+                                                d, heads, threads, sink.data_ptr(), stream_ptr())
+                assert rc == 0, rc
+        us = timeit(fn)
+        res["paged_gather"].append({"pattern": name, "work_groups": len(recs),
+                                    "threads": threads, "MB": round(nbytes / 1e6, 2),
+                                    "us": round(us, 2), "TBps": round(nbytes / us / 1e6, 3),
+                                    "frac_of_peak": round(nbytes / us / 1e6 / 8.0, 4)})
+    return res
 
 
 def cpu_model():

@@ -30,6 +30,8 @@ SIGNATURES = {
                      c_i64, c_vp],
     "aia_attn_workspace_bytes": [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                                  ctypes.POINTER(c_i64)],
+    "aia_attn_workspace_layout": [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                  ctypes.POINTER(c_i64), c_i32],
     "aia_attn_plan": [c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                       c_vp, c_i64, c_vp],
     "aia_paged_attention_gqa": [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp,

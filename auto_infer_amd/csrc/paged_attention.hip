@@ -2345,6 +2345,23 @@ extern "C" int aia_attn_workspace_bytes(int32_t batch, int32_t num_tokens, int32
   return AIA_OK;
 }
 
+extern "C" int aia_attn_workspace_layout(int32_t batch, int32_t num_tokens, int32_t num_q_heads,
+                                         int32_t num_kv_heads, int32_t head_dim_v,
+                                         int32_t num_waves, int64_t* offsets, int32_t count) {
+  if (int rc = check_heads("aia_attn_workspace_layout", num_q_heads, num_kv_heads)) return rc;
+  if (batch < 0 || num_tokens < 0 || head_dim_v <= 0 || !offsets || count < 1)
+    return aia::fail(AIA_ERR_INVALID, "aia_attn_workspace_layout: bad arguments");
+  const Geometry g = geometry(num_q_heads, num_kv_heads, batch, num_tokens, head_dim_v);
+  const int32_t waves = resolve_waves(num_waves, g, head_dim_v);
+  const Layout L = layout(batch, num_tokens, g, head_dim_v, waves);
+  const int64_t v[] = {L.hdr, L.seg, L.wave, L.part_ml, L.part_o, L.req, L.mrg, L.pf, L.pfm,
+                       L.pfw, L.pf_ml, L.pf_o, L.total, L.seg_cap, L.mrg_cap, L.pf_cap,
+                       L.pf_unit_cap, L.pf_mrg_cap, waves, kPfRows, kPfKeys};
+  const int n = (int)(sizeof(v) / sizeof(v[0]));
+  for (int i = 0; i < count; ++i) offsets[i] = i < n ? v[i] : -1;
+  return AIA_OK;
+}
+
 extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
                              const int32_t* block_table, int32_t block_table_stride,
                              int32_t block_size, int32_t batch,

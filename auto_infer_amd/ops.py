@@ -259,6 +259,21 @@ def workspace_bytes(batch, num_tokens, num_q_heads, num_kv_heads, head_dim_v, nu
     return out.value
 
 
+_LAYOUT_KEYS = ("hdr", "seg", "wave", "part_ml", "part_o", "req", "mrg", "pf", "pfm", "pfw",
+                "pf_ml", "pf_o", "total", "seg_cap", "mrg_cap", "pf_cap", "pf_unit_cap",
+                "pf_mrg_cap", "waves", "pf_rows", "pf_keys")
+
+
+def workspace_layout(batch, num_tokens, num_q_heads, num_kv_heads, head_dim_v, num_waves=0):
+    """Byte offsets of a plan's parts in its workspace and the plan's
+    capacities (``aia_attn_workspace_layout``), as a dict: for tools and
+    tests that read a plan back."""
+    vals = (ctypes.c_int64 * len(_LAYOUT_KEYS))()
+    _native.call("aia_attn_workspace_layout", batch, num_tokens, num_q_heads, num_kv_heads,
+                 head_dim_v, num_waves, vals, len(_LAYOUT_KEYS))
+    return dict(zip(_LAYOUT_KEYS, vals))
+
+
 class AttentionPlan:
     """Device metadata + split-K work plan of one step.
 

@@ -58,6 +58,19 @@ int aia_attn_workspace_bytes(int32_t batch, int32_t num_tokens,
                              int32_t num_q_heads, int32_t num_kv_heads,
                              int32_t head_dim_v, int32_t num_waves, int64_t* bytes);
 
+/* Where a plan keeps its parts in the workspace, for tools and tests that
+ * read a plan back (no counterpart in the reference, whose plan is the host
+ * lists themselves).  Writes up to `count` int64 values, -1 past the end:
+ * byte offsets of the header, segment records, range records, split
+ * partials (max/sum, values), request offsets, merge records, prefill unit
+ * records, prefill merge records, dealt prefill work-groups, prefill
+ * partials (max/sum, values) and the total size; then the capacities
+ * (segments, merge records, prefill items, prefill units, prefill merges),
+ * the range count, and the prefill item rows and tile keys. */
+int aia_attn_workspace_layout(int32_t batch, int32_t num_tokens, int32_t num_q_heads,
+                              int32_t num_kv_heads, int32_t head_dim_v, int32_t num_waves,
+                              int64_t* offsets, int32_t count);
+
 /* Split-K work plan for one step: reads the device copies of
  * cu_seqlens_q (batch + 1 entries, leading 0 -- the reference keeps the
  * cumulative ends as a host list, model_runner.py:137 / ForwardContext

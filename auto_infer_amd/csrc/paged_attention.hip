@@ -29,6 +29,8 @@
 #include <math.h>
 
 #include <atomic>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <type_traits>
 
@@ -835,6 +837,183 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int x = w % kXcdsPlan, i = w / kXcdsPlan;
     const bool used = spread ? i < q8 + (x < rem8 ? 1 : 0) : w < nr_used;
     if (!used)
+      *reinterpret_cast<int4*>(wave_rec + (int64_t)w * kRecInts) = make_int4(-1, 0, 0, tpw);
+  }
+}
+
+// Small GQA steps (no prefill routing, at most 64 segments: config-1 and
+// MTP-verify sized batches) are planned by one wave for the per-request and
+// per-segment phases -- DPP scans and lane shuffles, no block barriers and
+// no global round trip between phases -- and then by the whole work-group
+// for the range records.  The plan is the one plan_kernel makes for the
+// same step, record for record (tests compare the two workspaces).
+constexpr int kSmallPlanThreads = 256;
+constexpr int kSmallPlanSegs = 64;
+
+__device__ __forceinline__ int wave_total(int x) {   // sum over the 64 lanes, in every lane
+  return __builtin_amdgcn_readlane(wave_incl_scan(x), 63);
+}
+
+__global__ __launch_bounds__(kSmallPlanThreads) void plan_small_kernel(
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ kvlen,
+    const int32_t* __restrict__ block_table, int64_t bt_stride, int32_t block_size,
+    int32_t batch, Geometry g, int32_t waves, int32_t dv,
+    int32_t* __restrict__ hdr, int32_t* __restrict__ seg, int32_t* __restrict__ wave_rec,
+    int32_t* __restrict__ mrg, int32_t seg_cap) {
+  __shared__ int4 srec[kSmallPlanSegs + 1][2];   // segment records (+ sentinel)
+  __shared__ int sinfo[4];                        // nseg, total tiles, tpw
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int per_req = g.nkvg * g.nhb;
+  if (tid < 64) {
+    // 1) segments per request (lane = request)
+    int c0 = 0, c1 = 0, lk = 0, cnt = 0;
+    if (lane < batch) {
+      c0 = cu_q[lane]; c1 = cu_q[lane + 1]; lk = kvlen[lane];
+      const int lq = c1 - c0;
+      cnt = lq > 0 ? ((lq + g.qs - 1) / g.qs) * per_req : 0;
+    }
+    const int inc = wave_incl_scan(cnt);
+    const int req_off = inc - cnt;
+    int nseg = __builtin_amdgcn_readlane(inc, 63);
+    int overflow = 0;
+    if (nseg > seg_cap || nseg > kSmallPlanSegs) { nseg = 0; overflow = 1; }
+
+    // 2) lane = segment: its request (last b with req_off[b] <= s), record
+    // fields and key tiles
+    const int s = lane;
+    int rec0 = 0, rec1 = 0, rec2 = 0, rec3 = 0, lim_base = 0, nt = 0;
+    {
+      // a fixed number of steps with every lane active, so each shuffle
+      // reads lanes that take part in it
+      int lo = 0, hi = batch - 1;
+#pragma unroll
+      for (int it = 0; it < 6; ++it) {
+        const int mid = (lo + hi + 1) >> 1;
+        const bool le = __shfl(req_off, mid & 63) <= s;
+        if (lo < hi) {
+          if (le) lo = mid; else hi = mid - 1;
+        }
+      }
+      const int b = lo;
+      const int local = s - __shfl(req_off, b);
+      const int q_begin = __shfl(c0, b), lq = __shfl(c1, b) - q_begin, lkb = __shfl(lk, b);
+      if (s < nseg) {
+        const int hb = g.nhb == 1 ? 0 : local % g.nhb;
+        const int kvg = g.nkvg == 1 ? 0 : (local / g.nhb) % g.nkvg;
+        const int qblk = per_req == 1 ? local : local / per_req;
+        const int q0 = qblk * g.qs;
+        const int nq = min(g.qs, lq - q0);
+        lim_base = lkb - lq + q0;
+        const int visible = max(0, min(lkb, lim_base + nq));
+        nt = max(1, (visible + kTile - 1) / kTile);
+        rec0 = b; rec1 = kvg | (hb << 16) | ((q0 + nq == lq) << 30);
+        rec2 = q_begin + q0; rec3 = nq | (q0 << 8);
+      }
+    }
+    const int real_tiles = wave_total(nt);
+    // range length, padding as in plan_kernel
+    int tpw = max(1, (real_tiles + waves - 1) / waves);
+    const bool pad = 2 * nseg <= waves && tpw < kPadBelow;
+    const int pw = (pad && 2 * nseg <= waves * 7 / 8) ? waves * 7 / 8 : waves;
+    if (pad) {
+      tpw = max(1, (real_tiles + pw - 1) / pw);
+      int hi = max(1, (real_tiles + pw - nseg - 1) / (pw - nseg));
+      while (tpw < hi) {
+        const int mid = (tpw + hi) >> 1;
+        const int tot = wave_total(s < nseg ? (nt + mid - 1) / mid : 0);
+        if (tot <= pw) hi = mid; else tpw = mid + 1;
+      }
+    }
+    const int span = s < nseg ? (pad ? (nt + tpw - 1) / tpw * tpw : nt) : 0;
+    const int tinc = wave_incl_scan(span);
+    const int tb = tinc - span;
+    const int total_tiles = __builtin_amdgcn_readlane(tinc, 63);
+
+    // 3) partial slots and merge records
+    int np = 0, mcnt = 0, nwv = 0, nsl = 0, rows = 0;
+    if (s < nseg) {
+      np = (tb + nt - 1) / tpw - tb / tpw + 1;
+      if (np > 1) {
+        const int nq = rec3 & 0xff;
+        const int nblk = (nq + g.qb - 1) / g.qb;
+        rows = (nblk - 1) * kRows + min(kRows, (nq - (nblk - 1) * g.qb) * g.hb);
+        nwv = min(g.nw, g.hkv - (rec1 & 0xffff) * g.nw);
+        nsl = (rows * (dv / kMergeDims) + 63) / 64;
+        mcnt = nwv * nsl;
+      }
+    }
+    const int pinc = wave_incl_scan(np), minc = wave_incl_scan(mcnt);
+    const int part_base = pinc - np, mbase = minc - mcnt;
+    const int nparts = __builtin_amdgcn_readlane(pinc, 63);
+    const int nmrg = __builtin_amdgcn_readlane(minc, 63);
+    if (s < nseg) {
+      const int4 r0 = make_int4(rec0, rec1, rec2, rec3);
+      const int4 r1 = make_int4(lim_base, tb, tb + nt, part_base);
+      int4* r = reinterpret_cast<int4*>(seg + (int64_t)s * 8);
+      r[0] = r0; r[1] = r1;
+      srec[s][0] = r0; srec[s][1] = r1;
+      const int seg_rows = kRows * g.rb;
+      int4* m = reinterpret_cast<int4*>(mrg + (int64_t)mbase * kMrgInts);
+      for (int w = 0; w < nwv; ++w)
+        for (int sl = 0; sl < nsl; ++sl, m += kMrgInts / 4) {
+          m[0] = make_int4(rec2, rec3 & 0xff, (rec1 & 0xffff) * g.nw + w, (rec1 >> 16) & 0x3fff);
+          m[1] = make_int4((part_base * g.nw + w) * seg_rows, np, sl, rows);
+        }
+    }
+    if (lane == 0) {
+      hdr[0] = nseg; hdr[1] = total_tiles; hdr[2] = tpw; hdr[3] = nparts; hdr[4] = waves;
+      hdr[5] = nmrg; hdr[6] = 0; hdr[7] = 0;
+      hdr[8] = overflow ? -1 : 0;
+      hdr[9] = 0;
+      int4* r = reinterpret_cast<int4*>(seg + (int64_t)nseg * 8);   // sentinel
+      r[0] = make_int4(0, 0, 0, 0);
+      r[1] = make_int4(0, total_tiles, total_tiles, nparts);
+      srec[nseg][1] = make_int4(0, total_tiles, total_tiles, nparts);
+      sinfo[0] = nseg; sinfo[1] = total_tiles; sinfo[2] = tpw;
+    }
+  }
+  __syncthreads();
+
+  // 4) range records, spread over the XCDs as plan_kernel places them
+  const int nseg = sinfo[0], total_tiles = sinfo[1], tpw = sinfo[2];
+  const int nr_used = min(waves, (total_tiles + tpw - 1) / tpw);
+  const int q8 = nr_used / kXcdsPlan, rem8 = nr_used - q8 * kXcdsPlan;
+  for (int r = tid; r < nr_used && nseg > 0; r += kSmallPlanThreads) {
+    const int t0 = r * tpw;
+    const int t1 = min(total_tiles, t0 + tpw);
+    int lo = 0, hi = nseg - 1;     // last s with tile_begin <= t0
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (srec[mid][1].y <= t0) lo = mid; else hi = mid - 1;
+    }
+    int lo2 = lo, hi2 = nseg - 1;  // last s with tile_begin < t1
+    while (lo2 < hi2) {
+      const int mid = (lo2 + hi2 + 1) >> 1;
+      if (srec[mid][1].y < t1) lo2 = mid; else hi2 = mid - 1;
+    }
+    const int4 r0 = srec[lo][0], r1 = srec[lo][1];
+    const int b = r0.x, nq = r0.w & 0xff;
+    const int nblk_vis = (max(0, r1.x + nq) + block_size - 1) / block_size;
+    const int blk_base = ((t0 - r1.y) * kTile) / block_size;
+    const int32_t* btrow = block_table + (int64_t)b * bt_stride;
+    int bv[kRecBlocks];
+#pragma unroll
+    for (int i = 0; i < kRecBlocks; ++i) bv[i] = blk_base + i < nblk_vis ? btrow[blk_base + i] : 0;
+    const int big = (q8 + 1) * rem8;
+    const int x = r < big ? r / (q8 + 1) : rem8 + (r - big) / q8;
+    const int i8 = r < big ? r - x * (q8 + 1) : r - big - (x - rem8) * q8;
+    int4* o4 = reinterpret_cast<int4*>(wave_rec + (int64_t)(i8 * kXcdsPlan + x) * kRecInts);
+    o4[0] = make_int4(lo, t0, t1, tpw);
+    o4[1] = r0;
+    o4[2] = r1;
+    o4[3] = make_int4(blk_base, lo2, 0, 0);
+#pragma unroll
+    for (int i = 0; i < kRecBlocks / 4; ++i)
+      o4[4 + i] = make_int4(bv[4 * i], bv[4 * i + 1], bv[4 * i + 2], bv[4 * i + 3]);
+  }
+  for (int w = tid; w < waves; w += kSmallPlanThreads) {     // slots no range maps to
+    const int x = w % kXcdsPlan, i = w / kXcdsPlan;
+    if (nseg == 0 || i >= q8 + (x < rem8 ? 1 : 0))
       *reinterpret_cast<int4*>(wave_rec + (int64_t)w * kRecInts) = make_int4(-1, 0, 0, tpw);
   }
 }
@@ -2325,6 +2504,18 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
   return aia::check_hip(hipGetLastError(), "merge_kernel launch");
 }
 
+// The small planner takes GQA steps without prefill routing whose segments
+// fit one wave (AIA_PLANNER=large in the environment, read once, sends every
+// step to plan_kernel: for comparisons).
+bool small_plan(const Geometry& g, int32_t dv, int32_t batch, const Layout& L) {
+  static const bool force_large = [] {
+    const char* e = getenv("AIA_PLANNER");
+    return e && strcmp(e, "large") == 0;
+  }();
+  return !force_large && dv != 512 && !g.pf && batch >= 1 && batch <= 64 &&
+         L.seg_cap <= kSmallPlanSegs && L.pf_cap == 0;
+}
+
 int check_heads(const char* fn, int32_t hq, int32_t hkv) {
   if (hq <= 0 || hkv <= 0 || hq % hkv != 0)
     return aia::fail(AIA_ERR_INVALID, "%s: num_q_heads %d must be a positive multiple of num_kv_heads %d",
@@ -2385,6 +2576,14 @@ extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens
     return fail(AIA_ERR_CAPACITY, "aia_attn_plan: workspace %lld bytes < %lld needed",
                 (long long)workspace_bytes, (long long)L.total);
   char* ws = static_cast<char*>(workspace);
+  if (small_plan(g, head_dim_v, batch, L)) {
+    plan_small_kernel<<<1, kSmallPlanThreads, 0, (hipStream_t)stream>>>(
+        cu_seqlens_q, seqlens_kv, block_table, block_table_stride, block_size, batch, g, waves,
+        head_dim_v, reinterpret_cast<int32_t*>(ws + L.hdr),
+        reinterpret_cast<int32_t*>(ws + L.seg), reinterpret_cast<int32_t*>(ws + L.wave),
+        reinterpret_cast<int32_t*>(ws + L.mrg), (int32_t)L.seg_cap);
+    return check_hip(hipGetLastError(), "aia_attn_plan launch");
+  }
   plan_kernel<<<1, kPlanThreads, 0, (hipStream_t)stream>>>(
       cu_seqlens_q, seqlens_kv, block_table, block_table_stride, block_size, batch, g, waves,
       head_dim_v, reinterpret_cast<int32_t*>(ws + L.hdr),

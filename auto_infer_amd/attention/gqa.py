@@ -64,7 +64,8 @@ class GqaHipBackend(AttentionBackend):
         if self._fusable(qkv, ctx):
             q, k, v = ops.qk_norm_rope(qkv, n_q, n_kv, ctx.cos, ctx.sin, qn,
                                        w.get(p + "k_norm.weight") if qn is not None else None,
-                                       self.rms_eps if self.rms_eps is not None else 1e-6)
+                                       self.rms_eps if self.rms_eps is not None else 1e-6,
+                                       head_dim=hd)
         else:
             q, k, v = qkv.split((n_q * hd, n_kv * hd, n_kv * hd), dim=-1)
             q = q.view(T, n_q, hd)
@@ -83,9 +84,10 @@ class GqaHipBackend(AttentionBackend):
         T = qkv.shape[0]
         def aligned(t):          # 16-byte accesses: 8-element strides, 16-byte base
             return t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
-        return (self.fuse_pre_attention and self.head_dim == 128 and qkv.dtype == torch.bfloat16
+        hd = self.head_dim
+        return (self.fuse_pre_attention and hd in (128, 64) and qkv.dtype == torch.bfloat16
                 and qkv.is_cuda and qkv.stride(-1) == 1 and aligned(qkv)
-                and all(t.dtype == torch.bfloat16 and t.numel() == T * 128 and t.stride(-1) == 1
+                and all(t.dtype == torch.bfloat16 and t.numel() == T * hd and t.stride(-1) == 1
                         and aligned(t) for t in (ctx.cos, ctx.sin)))
 
     def _write_kv(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor, ctx) -> None:

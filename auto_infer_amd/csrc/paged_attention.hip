@@ -147,7 +147,7 @@ Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_
   // rows: with at least one query token per request, none holds more than
   // tokens - batch + 1.  (The planner routes nothing when this says no, so a
   // batch that breaks the assumption still runs, on split-K.)
-  g.pf = (AIA_PREFILL && dv == kHeadDim && batch > 0 &&
+  g.pf = (AIA_PREFILL && (dv == kHeadDim || dv == 64) && batch > 0 &&
           ((int64_t)tokens - batch + 1) * g.group >= kPfRows) ? 1 : 0;
   // with prefill routing, requests with many query rows leave the split-K
   // kernel, whose segments are then decode / short-verify sized
@@ -208,7 +208,7 @@ Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int3
   L.pfm = off;      off = align256(off + L.pf_mrg_cap * 16);
   L.pfw = off;      off = align256(off + (g.pf ? kPfTargetWgs * 48 : 0));   // dealt work-groups
   L.pf_ml = off;    off = align256(off + L.pf_slots * kPfRows * 8);
-  L.pf_o = off;     off = align256(off + L.pf_slots * kPfRows * (int64_t)kHeadDim * 2);
+  L.pf_o = off;     off = align256(off + L.pf_slots * kPfRows * (int64_t)dv * 2);
   L.total = off;
   return L;
 }
@@ -1446,11 +1446,10 @@ struct PrefillArgs {
   int32_t part_units;        // units the partial buffer holds
 };
 
-// LDS rows of the staged K and V tiles are 256 bytes, unpadded: the direct
+// LDS rows of the staged K and V tiles are 2 D bytes, unpadded: the direct
 // loads write whole 1 KB runs, so the chunks of each row are swizzled
 // instead (see the loader).
-constexpr int kKStride = kHeadDim;
-constexpr int kPfVStride = kHeadDim;
+constexpr int kKStride = kHeadDim;   // the mixed kernel's (D = 128) buffer rows
 #ifndef AIA_PF_LAZY
 #define AIA_PF_LAZY 8.0f
 #endif
@@ -1501,10 +1500,13 @@ constexpr float kLazyLog2 = AIA_PF_LAZY;              // max growth (log2) befor
 #ifndef AIA_PF_WPE
 #define AIA_PF_WPE 2
 #endif
-template <bool ONE_BLOCK, bool FUSED>
+template <bool ONE_BLOCK, bool FUSED, int D>
 __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
                                                  uint16_t* k0, uint16_t* k1,
                                                  uint16_t* v0, uint16_t* v1) {
+  constexpr int KJ = D / 32;        // 32-dim MFMA k-steps
+  constexpr int DT = D / 16;        // 16-dim output tiles
+  constexpr int RC = D / 8;         // 16-byte chunks per K / V row
   // The planner writes work-group b's record at dealt[b] when the
   // work-groups fit the fill target (hdr[9] = their number; dealt by size, or
   // in xcd_range order); it is loaded beside the header rather than after
@@ -1547,24 +1549,24 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int row_elems = a.hkv * kHeadDim;
+  const int row_elems = a.hkv * D;
   const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
 
   // new K/V rows of the tokens whose first row lies in this item (written by
   // the item's first chunk)
   if (FUSED && t0 == 0) {
     const int t_lo = (row0 + G - 1) / G, t_hi = min(lq, (row_end - 1) / G + 1);
-    for (int e = tid; e < (t_hi - t_lo) * 16; e += kPfWaves * 64) {
-      const int t = t_lo + (e >> 4), c = e & 15;
+    for (int e = tid; e < (t_hi - t_lo) * RC; e += kPfWaves * 64) {
+      const int t = t_lo + e / RC, c = e % RC;
       const int p = ctx0 + t;
       if (p < 0) continue;
       const int blk = min(max(btrow[p / a.bs], 0), a.nb - 1);
-      const int64_t dst = ((int64_t)blk * a.bs + p % a.bs) * row_elems + (int64_t)kvh * kHeadDim;
+      const int64_t dst = ((int64_t)blk * a.bs + p % a.bs) * row_elems + (int64_t)kvh * D;
       const int64_t tok = q_begin + t;
       reinterpret_cast<uint4*>(a.kc + dst)[c] =
-          reinterpret_cast<const uint4*>(a.kn + tok * a.kn_ts + (int64_t)kvh * kHeadDim)[c];
+          reinterpret_cast<const uint4*>(a.kn + tok * a.kn_ts + (int64_t)kvh * D)[c];
       reinterpret_cast<uint4*>(a.vc + dst)[c] =
-          reinterpret_cast<const uint4*>(a.vn + tok * a.vn_ts + (int64_t)kvh * kHeadDim)[c];
+          reinterpret_cast<const uint4*>(a.vn + tok * a.vn_ts + (int64_t)kvh * D)[c];
     }
   }
 
@@ -1586,17 +1588,17 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     wlim_lo = min(wlim_lo, __shfl_xor(wlim_lo, d));
     wlim_hi = max(wlim_hi, __shfl_xor(wlim_hi, d));
   }
-  uint4 qf[kPfRt][4];
+  uint4 qf[kPfRt][KJ];
 #pragma unroll
   for (int rt = 0; rt < kPfRt; ++rt) {
     if (rv[rt]) {
       const uint4* qp = reinterpret_cast<const uint4*>(
           a.q + (int64_t)(q_begin + tokr[rt]) * a.q_ts + (int64_t)headr[rt] * a.q_hs);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) qf[rt][j] = qp[4 * j + g];
+      for (int j = 0; j < KJ; ++j) qf[rt][j] = qp[4 * j + g];
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) qf[rt][j] = make_uint4(0, 0, 0, 0);
+      for (int j = 0; j < KJ; ++j) qf[rt][j] = make_uint4(0, 0, 0, 0);
     }
   }
 
@@ -1609,13 +1611,14 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
   const bool whole = t0 == 0 && t1 == ntiles;
   if (!whole && unit >= a.part_units) return;
 
-  // Loader: thread tid moves 16-byte chunk (tid % 16) of keys kLdKeys i + tid / 16
-  // straight from global memory into LDS (no registers, no LDS stores).  Each
-  // wave's load writes one 1 KB run, four key rows of 256 bytes with lane l at
-  // byte 16 l; lane l fetches the chunk whose swizzled place that is: K chunk
-  // c of key r sits at c ^ (r % 16) and V chunk c at c ^ 2 (r % 8), so the K
-  // fragment reads (16 keys, one chunk each) and the V^T transposing reads (8
-  // keys, 32 bytes each) hit distinct banks without padded rows.
+  // Loader: thread tid moves 16-byte chunk (tid % RC) of keys kLdKeys i + tid / RC
+  // (RC = D / 8 chunks per row) straight from global memory into LDS (no
+  // registers, no LDS stores).  Each wave's load writes one 1 KB run, 1024 /
+  // (2 D) key rows of 2 D bytes with lane l at byte 16 l; lane l fetches the
+  // chunk whose swizzled place that is: K chunk c of key r sits at
+  // c ^ (r % RC) and V chunk c at c ^ 2 (r % (RC / 2)), so the K fragment
+  // reads (16 keys, one chunk each) and the V^T transposing reads (8 keys, 32
+  // bytes each) spread over the banks without padded rows.
   // When the block size is a multiple of the tile, a tile lies in one block
   // and a key's address is one multiply-add: lane l of every wave holds the
   // block id of tile tb + l, fetched 64 tiles at a time, and a tile takes its
@@ -1625,13 +1628,14 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
   // in flight during a tile's math.  Keys past the last visible one re-read
   // it (never a slot that may hold stale bytes); keys at this step's new
   // positions come from the new rows.
-  const int lkey = tid >> 4, lc = tid & 15;
-  const int64_t kvoff = (int64_t)kvh * kHeadDim;
+  const int lkey = tid / RC, lc = tid % RC;
+  const int64_t kvoff = (int64_t)kvh * D;
   const uint16_t* kcb = a.kc + kvoff;
   const uint16_t* vcb = a.vc + kvoff;
   const uint16_t* knb = FUSED ? a.kn + kvoff : nullptr;
   const uint16_t* vnb = FUSED ? a.vn + kvoff : nullptr;
-  constexpr int kLdKeys = kPfWaves * 4;                // keys per loader round
+  constexpr int kWaveKeys = 64 / RC;                   // key rows per wave per round
+  constexpr int kLdKeys = kPfWaves * kWaveKeys;        // keys per loader round
   constexpr int kLdRounds = kPfKeys / kLdKeys;
   static_assert(kLdKeys % 16 == 0 && kPfKeys % kLdKeys == 0,
                 "loader rounds of whole 16-key swizzle groups");
@@ -1661,9 +1665,10 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
       kp = fresh ? knb + tok * a.kn_ts : kp;
       vp = fresh ? vnb + tok * a.vn_ts : vp;
     }
-    const int rb = (kLdKeys * i + 4 * wid) * kHeadDim;     // the wave's first row
-    lds_load16(kp + 8 * (lc ^ (lkey & 15)), kdst + rb);   // rounds start at multiples of 16 keys
-    lds_load16(vp + 8 * (lc ^ (2 * (lkey & 7))), vdst + rb);
+    const int rb = (kLdKeys * i + kWaveKeys * wid) * D;     // the wave's first row
+    // (rounds start at multiples of 16 keys, so lkey stands for the key mod RC)
+    lds_load16(kp + 8 * (lc ^ (lkey & (RC - 1))), kdst + rb);
+    lds_load16(vp + 8 * (lc ^ (2 * (lkey & (RC / 2 - 1)))), vdst + rb);
   };
   auto load = [&](int t, auto buf_tag) {
     constexpr int B = decltype(buf_tag)::value;
@@ -1689,12 +1694,12 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     }
   };
 
-  float4_t o[kPfRt][8];
+  float4_t o[kPfRt][DT];
   float m[kPfRt], lsum[kPfRt];
 #pragma unroll
   for (int rt = 0; rt < kPfRt; ++rt) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[rt][dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < DT; ++dt) o[rt][dt] = float4_t{0.f, 0.f, 0.f, 0.f};
     m[rt] = -INFINITY;
     lsum[rt] = 0.f;
   }
@@ -1719,23 +1724,23 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     __builtin_amdgcn_sched_barrier(0);     // the block below is scheduled on its own
 #pragma unroll
     for (int st = 0; st < kSt; ++st) {
-      uint4 kf[4];
+      uint4 kf[KJ];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        kf[j] = *reinterpret_cast<const uint4*>(kt + (16 * st + n) * kKStride + 8 * ((4 * j + g) ^ n));
+      for (int j = 0; j < KJ; ++j)
+        kf[j] = *reinterpret_cast<const uint4*>(kt + (16 * st + n) * D + 8 * ((4 * j + g) ^ (n & (RC - 1))));
 #pragma unroll
       for (int rt = 0; rt < kPfRt; ++rt) {
         // (a row tile with no valid row computes rows that are never written)
         acc[rt][st] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[rt][st] = qk_step(kf[j], qf[rt][j], acc[rt][st]);
+        for (int j = 0; j < KJ; ++j) acc[rt][st] = qk_step(kf[j], qf[rt][j], acc[rt][st]);
       }
     }
-    __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4 * kPfQkAhead, 0);
+    __builtin_amdgcn_sched_group_barrier(kSgDsRead, KJ * kPfQkAhead, 0);
 #pragma unroll
     for (int st = 0; st < kSt; ++st) {
-      __builtin_amdgcn_sched_group_barrier(kSgMfma, 4 * kPfRt, 0);
-      if (st + kPfQkAhead < kSt) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(kSgMfma, KJ * kPfRt, 0);
+      if (st + kPfQkAhead < kSt) __builtin_amdgcn_sched_group_barrier(kSgDsRead, KJ, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     issue_next();
@@ -1782,7 +1787,7 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
         const float alpha = __builtin_amdgcn_exp2f(m[rt] - msub);
         lsum[rt] = lsum[rt] * alpha + psum;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[rt][dt] *= alpha;
+        for (int dt = 0; dt < DT; ++dt) o[rt][dt] *= alpha;
       } else {
         lsum[rt] += psum;
       }
@@ -1802,12 +1807,13 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     // transposing read as in vt_frag).
     const int vrow = 4 * g + (n >> 2);
 #pragma unroll
-    for (int f = 0; f < kSt / 2 * 8; ++f) {
-      const int pp = f >> 3, dt = f & 7;
+    for (int f = 0; f < kSt / 2 * DT; ++f) {
+      const int pp = f / DT, dt = f % DT;
+      const int vsw = 16 * (dt ^ (vrow & (RC / 2 - 1)));
       const short4_t x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_short4_t*)(vt + (32 * pp + vrow) * kPfVStride + 16 * (dt ^ (vrow & 7)) + 4 * (n & 3)));
+          (lds_short4_t*)(vt + (32 * pp + vrow) * D + vsw + 4 * (n & 3)));
       const short4_t x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_short4_t*)(vt + (32 * pp + 16 + vrow) * kPfVStride + 16 * (dt ^ (vrow & 7)) + 4 * (n & 3)));
+          (lds_short4_t*)(vt + (32 * pp + 16 + vrow) * D + vsw + 4 * (n & 3)));
       const bf16x8_t va = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
       for (int rt = 0; rt < kPfRt; ++rt)
@@ -1815,9 +1821,9 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     }
     __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2 * kPfPvAhead, 0);
 #pragma unroll
-    for (int f = 0; f < kSt / 2 * 8; ++f) {
+    for (int f = 0; f < kSt / 2 * DT; ++f) {
       __builtin_amdgcn_sched_group_barrier(kSgMfma, kPfRt, 0);
-      if (f + kPfPvAhead < kSt / 2 * 8) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+      if (f + kPfPvAhead < kSt / 2 * DT) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -1884,7 +1890,7 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     float cmax = 0.f;
     if (!whole) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) cmax = fmaxf(cmax, fabsf(o[rt][dt][v]));
       cmax = aia::group4_max(cmax);
@@ -1893,9 +1899,9 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     if (!whole) {
       const float c = cmax > 0.f ? cmax : 1.f, ic = 1.f / c;
       const int64_t prow = ((int64_t)unit * a.hkv + kvh) * kPfRows + (wid * kPfRt + rt) * kRows + n;
-      uint16_t* pp = a.part_o + prow * kHeadDim;
+      uint16_t* pp = a.part_o + prow * D;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
+      for (int dt = 0; dt < DT; ++dt) {
         uint2 hv;
         hv.x = pack_f16x2(o[rt][dt][0] * ic, o[rt][dt][1] * ic);
         hv.y = pack_f16x2(o[rt][dt][2] * ic, o[rt][dt][3] * ic);
@@ -1907,7 +1913,7 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     const float inv = lsum[rt] > 0.f ? 1.f / lsum[rt] : 0.f;
     uint16_t* op = a.out + (int64_t)(q_begin + tokr[rt]) * a.o_ts + (int64_t)headr[rt] * a.o_hs;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
+    for (int dt = 0; dt < DT; ++dt) {
       uint2 wv;
       wv.x = aia::pack_bf16x2(o[rt][dt][0] * inv, o[rt][dt][1] * inv);
       wv.y = aia::pack_bf16x2(o[rt][dt][2] * inv, o[rt][dt][3] * inv);
@@ -1916,14 +1922,14 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
   }
 }
 
-template <bool ONE_BLOCK, bool FUSED>
+template <bool ONE_BLOCK, bool FUSED, int D>
 __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(AIA_PF_WPE, AIA_PF_WPE)))
 void gqa_prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t k0[kPfKeys * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t k1[kPfKeys * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t v0[kPfKeys * kPfVStride];
-  __shared__ __attribute__((aligned(16))) uint16_t v1[kPfKeys * kPfVStride];
-  gqa_prefill_body<ONE_BLOCK, FUSED>(a, blockIdx.x, k0, k1, v0, v1);
+  __shared__ __attribute__((aligned(16))) uint16_t k0[kPfKeys * D];
+  __shared__ __attribute__((aligned(16))) uint16_t k1[kPfKeys * D];
+  __shared__ __attribute__((aligned(16))) uint16_t v0[kPfKeys * D];
+  __shared__ __attribute__((aligned(16))) uint16_t v1[kPfKeys * D];
+  gqa_prefill_body<ONE_BLOCK, FUSED, D>(a, blockIdx.x, k0, k1, v0, v1);
 }
 
 // Mixed steps (prefill items beside split-K decode ranges) in one grid, for
@@ -1944,8 +1950,8 @@ __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(A
 void gqa_mixed_kernel(AttnArgs a, PrefillArgs pa, int npf) {
   __shared__ __attribute__((aligned(16))) uint16_t k0[kMixedK0];
   __shared__ __attribute__((aligned(16))) uint16_t k1[kPfKeys * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t v0[kPfKeys * kPfVStride];
-  __shared__ __attribute__((aligned(16))) uint16_t v1[kPfKeys * kPfVStride];
+  __shared__ __attribute__((aligned(16))) uint16_t v0[kPfKeys * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t v1[kPfKeys * kKStride];
   // Prefill units take the first npf block ids and the decode ranges the
   // rest: the units are dealt out first, one or two per CU, and the ranges
   // fill the remaining slots and every slot a unit frees.  (Alternating the
@@ -1955,7 +1961,7 @@ void gqa_mixed_kernel(AttnArgs a, PrefillArgs pa, int npf) {
   const bool prefill = b < npf;
   const int idx = prefill ? b : b - npf;
   if (prefill)
-    gqa_prefill_body<ONE_BLOCK, FUSED>(pa, idx, k0, k1, v0, v1);
+    gqa_prefill_body<ONE_BLOCK, FUSED, kHeadDim>(pa, idx, k0, k1, v0, v1);
   else
     gqa_attn_body<kPfWaves, 1, kHeadDim>(a, idx,
                                          reinterpret_cast<uint16_t(*)[kTile * kVStride]>(&k0[0]));
@@ -2000,7 +2006,10 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int64_t pstride = (int64_t)a.nw * seg_rows;
   // the first prefill record and the count go out with the first split-K
   // record, so a prefill work-group's chain is record, then partials
-  constexpr int kSlices = kPfRows / 16;
+  // prefill chunk merges: a thread takes 8 dims of a row, so a pass of the
+  // work-group covers 2048 / dv rows (16 at head_dim 128, 32 at 64)
+  const int pf_tpr = a.dv / 8, pf_rpp = 256 / pf_tpr;
+  const int kSlices = kPfRows / pf_rpp;
   const int per_rec = a.hkv * kSlices;
   // planner status, read now and used at the end (no extra round trip)
   const int status = a.hdr[8];
@@ -2108,7 +2117,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     __syncthreads();
   }
 
-  // Prefill chunk merges, one work item per (record, kv head, 16 rows):
+  // Prefill chunk merges, one work item per (record, kv head, pf_rpp rows):
   // thread (row r, 8 dims) folds the record's fp16 partials (scaled per row,
   // see the prefill kernel) with the same rule, 8 at a time so a batch costs
   // one round trip.
@@ -2119,7 +2128,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     const int kvh = rem / kSlices, slice = rem - kvh * kSlices;
     const int4 r = it == blockIdx.x ? pr0 : a.pf_mrg[rec];
     const int q_begin = r.x, row0 = r.y, u0 = r.z, k = r.w & 0xffff, rows = r.w >> 16;
-    const int rl = slice * 16 + (threadIdx.x >> 4), c = (threadIdx.x & 15) * 8;
+    const int rl = slice * pf_rpp + (int)threadIdx.x / pf_tpr, c = ((int)threadIdx.x % pf_tpr) * 8;
     const int row = row0 + rl;
     if (rl >= rows) continue;
     float4 acc[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
@@ -2132,7 +2141,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
         if (j0 + j >= k) break;                    // k is the same for the whole work-group
         const int64_t prow = ((int64_t)(u0 + j0 + j) * a.hkv + kvh) * kPfRows + rl;
         ml[j] = a.pf_ml[prow];
-        const uint4 h = *reinterpret_cast<const uint4*>(a.pf_o + prow * kHeadDim + c);
+        const uint4 h = *reinterpret_cast<const uint4*>(a.pf_o + prow * a.dv + c);
         const half2_t h0 = __builtin_bit_cast(half2_t, h.x), h1 = __builtin_bit_cast(half2_t, h.y);
         const half2_t h2 = __builtin_bit_cast(half2_t, h.z), h3 = __builtin_bit_cast(half2_t, h.w);
         x[j][0] = make_float4((float)h0[0], (float)h0[1], (float)h1[0], (float)h1[1]);
@@ -2493,10 +2502,11 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
   mg.mrg = reinterpret_cast<const int32_t*>(ws + L.mrg); mg.mrg_cap = L.mrg_cap;
   const bool pf = L.pf_mrg_cap > 0;
   mg.pf_mrg = pf ? reinterpret_cast<const int4*>(ws + L.pfm) : nullptr;
-  mg.pf_items_cap = L.pf_mrg_cap * g.hkv * (kPfRows / 16);
+  const int64_t pf_slices = (int64_t)kPfRows * dv / 2048;   // see merge_kernel
+  mg.pf_items_cap = L.pf_mrg_cap * g.hkv * pf_slices;
   mg.pf_o = reinterpret_cast<const uint16_t*>(ws + L.pf_o);
   mg.pf_ml = reinterpret_cast<const float2*>(ws + L.pf_ml);
-  const int64_t pitems = pf ? L.pf_mrg_cap * g.hkv * (kPfRows / 16) : 0;
+  const int64_t pitems = pf ? L.pf_mrg_cap * g.hkv * pf_slices : 0;
   const int64_t items = L.mrg_cap > pitems ? L.mrg_cap : pitems;
   int64_t mgrid = items < 2048 ? items : 2048;
   if (mgrid < 1) mgrid = 1;
@@ -2709,10 +2719,14 @@ extern "C" int aia_paged_attention_gqa(
     if (int rc = check_hip(hipGetLastError(), "gqa_attn_kernel launch")) return rc;
     if (L.pf_cap > 0) {
       const dim3 grid((unsigned)(L.pf_unit_cap * g.hkv));
-      if (one_block && pa.kn) gqa_prefill_kernel<true, true><<<grid, kPfWaves * 64, 0, s>>>(pa);
-      else if (one_block) gqa_prefill_kernel<true, false><<<grid, kPfWaves * 64, 0, s>>>(pa);
-      else if (pa.kn) gqa_prefill_kernel<false, true><<<grid, kPfWaves * 64, 0, s>>>(pa);
-      else gqa_prefill_kernel<false, false><<<grid, kPfWaves * 64, 0, s>>>(pa);
+#define AIA_PF_LAUNCH(D)                                                                   \
+  (one_block && pa.kn ? gqa_prefill_kernel<true, true, D><<<grid, kPfWaves * 64, 0, s>>>(pa)   \
+   : one_block        ? gqa_prefill_kernel<true, false, D><<<grid, kPfWaves * 64, 0, s>>>(pa)  \
+   : pa.kn            ? gqa_prefill_kernel<false, true, D><<<grid, kPfWaves * 64, 0, s>>>(pa)  \
+                      : gqa_prefill_kernel<false, false, D><<<grid, kPfWaves * 64, 0, s>>>(pa))
+      if (head_dim == 64) AIA_PF_LAUNCH(64);
+      else AIA_PF_LAUNCH(kHeadDim);
+#undef AIA_PF_LAUNCH
       if (int rc = check_hip(hipGetLastError(), "gqa_prefill_kernel launch")) return rc;
     }
   }

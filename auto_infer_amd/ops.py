@@ -47,12 +47,13 @@ def _row_stride(t, name):
 # ---------------------------------------------------------------- KV write
 
 def qk_norm_rope(qkv, num_q_heads, num_kv_heads, cos, sin, q_norm_weight=None,
-                 k_norm_weight=None, eps=1e-6):
+                 k_norm_weight=None, eps=1e-6, head_dim=128):
     """Fused pre-attention over a packed qkv projection, in place: optional
     per-head RMSNorm of the Q and K heads (Qwen3 QK-Norm) and NeoX RoPE with
-    ``cos``/``sin`` of shape (T, 1, 128) or (T, 128).  Returns the (q, k, v)
-    views of ``qkv`` -- (T, Hq, 128), (T, Hkv, 128), (T, Hkv, 128) -- ready
-    for ``paged_attention_gqa(q, ..., key_new=k, value_new=v)``.
+    ``cos``/``sin`` of shape (T, 1, D) or (T, D), D = ``head_dim`` (128 or
+    64).  Returns the (q, k, v) views of ``qkv`` -- (T, Hq, D), (T, Hkv, D),
+    (T, Hkv, D) -- ready for ``paged_attention_gqa(q, ..., key_new=k,
+    value_new=v)``.
 
     Replaces the split / rms_norm / rotary steps of the reference's
     ``_GqaProjRopeMixin.attention`` (auto_infer/layers/attention/gqa.py:
@@ -60,19 +61,21 @@ def qk_norm_rope(qkv, num_q_heads, num_kv_heads, cos, sin, q_norm_weight=None,
     _check_device_tensor(qkv, "qkv", _BF16)
     _require(qkv.dim() == 2 and qkv.stride(1) == 1, "qkv must be (T, width) with unit inner stride")
     T, width = qkv.shape
-    D = 128
+    D = int(head_dim)
+    if D not in (128, 64):
+        raise NotImplementedError(f"qk_norm_rope: head_dim {D} (128 or 64)")
     _require(width == (num_q_heads + 2 * num_kv_heads) * D,
-             f"qkv width {width} != (Hq + 2 Hkv) x 128")
+             f"qkv width {width} != (Hq + 2 Hkv) x {D}")
     cs = []
     for t, name in ((cos, "cos"), (sin, "sin")):
         _check_device_tensor(t, name, _BF16)
         _require(t.shape[0] == T and t.shape[-1] == D and t.numel() == T * D and t.stride(-1) == 1,
-                 f"{name} must hold one 128-wide row per token")
+                 f"{name} must hold one {D}-wide row per token")
         cs.append(t.stride(0))
     for t, name in ((q_norm_weight, "q_norm_weight"), (k_norm_weight, "k_norm_weight")):
         if t is not None:
             _check_device_tensor(t, name, _BF16)
-            _require(t.numel() == D and t.is_contiguous(), f"{name} must be 128 contiguous values")
+            _require(t.numel() == D and t.is_contiguous(), f"{name} must be {D} contiguous values")
     _native.call("aia_qk_norm_rope", _ptr(qkv), qkv.stride(0), T, num_q_heads, num_kv_heads, D,
                  _ptr(cos), cs[0], _ptr(sin), cs[1], _ptr(q_norm_weight), _ptr(k_norm_weight),
                  float(eps), _stream(qkv.device))

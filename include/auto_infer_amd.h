@@ -108,9 +108,8 @@ int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
  * out:    (num_tokens, Hq, head_dim) with the given strides.
  * head_dim must be 128 (Qwen2-7B, Qwen3) or 64 (Qwen2 / Qwen2.5 0.5B:
  * hidden 896 over 14 heads), AIA_ERR_UNSUPPORTED otherwise; scale must be
- * positive (AIA_ERR_INVALID otherwise).  Prefill items exist for head_dim
- * 128; at 64 every row runs on the split-K kernel (two query blocks per key
- * tile for prefill chunks).
+ * positive (AIA_ERR_INVALID otherwise).  Requests whose query rows fill
+ * 128-row items run on the prefill kernel at both head dims.
  * The workspace must hold a plan made by
  * aia_attn_plan with the same metadata, head counts and num_waves.
  * key_new / value_new (optional, both or neither): this step's new K/V rows
@@ -265,15 +264,16 @@ int aia_splice_tokens(const int64_t* pairs, int32_t count, int64_t* target, int6
                       void* stream);
 
 /* Fused pre-attention, in place over a packed qkv projection (T rows of
- * (Hq + 2 Hkv) x 128 bf16 values, token stride qkv_token_stride): per-head
+ * (Hq + 2 Hkv) x head_dim bf16 values, token stride qkv_token_stride): per-head
  * RMSNorm of the Q and K heads with the given weights (both or neither;
  * Qwen3 QK-Norm) and NeoX RoPE x * cos + rotate_half(x) * sin with cos/sin
- * (T, 128) bf16 rows.  V is left as is.  Replaces the split / rms_norm /
+ * (T, head_dim) bf16 rows.  V is left as is.  Replaces the split / rms_norm /
  * rotary steps of _GqaProjRopeMixin.attention (auto_infer/layers/attention/
  * gqa.py:27-49; auto_infer/layers/norm.py:5-8; auto_infer/layers/
  * rotary_embedding/__init__.py:10-13), rounding to bf16 where those bf16
  * ops round.  The Q, K and V slices then go to aia_paged_attention_gqa as
- * query / key_new / value_new through their strides.  head_dim must be 128. */
+ * query / key_new / value_new through their strides.  head_dim must be 128
+ * or 64 (AIA_ERR_UNSUPPORTED otherwise). */
 int aia_qk_norm_rope(void* qkv, int64_t qkv_token_stride, int32_t num_tokens,
                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                      const void* cos, int64_t cos_token_stride, const void* sin,

@@ -293,12 +293,18 @@ def test_empty_step():
     ([100, 70], [700, 70], 28, 4, 64),                    # block size = tile
     ([300], [1300], 16, 8, 256),                          # tiles inside a block
 ])
-def test_prefill_route(lqs, lks, hq, hkv, bs):
+@pytest.mark.parametrize("d", [128, 64])
+def test_prefill_route(lqs, lks, hq, hkv, bs, d):
     """Requests whose query rows (tokens x group) fill a 128-row item run on
     the prefill kernel (K/V tiles staged in LDS once per 128 rows); the rest
-    of the batch stays on split-K.  Both against the oracle."""
+    of the batch stays on split-K.  Both against the oracle, at head_dim 128
+    and 64; the plan's header shows the prefill units."""
     step = workloads.make_gqa_step(lqs=lqs, lks=lks, num_q_heads=hq, num_kv_heads=hkv,
-                                   block_size=bs, seed=57)
+                                   head_dim=d, block_size=bs, seed=57)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, hq, hkv, d, bs)
+    torch.cuda.synchronize()
+    assert plan.workspace[:64].cpu().view(torch.int32)[6].item() > 0     # prefill units
     check(step)
 
 
@@ -338,12 +344,14 @@ def test_prefill_route_repeated_and_deterministic():
     ([200, 1, 3], [5000, 300, 40], 32, 8, 16),            # chunks + split-K rows, block 16
     ([64, 64], [64, 3000], 16, 8, 64),                    # one item short, one chunked
 ])
-def test_prefill_chunked_items(lqs, lks, hq, hkv, bs):
+@pytest.mark.parametrize("d", [128, 64])
+def test_prefill_chunked_items(lqs, lks, hq, hkv, bs, d):
     """Too few prefill items to fill the chip: each item's keys are cut into
     balanced chunks whose partials are merged (log-sum-exp) in the merge
-    pass; the result matches the oracle and does not depend on the cut."""
+    pass; the result matches the oracle and does not depend on the cut
+    (head_dim 128 and 64)."""
     step = workloads.make_gqa_step(lqs=lqs, lks=lks, num_q_heads=hq, num_kv_heads=hkv,
-                                   block_size=bs, seed=61)
+                                   head_dim=d, block_size=bs, seed=61)
     check(step)
 
 

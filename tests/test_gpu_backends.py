@@ -170,13 +170,14 @@ def test_mla_backend_absorbed_prefill_then_decode():
 
 
 @pytest.mark.parametrize("qwen3", [False, True])
-def test_gqa_fused_pre_attention_matches_torch_path(qwen3):
+@pytest.mark.parametrize("d", [128, 64])
+def test_gqa_fused_pre_attention_matches_torch_path(qwen3, d):
     """The in-place QK-norm + RoPE kernel against the torch ops it replaces
     (split, rms_norm, rotate_half), end to end through attention(): without
     QK-norm the KV caches are bit-exact, with it within one bf16 ulp of each
     row's largest value."""
     g = torch.Generator().manual_seed(7)
-    hq, hkv, d, hidden, bs = 8, 2, 128, 256, 16
+    hq, hkv, hidden, bs = 8, 2, 256, 16
     p = "model.layers.0.self_attn."
     w = {p + "qkv_proj.weight": (torch.randn((hq + 2 * hkv) * d, hidden, generator=g) / 16).bfloat16(),
          p + "o_proj.weight": (torch.randn(hidden, hq * d, generator=g) / 32).bfloat16()}

@@ -17,21 +17,21 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-def case(T, hq, hkv, norm, seed, pos_hi=40000):
+def case(T, hq, hkv, norm, seed, pos_hi=40000, d=128):
     g = torch.Generator().manual_seed(seed)
-    qkv = (torch.randn(T, (hq + 2 * hkv) * 128, generator=g) * 2).bfloat16()
+    qkv = (torch.randn(T, (hq + 2 * hkv) * d, generator=g) * 2).bfloat16()
     pos = torch.randint(0, pos_hi, (T,), generator=g)
-    cos, sin = rope_tables(pos, 128)
-    wq = (1 + 0.2 * torch.randn(128, generator=g)).bfloat16() if norm else None
-    wk = (1 + 0.2 * torch.randn(128, generator=g)).bfloat16() if norm else None
+    cos, sin = rope_tables(pos, d)
+    wq = (1 + 0.2 * torch.randn(d, generator=g)).bfloat16() if norm else None
+    wk = (1 + 0.2 * torch.randn(d, generator=g)).bfloat16() if norm else None
     return qkv, cos, sin, wq, wk
 
 
-def gpu(qkv, hq, hkv, cos, sin, wq, wk):
+def gpu(qkv, hq, hkv, cos, sin, wq, wk, d=128):
     buf = qkv.to(DEV)
     q, k, v = ops.qk_norm_rope(buf, hq, hkv, cos.to(DEV), sin.to(DEV),
                                None if wq is None else wq.to(DEV),
-                               None if wk is None else wk.to(DEV), 1e-6)
+                               None if wk is None else wk.to(DEV), 1e-6, head_dim=d)
     torch.cuda.synchronize()
     return q.cpu(), k.cpu(), v.cpu()
 
@@ -39,9 +39,11 @@ def gpu(qkv, hq, hkv, cos, sin, wq, wk):
 @pytest.mark.parametrize("T,hq,hkv", [(16, 16, 8), (2048, 28, 4), (32, 32, 8), (1, 64, 8),
                                       (7, 4, 2)])
 @pytest.mark.parametrize("norm", [False, True])
-def test_qk_norm_rope_vs_oracle(T, hq, hkv, norm):
-    qkv, cos, sin, wq, wk = case(T, hq, hkv, norm, seed=T + hq)
-    gq, gk, gv = gpu(qkv, hq, hkv, cos, sin, wq, wk)
+@pytest.mark.parametrize("d", [128, 64])
+def test_qk_norm_rope_vs_oracle(T, hq, hkv, norm, d):
+    """head_dim 128 (Qwen2-7B / Qwen3) and 64 (Qwen2 / Qwen2.5 0.5B)."""
+    qkv, cos, sin, wq, wk = case(T, hq, hkv, norm, seed=T + hq, d=d)
+    gq, gk, gv = gpu(qkv, hq, hkv, cos, sin, wq, wk, d)
     eq, ek, ev = qk_norm_rope(qkv, hq, hkv, cos, sin, wq, wk, 1e-6)
     assert torch.equal(gv, ev)
     for got, exp in ((gq, eq), (gk, ek)):
@@ -81,3 +83,10 @@ def test_rejects_bad_shapes():
         ops.qk_norm_rope(qkv, 8, 4, cos, cos)          # width != (Hq + 2 Hkv) x 128
     with pytest.raises(ValueError):
         ops.qk_norm_rope(qkv[:, :1024], 4, 2, cos[:, :, :64], cos[:, :, :64])
+
+
+def test_unsupported_head_dim():
+    qkv = torch.zeros(4, (8 + 4) * 96, dtype=torch.bfloat16, device=DEV)
+    cos = torch.zeros(4, 1, 96, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(NotImplementedError):
+        ops.qk_norm_rope(qkv, 8, 2, cos, cos, head_dim=96)

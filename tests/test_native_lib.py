@@ -58,8 +58,8 @@ def test_argument_validation_of_the_fused_kernels_without_gpu():
     exception types."""
     lib = _native.load()
     vp = ctypes.c_void_p
-    # qk norm + rope: head_dim other than 128 is unsupported
-    rc = lib.aia_qk_norm_rope(vp(16), 1024, 4, 4, 2, 64, vp(16), 64, vp(16), 64, None, None,
+    # qk norm + rope: head_dim other than 128 and 64 is unsupported
+    rc = lib.aia_qk_norm_rope(vp(16), 1024, 4, 4, 2, 96, vp(16), 96, vp(16), 96, None, None,
                               ctypes.c_float(1e-6), None)
     assert rc == _native.AIA_ERR_UNSUPPORTED
     with pytest.raises(NotImplementedError, match="head_dim"):

@@ -217,6 +217,34 @@ def probe_sweep(timeit, L):
                                     "threads": threads, "MB": round(nbytes / 1e6, 2),
                                     "us": round(us, 2), "TBps": round(nbytes / us / 1e6, 3),
                                     "frac_of_peak": round(nbytes / us / 1e6 / 8.0, 4)})
+    del kcs, vcs
+    # configs[2] (absorbed MLA): its plan's ranges, every 576-wide latent row
+    # read once -- as two 288-wide halves through the probe's K and V
+    # pointers (one "kv head" of 288 of two per row)
+    m = workloads.config3_mla(seed=0)
+    bt = m.block_table.to(dev)
+    B = len(m.seqlens_kv)
+    plan = ops.AttentionPlan.from_lists(bt, m.cu_seqlens_q, m.seqlens_kv, 16, 1, 512,
+                                        m.cache.shape[1])
+    mranges = config1_ranges(plan, seg_cap=B + m.num_tokens)
+    caches = [m.cache.to(dev)] + [torch.randn(m.cache.shape, generator=gen, device=dev).bfloat16()
+                                  for _ in range(L - 1)]
+    nbytes = sum(m.seqlens_kv) * 576 * 2
+    rt = torch.tensor(mranges, dtype=torch.int32, device=dev)
+    def fn():
+        for i in range(L):
+            c = caches[i]
+            rc = lib.aia_probe_paged_gather(c.data_ptr(), c.data_ptr() + 288 * 2, rt.data_ptr(),
+                                            len(mranges), bt.data_ptr(), bt.stride(0),
+                                            m.cache.shape[1], 2, 288, 1, 576, sink.data_ptr(),
+                                            stream_ptr())
+            assert rc == 0, rc
+    us = timeit(fn)
+    res["paged_gather"].append({"pattern": "configs[2] MLA ranges, 576-wide latent rows",
+                                "work_groups": len(mranges), "threads": 576,
+                                "MB": round(nbytes / 1e6, 2), "us": round(us, 2),
+                                "TBps": round(nbytes / us / 1e6, 3),
+                                "frac_of_peak": round(nbytes / us / 1e6 / 8.0, 4)})
     return res
 
 

@@ -1990,13 +1990,24 @@ struct MergeArgs {
 // (split segment, kv head, slice of 64 output elements), an element being 16
 // dims of one row of the segment's row span (rows of a block past its qb
 // tokens are skipped), and nothing for segments that one range covers.  The
-// 4 waves of a work-group take every 4th partial each, so all partial loads
+// G waves of a work-group take every G-th partial each, so all partial loads
 // of an item are in flight together, and combine their running (max, sum,
 // accumulator) through LDS.  The item count is loaded together with the
 // first record.
-constexpr int kMergeGroups = 4;
+// Waves per merge work-group: 4, or 8 where items hold 64-element slices
+// with a dozen or more partials (absorbed MLA, verify rows of 8+ heads x
+// tokens, about 8+ ranges per segment), which then fold in one load round
+// (configs[2] 52.1-52.7 -> 51.3-51.6 us, configs[3] 41.2-41.5 -> 40.6; with
+// 8 everywhere config 1 went 22.7-22.9 -> 23.2, configs[1]'s prefill chunks
+// 43.5 -> 45.8, and configs[4] (one or two partials per item) 605-607 ->
+// 610).
+#ifndef AIA_MERGE_WIDE
+#define AIA_MERGE_WIDE 1
+#endif
+template <int kMergeGroups>
 
-__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+__global__ __launch_bounds__(64 * kMergeGroups) void merge_kernel(MergeArgs a) {
+  constexpr int kMergeThreads = 64 * kMergeGroups;
   __shared__ float4 sacc[kMergeGroups - 1][kMergeDims / 4][64];
   __shared__ float2 sml[kMergeGroups - 1][64];
   const int lane = threadIdx.x & 63, kg = threadIdx.x >> 6;
@@ -2007,8 +2018,8 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   // the first prefill record and the count go out with the first split-K
   // record, so a prefill work-group's chain is record, then partials
   // prefill chunk merges: a thread takes 8 dims of a row, so a pass of the
-  // work-group covers 2048 / dv rows (16 at head_dim 128, 32 at 64)
-  const int pf_tpr = a.dv / 8, pf_rpp = 256 / pf_tpr;
+  // work-group covers 8 kMergeThreads / dv rows (16 at head_dim 128, 32 at 64)
+  const int pf_tpr = a.dv / 8, pf_rpp = kMergeThreads / pf_tpr;
   const int kSlices = kPfRows / pf_rpp;
   const int per_rec = a.hkv * kSlices;
   // planner status, read now and used at the end (no extra round trip)
@@ -2490,7 +2501,8 @@ void mla_attn_kernel(MlaArgs a) {
   }
 }
 
-int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32_t dv, int32_t tokens,
+int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32_t dv, int32_t batch,
+                 int32_t tokens, int32_t waves,
                  const uint16_t* part_o,
                  const float2* part_ml, const int32_t* seg, uint16_t* out, int64_t o_ts,
                  int64_t o_hs, hipStream_t s) {
@@ -2502,7 +2514,13 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
   mg.mrg = reinterpret_cast<const int32_t*>(ws + L.mrg); mg.mrg_cap = L.mrg_cap;
   const bool pf = L.pf_mrg_cap > 0;
   mg.pf_mrg = pf ? reinterpret_cast<const int4*>(ws + L.pfm) : nullptr;
-  const int64_t pf_slices = (int64_t)kPfRows * dv / 2048;   // see merge_kernel
+  // wide: 64-element slices (MLA, or 8+ rows per segment) and about 8 or
+  // more ranges per segment, i.e. a dozen partials per item
+  const bool wide = AIA_MERGE_WIDE && L.pf_mrg_cap == 0 &&
+                    (dv == kMlaV || (int64_t)g.hb * ((tokens + batch - 1) / batch) >= 8) &&
+                    (int64_t)waves >= 8LL * batch * g.nkvg * g.nhb;
+  const int threads = wide ? 512 : 256;
+  const int64_t pf_slices = (int64_t)kPfRows * dv / (8 * threads);   // see merge_kernel
   mg.pf_items_cap = L.pf_mrg_cap * g.hkv * pf_slices;
   mg.pf_o = reinterpret_cast<const uint16_t*>(ws + L.pf_o);
   mg.pf_ml = reinterpret_cast<const float2*>(ws + L.pf_ml);
@@ -2510,7 +2528,8 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
   const int64_t items = L.mrg_cap > pitems ? L.mrg_cap : pitems;
   int64_t mgrid = items < 2048 ? items : 2048;
   if (mgrid < 1) mgrid = 1;
-  merge_kernel<<<(unsigned)mgrid, 256, 0, s>>>(mg);
+  if (wide) merge_kernel<8><<<(unsigned)mgrid, threads, 0, s>>>(mg);
+  else merge_kernel<4><<<(unsigned)mgrid, threads, 0, s>>>(mg);
   return aia::check_hip(hipGetLastError(), "merge_kernel launch");
 }
 
@@ -2730,7 +2749,7 @@ extern "C" int aia_paged_attention_gqa(
       if (int rc = check_hip(hipGetLastError(), "gqa_prefill_kernel launch")) return rc;
     }
   }
-  return launch_merge(ws, L, g, g.nw, head_dim, num_tokens, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
+  return launch_merge(ws, L, g, g.nw, head_dim, batch, num_tokens, waves, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
                       s);
 }
 
@@ -2787,6 +2806,6 @@ extern "C" int aia_paged_attention_mla(
   if (g.rb == 2) mla_attn_kernel<2><<<waves, 256, 0, s>>>(a);
   else mla_attn_kernel<1><<<waves, 256, 0, s>>>(a);
   if (int rc = check_hip(hipGetLastError(), "mla_attn_kernel launch")) return rc;
-  return launch_merge(ws, L, g, 1, kMlaV, num_tokens, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
+  return launch_merge(ws, L, g, 1, kMlaV, batch, num_tokens, waves, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
                       s);
 }

@@ -133,16 +133,19 @@ def _probe_lib():
     return lib
 
 
-def config1_ranges(plan, seg_cap):
-    """The key ranges of a config-1 plan, read back from its workspace in
-    work-group order: {request, first key, end key, 0} per record slot
-    (empty slots read nothing).  Record slot layout: int4 {segment, first
-    tile, end tile, tiles per range}, then the segment's 8-int record
-    {request, .., .., .., lim_base, tile_begin, tile_end, ..}."""
+def config1_ranges(plan):
+    """The key ranges of a plan, read back from its workspace in work-group
+    order: {request, first key, end key, 0} per record slot (empty slots
+    read nothing).  Record slot layout: int4 {segment, first tile, end tile,
+    tiles per range}, then the segment's 8-int record {request, .., .., ..,
+    lim_base, tile_begin, tile_end, ..}."""
+    from auto_infer_amd import ops
     torch.cuda.synchronize()
     ws = plan.workspace.cpu().view(torch.int32)
     waves = int(ws[4])
-    rec_off = (256 + (seg_cap + 1) * 32 + 255) // 256 * 256 // 4
+    L = ops.workspace_layout(plan.batch, plan.num_tokens, plan.num_q_heads, plan.num_kv_heads,
+                             plan.head_dim_v, plan.num_waves)
+    rec_off = L["wave"] // 4
     recs = ws[rec_off: rec_off + waves * 32].view(waves, 32).tolist()
     out = []
     for r in recs:
@@ -195,7 +198,7 @@ def probe_sweep(timeit, L):
     cu = torch.tensor([0, *step.cu_seqlens_q], dtype=torch.int32, device=dev)
     kvl = torch.tensor(step.seqlens_kv, dtype=torch.int32, device=dev)
     plan = ops.AttentionPlan(bt, cu, kvl, step.num_tokens, 16, hkv, d, bs)
-    ranges = config1_ranges(plan, seg_cap=16 + 2)
+    ranges = config1_ranges(plan)
     gen = torch.Generator(device=dev).manual_seed(3)
     kcs = [torch.randn(step.k_cache.shape, generator=gen, device=dev).bfloat16() for _ in range(L)]
     vcs = [torch.randn(step.v_cache.shape, generator=gen, device=dev).bfloat16() for _ in range(L)]
@@ -223,10 +226,9 @@ def probe_sweep(timeit, L):
     # pointers (one "kv head" of 288 of two per row)
     m = workloads.config3_mla(seed=0)
     bt = m.block_table.to(dev)
-    B = len(m.seqlens_kv)
     plan = ops.AttentionPlan.from_lists(bt, m.cu_seqlens_q, m.seqlens_kv, 16, 1, 512,
                                         m.cache.shape[1])
-    mranges = config1_ranges(plan, seg_cap=B + m.num_tokens)
+    mranges = config1_ranges(plan)
     caches = [m.cache.to(dev)] + [torch.randn(m.cache.shape, generator=gen, device=dev).bfloat16()
                                   for _ in range(L - 1)]
     nbytes = sum(m.seqlens_kv) * 576 * 2

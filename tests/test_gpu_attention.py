@@ -477,9 +477,7 @@ def test_gqa_plan_ranges_spread_over_the_xcds(seed):
     ws = plan.workspace.cpu().view(torch.int32)
     hdr = ws[:64].tolist()
     total, tpw, waves = hdr[1], hdr[2], hdr[4]
-    # layout for Hq 16 / Hkv 8, one query token per request: 18 segment slots
-    seg_cap = 16 + 2
-    rec_off = (256 + (seg_cap + 1) * 32 + 255) // 256 * 256
+    rec_off = ops.workspace_layout(16, 16, 16, 8, 128)["wave"]
     recs = ws[rec_off // 4: rec_off // 4 + waves * 32].view(waves, 32)
     nr = -(-total // tpw)
     assert tpw >= 1 and nr <= waves

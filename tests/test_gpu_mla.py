@@ -83,14 +83,13 @@ def test_mla_balanced_plan_other_range_counts(waves):
 
 def _read_plan(plan):
     """(header, segment records, range records) of an MLA decode plan read
-    back from its workspace (offsets as the planner lays them out: header
-    at 0, 8-int segment records at 256, 32-int range records after
-    seg_cap + 1 segment records, each part 256-byte aligned)."""
+    back from its workspace, at the offsets aia_attn_workspace_layout
+    gives (header at 0, 8-int segment records, 32-int range records)."""
     ws = plan.workspace.cpu().view(torch.int32)
     hdr = ws[:64].tolist()
-    seg_cap = plan.batch + plan.num_tokens           # MLA decode: one segment per token
-    seg_off = 256
-    rec_off = (seg_off + (seg_cap + 1) * 32 + 255) // 256 * 256
+    L = ops.workspace_layout(plan.batch, plan.num_tokens, plan.num_q_heads, plan.num_kv_heads,
+                             plan.head_dim_v, plan.num_waves)
+    seg_off, rec_off = L["seg"], L["wave"]
     nseg = hdr[0]
     seg = ws[seg_off // 4: seg_off // 4 + nseg * 8].view(nseg, 8)
     recs = ws[rec_off // 4: rec_off // 4 + hdr[4] * 32].view(hdr[4], 32)

@@ -28,6 +28,8 @@ SIGNATURES = {
     "aia_last_error": [],
     "aia_kv_write": [c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32,
                      c_i64, c_vp],
+    "aia_kv_write_nz": [c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i64,
+                        c_vp],
     "aia_attn_workspace_bytes": [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                                  ctypes.POINTER(c_i64)],
     "aia_attn_workspace_layout": [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,

@@ -9,7 +9,11 @@ the same op-pair seam ``_write_kv`` / ``_attn``.  Only the op pair differs:
 the KV slot write and the split-K paged attention run as HIP kernels.
 The backend is graph-capturable (no host sync, no allocation in ``_attn``
 once the step's plan exists), so it serves both the "paged" and "graph"
-modes.
+modes.  With ``kv_layout="nz"`` it also takes the caches of the reference's
+graph-mode backend (``GraphGqaBackend``, gqa.py:134-226): per layer a (k, v)
+pair of (num_blocks, block_size, n_kv, head_dim) tensors whose memory is the
+16-wide fractal NZ layout (viewed (num_blocks, n_kv * head_dim / 16,
+block_size, 16) by npu_scatter_pa_kv_cache and FIA-v2, gqa.py:202-226).
 """
 import torch
 
@@ -23,7 +27,8 @@ class GqaHipBackend(AttentionBackend):
 
     def __init__(self, n_q_heads: int, n_kv_heads: int, head_dim: int, scale: float,
                  num_layers: int, device, dtype, w: dict = None, layer_prefix=None,
-                 rms_eps=None, fuse_kv_write: bool = True, fuse_pre_attention: bool = True):
+                 rms_eps=None, fuse_kv_write: bool = True, fuse_pre_attention: bool = True,
+                 kv_layout: str = "nd"):
         self.n_q_heads = n_q_heads
         self.n_kv_heads = n_kv_heads
         self.head_dim = head_dim
@@ -47,12 +52,26 @@ class GqaHipBackend(AttentionBackend):
         # one in-place kernel over the qkv projection (bf16 rounding where the
         # torch ops round); q, k, v are then strided views of it.
         self.fuse_pre_attention = fuse_pre_attention
+        if kv_layout not in ops.KV_LAYOUTS:
+            raise ValueError(f"kv_layout must be one of {sorted(ops.KV_LAYOUTS)}")
+        self.kv_layout = kv_layout
         self._pending = None
 
     def alloc_kv_caches(self, num_blocks: int, block_size: int) -> list:
+        if self.kv_layout == "nz":      # GraphGqaBackend.alloc_kv_caches (gqa.py:195-204)
+            shape = (num_blocks, block_size, self.n_kv_heads, self.head_dim)
+            return [(torch.zeros(shape, device=self.device, dtype=self.dtype),
+                     torch.zeros(shape, device=self.device, dtype=self.dtype))
+                    for _ in range(self.num_layers)]
         shape = (2, num_blocks, block_size, self.n_kv_heads, self.head_dim)
         return [torch.zeros(shape, device=self.device, dtype=self.dtype)
                 for _ in range(self.num_layers)]
+
+    def _write(self, k, v, kc, vc, slot_mapping):
+        if self.kv_layout == "nz":
+            ops.write_kv_nz(k, v, kc, vc, slot_mapping)
+        else:
+            ops.write_kv(k, v, kc, vc, slot_mapping)
 
     def attention(self, layer_idx: int, x: torch.Tensor, ctx) -> torch.Tensor:
         T = x.shape[0]
@@ -96,17 +115,19 @@ class GqaHipBackend(AttentionBackend):
                 and k.shape[0] == ctx.slot_mapping.shape[0]):
             self._pending = (layer_idx, id(ctx), k, v)
             return
-        ops.write_kv(k, v, cache[0], cache[1], ctx.slot_mapping)
+        self._write(k, v, cache[0], cache[1], ctx.slot_mapping)
 
     def _attn(self, layer_idx: int, q, k, v, ctx) -> torch.Tensor:
         cache = ctx.kv_caches[layer_idx]
-        plan = step_plan(ctx, self.n_q_heads, self.n_kv_heads, self.head_dim, cache.shape[2])
+        plan = step_plan(ctx, self.n_q_heads, self.n_kv_heads, self.head_dim, cache[0].shape[1])
         pending, self._pending = self._pending, None
         if pending is not None and pending[:2] == (layer_idx, id(ctx)):
             return ops.paged_attention_gqa(q, cache[0], cache[1], plan, self.scale,
-                                           key_new=pending[2], value_new=pending[3])
+                                           key_new=pending[2], value_new=pending[3],
+                                           kv_layout=self.kv_layout)
         if pending is not None:      # a deferred write for another call: do it now
             lay, _, pk, pv = pending
             c = ctx.kv_caches[lay]
-            ops.write_kv(pk, pv, c[0], c[1], ctx.slot_mapping)
-        return ops.paged_attention_gqa(q, cache[0], cache[1], plan, self.scale)
+            self._write(pk, pv, c[0], c[1], ctx.slot_mapping)
+        return ops.paged_attention_gqa(q, cache[0], cache[1], plan, self.scale,
+                                       kv_layout=self.kv_layout)

@@ -4,7 +4,10 @@ Mirrors auto_infer/layers/attention/registry.py: ``register_attention_family``
 (:11-16), ``register_mtp_attention_family`` (:19-28), ``build_attention_backend``
 (:119-136) and ``build_mtp_attention_backend`` (:139-157), same validation,
 exception types and message stems.  The families this package adds are
-``"gqa_hip"`` and ``"mla_hip"`` (and MTP ``"gqa_hip"``).  ``register_into``
+``"gqa_hip"`` and ``"mla_hip"`` (and MTP ``"gqa_hip"``), plus ``"gqa_hip_nz"``
+(and MTP ``"gqa_hip_nz"``): the same GQA backend over the two-tensor, 16-wide
+NZ KV caches of the reference's graph mode (``GraphGqaBackend``,
+gqa.py:192-211), for runners that hand the caches to other NZ consumers.  ``register_into``
 installs the same builders into another registry -- the reference's own --
 which is how a maintainer plugs them in without touching its dispatcher.
 """
@@ -17,6 +20,7 @@ _MTP_FAMILIES: dict = {}
 
 GQA_FAMILY = "gqa_hip"
 MLA_FAMILY = "mla_hip"
+GQA_NZ_FAMILY = "gqa_hip_nz"
 
 
 def register_attention_family(name: str, builder: AttentionBuilder) -> None:
@@ -42,15 +46,19 @@ def _paged_only(family, mode):
             f"full-softmax backends")
 
 
-def _gqa_hip(model, mode: str):
+def _gqa_hip(model, mode: str, kv_layout: str = "nd", family: str = GQA_FAMILY):
     from auto_infer_amd.attention.gqa import GqaHipBackend
-    _paged_only(GQA_FAMILY, mode)
+    _paged_only(family, mode)
     cfg = model.cfg
     return GqaHipBackend(
         n_q_heads=model.n_q_local, n_kv_heads=model.n_kv_local, head_dim=cfg.head_dim,
         scale=cfg.head_dim ** -0.5, num_layers=cfg.num_layers, device=model.device,
         dtype=model.dtype, w=model.w, layer_prefix=model.layer_prefix,
-        rms_eps=getattr(cfg, "rms_eps", None))
+        rms_eps=getattr(cfg, "rms_eps", None), kv_layout=kv_layout)
+
+
+def _gqa_hip_nz(model, mode: str):
+    return _gqa_hip(model, mode, "nz", GQA_NZ_FAMILY)
 
 
 def _mla_hip(model, mode: str):
@@ -65,17 +73,22 @@ def _mla_hip(model, mode: str):
         device=model.device, dtype=model.dtype, layer_prefix=model.layer_prefix)
 
 
-def _gqa_hip_mtp(model, mode: str, prefix: str):
+def _gqa_hip_mtp(model, mode: str, prefix: str, kv_layout: str = "nd"):
     from auto_infer_amd.attention.gqa import GqaHipBackend
     cfg = model.cfg
     return GqaHipBackend(
         n_q_heads=model.n_q_local, n_kv_heads=model.n_kv_local, head_dim=cfg.head_dim,
         scale=cfg.head_dim ** -0.5, num_layers=1, device=model.device, dtype=model.dtype,
-        w=model.w, layer_prefix=lambda _: prefix, rms_eps=getattr(cfg, "rms_eps", None))
+        w=model.w, layer_prefix=lambda _: prefix, rms_eps=getattr(cfg, "rms_eps", None),
+        kv_layout=kv_layout)
 
 
-BUILDERS = {GQA_FAMILY: _gqa_hip, MLA_FAMILY: _mla_hip}
-MTP_BUILDERS = {GQA_FAMILY: _gqa_hip_mtp}
+def _gqa_hip_nz_mtp(model, mode: str, prefix: str):
+    return _gqa_hip_mtp(model, mode, prefix, "nz")
+
+
+BUILDERS = {GQA_FAMILY: _gqa_hip, MLA_FAMILY: _mla_hip, GQA_NZ_FAMILY: _gqa_hip_nz}
+MTP_BUILDERS = {GQA_FAMILY: _gqa_hip_mtp, GQA_NZ_FAMILY: _gqa_hip_nz_mtp}
 
 
 def register_into(register_family=register_attention_family,

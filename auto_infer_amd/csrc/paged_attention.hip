@@ -1139,7 +1139,20 @@ constexpr int kPipe = AIA_PIPE;
 // (qb = 16 / hb).  Every K/V tile is loaded once and used by all blocks, so a
 // prefill chunk reads its keys 1/RB as often; blocks past the segment's last
 // token are skipped (a uniform branch), so a decode segment costs one block.
-template <int RB, int D>
+// Cache layouts.  ND: (num_blocks, block_size, Hkv, D), a token slot's heads
+// contiguous.  NZ: the 16-wide fractal layout of the reference's graph-mode
+// caches (gqa.py:163,202-226): each block viewed (Hkv D / 16, block_size,
+// 16), so 16 dims of all of a block's tokens are contiguous.  kv_piece gives
+// the 16-byte index of piece p (8 dims) of head h of (block, offset).
+template <bool NZ>
+__device__ __forceinline__ int64_t kv_piece(int64_t blk, int off, int bs, int row_elems, int h,
+                                            int D, int p) {
+  if (!NZ) return (((blk * bs + off) * row_elems + (int64_t)h * D) >> 3) + p;
+  return ((blk * bs * row_elems) >> 3) +
+         (((int64_t)(h * (D / 16) + (p >> 1)) * bs + off) << 1) + (p & 1);
+}
+
+template <int RB, int D, bool NZ>
 __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, int s, int lt0,
                                             int lt1, int w, int tpw, uint16_t* vt, int lane,
                                             int wid, bool use_pre, int pre) {
@@ -1178,6 +1191,9 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
   const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
   const int nblk_vis = (visible + a.bs - 1) / a.bs;
   int blk_base = 0, btv = 0, w1 = 0;
+  // 16-byte pieces between MFMA k-steps j and j + 1 of a cached key (4 pieces
+  // on in ND; two 16-dim chunks of block_size x 16 on in NZ)
+  const int64_t jstride = NZ ? 4 * (int64_t)a.bs : 4;
 
   uint4 qf[RB][KJ];
 #pragma unroll
@@ -1217,27 +1233,30 @@ __device__ __forceinline__ void gqa_segment(const AttnArgs& a, const int* rec, i
     // block ids outside the pool are clamped so a bad table cannot fault
     const int blk = min(max(__shfl(btv, bi - blk_base), 0), a.nb - 1);
     const int off = tok - bi * a.bs;
-    const int64_t base = ((int64_t)blk * a.bs + off) * row_elems + (int64_t)kvh * D;
+    // 16-byte index of this lane's first piece (4 g + 0) in the cache; piece
+    // 4 j + g is jstride further on in either layout
+    const int64_t base = kv_piece<NZ>(blk, off, a.bs, row_elems, kvh, D, g);
     const bool fresh = live && tok >= new_start;
     const int64_t nrow = (int64_t)(q_begin + tok - new_start);
-    const uint4* kp = reinterpret_cast<const uint4*>(
-        fresh ? a.kn + nrow * a.kn_ts + (int64_t)kvh * D : a.kc + base);
-    const uint4* vp = reinterpret_cast<const uint4*>(
-        fresh ? a.vn + nrow * a.vn_ts + (int64_t)kvh * D : a.vc + base);
+    const uint4* kp = fresh ? reinterpret_cast<const uint4*>(a.kn + nrow * a.kn_ts + (int64_t)kvh * D) + g
+                            : reinterpret_cast<const uint4*>(a.kc) + base;
+    const uint4* vp = fresh ? reinterpret_cast<const uint4*>(a.vn + nrow * a.vn_ts + (int64_t)kvh * D) + g
+                            : reinterpret_cast<const uint4*>(a.vc) + base;
+    const int64_t js = fresh ? 4 : jstride;
     // cache slot this lane writes after the tile arrives (-1: nothing)
     wdst = (writer && fresh && lt * kTile + n < visible) ? base : (int64_t)-1;
 #pragma unroll
-    for (int j = 0; j < KJ; ++j) kk[j] = kp[4 * j + g];
+    for (int j = 0; j < KJ; ++j) kk[j] = kp[j * js];
 #pragma unroll
-    for (int j = 0; j < KJ; ++j) vv[j] = vp[4 * j + g];
+    for (int j = 0; j < KJ; ++j) vv[j] = vp[j * js];
   };
 
   auto compute = [&](int lt, const uint4 (&kk)[KJ], const uint4 (&vv)[KJ], int64_t wdst) {
     if (wdst >= 0) {   // KV slot write of a new row (its bytes just arrived)
-      uint4* kd = reinterpret_cast<uint4*>(a.kc + wdst);
-      uint4* vd = reinterpret_cast<uint4*>(a.vc + wdst);
+      uint4* kd = reinterpret_cast<uint4*>(a.kc) + wdst;
+      uint4* vd = reinterpret_cast<uint4*>(a.vc) + wdst;
 #pragma unroll
-      for (int j = 0; j < KJ; ++j) { kd[4 * j + g] = kk[j]; vd[4 * j + g] = vv[j]; }
+      for (int j = 0; j < KJ; ++j) { kd[j * jstride] = kk[j]; vd[j * jstride] = vv[j]; }
     }
     float4_t acc[RB];
 #pragma unroll
@@ -1386,7 +1405,7 @@ __device__ __forceinline__ int xcd_range(int b, int n) {
 
 // One work-group per key range, one wave per kv head of the segment's group.
 // D: head dim, 128 or 64.
-template <int NW, int RB, int D>
+template <int NW, int RB, int D, bool NZ>
 #ifndef AIA_GQA_WAVES_PER_EU
 #define AIA_GQA_WAVES_PER_EU 2
 #endif
@@ -1417,7 +1436,7 @@ __device__ __forceinline__ void gqa_attn_body(const AttnArgs& a, int bid,
     if (rec[6] > t) {
       const int chunk_end = min(t_end, rec[6]);
       if ((rec[1] & 0xffff) * NW + wid < a.hkv)
-        gqa_segment<RB, D>(a, rec, s, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane, wid, first,
+        gqa_segment<RB, D, NZ>(a, rec, s, t - rec[5], chunk_end - rec[5], w, tpw, vt, lane, wid, first,
                         pre);
       first = false;
       t = chunk_end;
@@ -1430,11 +1449,11 @@ __device__ __forceinline__ void gqa_attn_body(const AttnArgs& a, int bid,
   }
 }
 
-template <int NW, int RB, int D>
+template <int NW, int RB, int D, bool NZ>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(AIA_GQA_WAVES_PER_EU, AIA_GQA_WAVES_PER_EU)))
 void gqa_attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vt_all[NW][kTile * kVStride];
-  gqa_attn_body<NW, RB, D>(a, blockIdx.x, vt_all);
+  gqa_attn_body<NW, RB, D, NZ>(a, blockIdx.x, vt_all);
 }
 
 // ---------------------------------------------------------------- prefill
@@ -1519,7 +1538,7 @@ constexpr float kLazyLog2 = AIA_PF_LAZY;              // max growth (log2) befor
 #ifndef AIA_PF_WPE
 #define AIA_PF_WPE 2
 #endif
-template <bool ONE_BLOCK, bool FUSED, int D>
+template <bool ONE_BLOCK, bool FUSED, int D, bool NZ>
 __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
                                                  uint16_t* k0, uint16_t* k1,
                                                  uint16_t* v0, uint16_t* v1) {
@@ -1580,11 +1599,11 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
       const int p = ctx0 + t;
       if (p < 0) continue;
       const int blk = min(max(btrow[p / a.bs], 0), a.nb - 1);
-      const int64_t dst = ((int64_t)blk * a.bs + p % a.bs) * row_elems + (int64_t)kvh * D;
+      const int64_t dst = kv_piece<NZ>(blk, p % a.bs, a.bs, row_elems, kvh, D, c);
       const int64_t tok = q_begin + t;
-      reinterpret_cast<uint4*>(a.kc + dst)[c] =
+      reinterpret_cast<uint4*>(a.kc)[dst] =
           reinterpret_cast<const uint4*>(a.kn + tok * a.kn_ts + (int64_t)kvh * D)[c];
-      reinterpret_cast<uint4*>(a.vc + dst)[c] =
+      reinterpret_cast<uint4*>(a.vc)[dst] =
           reinterpret_cast<const uint4*>(a.vn + tok * a.vn_ts + (int64_t)kvh * D)[c];
     }
   }
@@ -1674,20 +1693,29 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     }
     return __builtin_amdgcn_readlane(vbid, t - tb);
   };
-  auto load_row = [&](int i, int p, int slot, uint16_t* kdst, uint16_t* vdst) {
-    const int64_t e = (int64_t)slot * row_elems;
-    const uint16_t* kp = kcb + e;
-    const uint16_t* vp = vcb + e;
+  // key at position p, in block blk at offset boff
+  auto load_row = [&](int i, int p, int blk, int boff, uint16_t* kdst, uint16_t* vdst) {
+    // (rounds start at multiples of 16 keys, so lkey stands for the key mod RC)
+    const int ck = lc ^ (lkey & (RC - 1)), cv = lc ^ (2 * (lkey & (RC / 2 - 1)));
+    const uint16_t* kp;
+    const uint16_t* vp;
+    if (NZ) {
+      kp = a.kc + 8 * kv_piece<true>(blk, boff, a.bs, row_elems, kvh, D, ck);
+      vp = a.vc + 8 * kv_piece<true>(blk, boff, a.bs, row_elems, kvh, D, cv);
+    } else {
+      const int64_t e = ((int64_t)blk * a.bs + boff) * row_elems;
+      kp = kcb + e + 8 * ck;
+      vp = vcb + e + 8 * cv;
+    }
     if (FUSED) {
       const bool fresh = p >= ctx0;
       const int64_t tok = q_begin + (p - ctx0);
-      kp = fresh ? knb + tok * a.kn_ts : kp;
-      vp = fresh ? vnb + tok * a.vn_ts : vp;
+      kp = fresh ? knb + tok * a.kn_ts + 8 * ck : kp;
+      vp = fresh ? vnb + tok * a.vn_ts + 8 * cv : vp;
     }
     const int rb = (kLdKeys * i + kWaveKeys * wid) * D;     // the wave's first row
-    // (rounds start at multiples of 16 keys, so lkey stands for the key mod RC)
-    lds_load16(kp + 8 * (lc ^ (lkey & (RC - 1))), kdst + rb);
-    lds_load16(vp + 8 * (lc ^ (2 * (lkey & (RC / 2 - 1)))), vdst + rb);
+    lds_load16(kp, kdst + rb);
+    lds_load16(vp, vdst + rb);
   };
   auto load = [&](int t, auto buf_tag) {
     constexpr int B = decltype(buf_tag)::value;
@@ -1696,19 +1724,19 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
     const int kb = t * kPfKeys;
     if (ONE_BLOCK) {
       const int blk = min(max(tile_bid(t), 0), a.nb - 1);
-      const int slot0 = blk * a.bs + kb % a.bs;
+      const int boff0 = kb % a.bs;
       const int last = kend - 1 - kb;
 #pragma unroll
       for (int i = 0; i < kLdRounds; ++i) {
         const int off = min(kLdKeys * i + lkey, last);
-        load_row(i, kb + off, slot0 + off, kdst, vdst);
+        load_row(i, kb + off, blk, boff0 + off, kdst, vdst);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < kLdRounds; ++i) {
         const int p = min(kb + kLdKeys * i + lkey, kend - 1);
         const int blk = min(max(bid[i], 0), a.nb - 1);
-        load_row(i, p, blk * a.bs + p % a.bs, kdst, vdst);
+        load_row(i, p, blk, p % a.bs, kdst, vdst);
       }
     }
   };
@@ -1941,14 +1969,14 @@ __device__ __forceinline__ void gqa_prefill_body(const PrefillArgs& a, int wg,
   }
 }
 
-template <bool ONE_BLOCK, bool FUSED, int D>
+template <bool ONE_BLOCK, bool FUSED, int D, bool NZ>
 __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(AIA_PF_WPE, AIA_PF_WPE)))
 void gqa_prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t k0[kPfKeys * D];
   __shared__ __attribute__((aligned(16))) uint16_t k1[kPfKeys * D];
   __shared__ __attribute__((aligned(16))) uint16_t v0[kPfKeys * D];
   __shared__ __attribute__((aligned(16))) uint16_t v1[kPfKeys * D];
-  gqa_prefill_body<ONE_BLOCK, FUSED, D>(a, blockIdx.x, k0, k1, v0, v1);
+  gqa_prefill_body<ONE_BLOCK, FUSED, D, NZ>(a, blockIdx.x, k0, k1, v0, v1);
 }
 
 // Mixed steps (prefill items beside split-K decode ranges) in one grid, for
@@ -1964,7 +1992,7 @@ void gqa_prefill_kernel(PrefillArgs a) {
 // The decode role stages its V^T tiles in the first K buffer.
 constexpr int kMixedK0 = kPfWaves * kTile * kVStride > kPfKeys * kKStride
                              ? kPfWaves * kTile * kVStride : kPfKeys * kKStride;
-template <bool ONE_BLOCK, bool FUSED>
+template <bool ONE_BLOCK, bool FUSED, bool NZ>
 __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(AIA_PF_WPE, AIA_PF_WPE)))
 void gqa_mixed_kernel(AttnArgs a, PrefillArgs pa, int npf) {
   __shared__ __attribute__((aligned(16))) uint16_t k0[kMixedK0];
@@ -1980,9 +2008,9 @@ void gqa_mixed_kernel(AttnArgs a, PrefillArgs pa, int npf) {
   const bool prefill = b < npf;
   const int idx = prefill ? b : b - npf;
   if (prefill)
-    gqa_prefill_body<ONE_BLOCK, FUSED, kHeadDim>(pa, idx, k0, k1, v0, v1);
+    gqa_prefill_body<ONE_BLOCK, FUSED, kHeadDim, NZ>(pa, idx, k0, k1, v0, v1);
   else
-    gqa_attn_body<kPfWaves, 1, kHeadDim>(a, idx,
+    gqa_attn_body<kPfWaves, 1, kHeadDim, NZ>(a, idx,
                                          reinterpret_cast<uint16_t(*)[kTile * kVStride]>(&k0[0]));
 }
 
@@ -2564,6 +2592,54 @@ bool small_plan(const Geometry& g, int32_t dv, int32_t batch, const Layout& L) {
          L.seg_cap <= kSmallPlanSegs && L.pf_cap == 0;
 }
 
+// The attention launches of one call, for one cache layout.
+template <bool NZ>
+int launch_gqa(const AttnArgs& a, const PrefillArgs& pa, const Layout& L, const Geometry& g,
+               int32_t head_dim, int32_t waves, bool one_block, hipStream_t s) {
+  using aia::check_hip;
+  if (AIA_MIXED && L.pf_cap > 0 && g.nw == kPfWaves && g.rb == 1 && head_dim == kHeadDim) {
+    const int npf = (int)(L.pf_unit_cap * g.hkv);
+    const dim3 grid((unsigned)(npf + waves));
+    if (one_block && pa.kn) gqa_mixed_kernel<true, true, NZ><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
+    else if (one_block) gqa_mixed_kernel<true, false, NZ><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
+    else if (pa.kn) gqa_mixed_kernel<false, true, NZ><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
+    else gqa_mixed_kernel<false, false, NZ><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
+    if (int rc = check_hip(hipGetLastError(), "gqa_mixed_kernel launch")) return rc;
+  } else {
+#define AIA_GQA_LAUNCH_D(NW, D)                                                   \
+  (g.rb == 2 ? gqa_attn_kernel<NW, 2, D, NZ><<<waves, 64 * NW, 0, s>>>(a)            \
+             : gqa_attn_kernel<NW, 1, D, NZ><<<waves, 64 * NW, 0, s>>>(a))
+#define AIA_GQA_LAUNCH(NW)                                                        \
+  (head_dim == 64 ? AIA_GQA_LAUNCH_D(NW, 64) : AIA_GQA_LAUNCH_D(NW, kHeadDim))
+    switch (g.nw) {
+      case 1: AIA_GQA_LAUNCH(1); break;
+      case 2: AIA_GQA_LAUNCH(2); break;
+      case 3: AIA_GQA_LAUNCH(3); break;
+      case 4: AIA_GQA_LAUNCH(4); break;
+      case 5: AIA_GQA_LAUNCH(5); break;
+      case 6: AIA_GQA_LAUNCH(6); break;
+      case 7: AIA_GQA_LAUNCH(7); break;
+      default: AIA_GQA_LAUNCH(8); break;
+    }
+#undef AIA_GQA_LAUNCH
+#undef AIA_GQA_LAUNCH_D
+    if (int rc = check_hip(hipGetLastError(), "gqa_attn_kernel launch")) return rc;
+    if (L.pf_cap > 0) {
+      const dim3 grid((unsigned)(L.pf_unit_cap * g.hkv));
+#define AIA_PF_LAUNCH(D)                                                                   \
+  (one_block && pa.kn ? gqa_prefill_kernel<true, true, D, NZ><<<grid, kPfWaves * 64, 0, s>>>(pa)   \
+   : one_block        ? gqa_prefill_kernel<true, false, D, NZ><<<grid, kPfWaves * 64, 0, s>>>(pa)  \
+   : pa.kn            ? gqa_prefill_kernel<false, true, D, NZ><<<grid, kPfWaves * 64, 0, s>>>(pa)  \
+                      : gqa_prefill_kernel<false, false, D, NZ><<<grid, kPfWaves * 64, 0, s>>>(pa))
+      if (head_dim == 64) AIA_PF_LAUNCH(64);
+      else AIA_PF_LAUNCH(kHeadDim);
+#undef AIA_PF_LAUNCH
+      if (int rc = check_hip(hipGetLastError(), "gqa_prefill_kernel launch")) return rc;
+    }
+  }
+  return AIA_OK;
+}
+
 int check_heads(const char* fn, int32_t hq, int32_t hkv) {
   if (hq <= 0 || hkv <= 0 || hq % hkv != 0)
     return aia::fail(AIA_ERR_INVALID, "%s: num_q_heads %d must be a positive multiple of num_kv_heads %d",
@@ -2662,8 +2738,8 @@ extern "C" int aia_paged_attention_gqa(
   if (block_size <= 0 || num_blocks <= 0)
     return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: block_size %d / num_blocks %d",
                 block_size, num_blocks);
-  if (flags != 0)
-    return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: flags must be 0 (got 0x%x)", flags);
+  if (flags & ~AIA_ATTN_KV_NZ)
+    return fail(AIA_ERR_INVALID, "aia_paged_attention_gqa: unknown flags 0x%x", flags);
   if (num_tokens == 0 || batch == 0) return AIA_OK;    // empty step (zero-size tensors)
   if (!query || !key_cache || !value_cache || !block_table || !out || !workspace || !cu_seqlens_q ||
       !seqlens_kv)
@@ -2728,46 +2804,9 @@ extern "C" int aia_paged_attention_gqa(
     pa.part_units = (int32_t)(L.pf_slots / g.hkv);
   }
   const bool one_block = block_size % kPfKeys == 0;
-  if (AIA_MIXED && L.pf_cap > 0 && g.nw == kPfWaves && g.rb == 1 && head_dim == kHeadDim) {
-    const int npf = (int)(L.pf_unit_cap * g.hkv);
-    const dim3 grid((unsigned)(npf + waves));
-    if (one_block && pa.kn) gqa_mixed_kernel<true, true><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
-    else if (one_block) gqa_mixed_kernel<true, false><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
-    else if (pa.kn) gqa_mixed_kernel<false, true><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
-    else gqa_mixed_kernel<false, false><<<grid, kPfWaves * 64, 0, s>>>(a, pa, npf);
-    if (int rc = check_hip(hipGetLastError(), "gqa_mixed_kernel launch")) return rc;
-  } else {
-#define AIA_GQA_LAUNCH_D(NW, D)                                                   \
-  (g.rb == 2 ? gqa_attn_kernel<NW, 2, D><<<waves, 64 * NW, 0, s>>>(a)            \
-             : gqa_attn_kernel<NW, 1, D><<<waves, 64 * NW, 0, s>>>(a))
-#define AIA_GQA_LAUNCH(NW)                                                        \
-  (head_dim == 64 ? AIA_GQA_LAUNCH_D(NW, 64) : AIA_GQA_LAUNCH_D(NW, kHeadDim))
-    switch (g.nw) {
-      case 1: AIA_GQA_LAUNCH(1); break;
-      case 2: AIA_GQA_LAUNCH(2); break;
-      case 3: AIA_GQA_LAUNCH(3); break;
-      case 4: AIA_GQA_LAUNCH(4); break;
-      case 5: AIA_GQA_LAUNCH(5); break;
-      case 6: AIA_GQA_LAUNCH(6); break;
-      case 7: AIA_GQA_LAUNCH(7); break;
-      default: AIA_GQA_LAUNCH(8); break;
-    }
-#undef AIA_GQA_LAUNCH
-#undef AIA_GQA_LAUNCH_D
-    if (int rc = check_hip(hipGetLastError(), "gqa_attn_kernel launch")) return rc;
-    if (L.pf_cap > 0) {
-      const dim3 grid((unsigned)(L.pf_unit_cap * g.hkv));
-#define AIA_PF_LAUNCH(D)                                                                   \
-  (one_block && pa.kn ? gqa_prefill_kernel<true, true, D><<<grid, kPfWaves * 64, 0, s>>>(pa)   \
-   : one_block        ? gqa_prefill_kernel<true, false, D><<<grid, kPfWaves * 64, 0, s>>>(pa)  \
-   : pa.kn            ? gqa_prefill_kernel<false, true, D><<<grid, kPfWaves * 64, 0, s>>>(pa)  \
-                      : gqa_prefill_kernel<false, false, D><<<grid, kPfWaves * 64, 0, s>>>(pa))
-      if (head_dim == 64) AIA_PF_LAUNCH(64);
-      else AIA_PF_LAUNCH(kHeadDim);
-#undef AIA_PF_LAUNCH
-      if (int rc = check_hip(hipGetLastError(), "gqa_prefill_kernel launch")) return rc;
-    }
-  }
+  if (int rc = (flags & AIA_ATTN_KV_NZ) ? launch_gqa<true>(a, pa, L, g, head_dim, waves, one_block, s)
+                                        : launch_gqa<false>(a, pa, L, g, head_dim, waves, one_block, s))
+    return rc;
   return launch_merge(ws, L, g, g.nw, head_dim, batch, num_tokens, waves, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
                       s);
 }

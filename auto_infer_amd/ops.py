@@ -253,6 +253,41 @@ def write_kv(key, value, key_cache, value_cache, slot_mapping):
                  _stream(key.device))
 
 
+def write_kv_nz(key, value, key_cache, value_cache, slot_mapping):
+    """The KV slot write into caches in the NZ layout of the reference's
+    graph-mode backend (``npu_scatter_pa_kv_cache``, auto_infer/layers/
+    attention/gqa.py:202-211): the caches are (NB, bs, Hkv, D) tensors whose
+    memory is viewed (NB, Hkv*D/16, bs, 16).  ``value``/``value_cache`` may
+    be None.  Slots outside the cache are skipped."""
+    _check_device_tensor(key, "key", _BF16)
+    _check_device_tensor(key_cache, "key_cache", _BF16)
+    _check_device_tensor(slot_mapping, "slot_mapping", torch.int32)
+    _require(key_cache.dim() == 4 and key_cache.is_contiguous(),
+             "key_cache must be a contiguous (num_blocks, block_size, Hkv, D) tensor")
+    _require(slot_mapping.dim() == 1 and slot_mapping.is_contiguous() and
+             slot_mapping.shape[0] == key.shape[0], "slot_mapping must hold one slot per token")
+    nb, bs, hkv, d = key_cache.shape
+    row = hkv * d
+    _require(key.dim() == 3 and key.shape[1] * key.shape[2] == row, "key rows do not match the cache")
+    kts = _row_stride(key, "key")
+    vts = 0
+    if value is not None:
+        _check_device_tensor(value, "value", _BF16)
+        _check_device_tensor(value_cache, "value_cache", _BF16)
+        _require(tuple(value_cache.shape) == tuple(key_cache.shape) and value_cache.is_contiguous(),
+                 "value_cache must match key_cache")
+        _require(tuple(value.shape) == tuple(key.shape), "value must match key")
+        vts = _row_stride(value, "value")
+    else:
+        _require(value_cache is None, "value_cache given without value")
+    _native.call("aia_kv_write_nz", _ptr(key), kts, _ptr(value), vts, _ptr(key_cache),
+                 _ptr(value_cache), _ptr(slot_mapping), key.shape[0], row, bs, nb * bs,
+                 _stream(key.device))
+
+
+KV_LAYOUTS = {"nd": 0, "nz": 1}   # nz: AIA_ATTN_KV_NZ
+
+
 # ---------------------------------------------------------------- attention
 
 def workspace_bytes(batch, num_tokens, num_q_heads, num_kv_heads, head_dim_v, num_waves=0):
@@ -411,7 +446,7 @@ def _check_out(out, name, shape, device):
 
 
 def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None, flags=0,
-                        key_new=None, value_new=None):
+                        key_new=None, value_new=None, kv_layout="nd"):
     """Paged GQA attention (reference base.py:48-61 FIA semantics).
 
     query (T, Hq, D) bf16 with D = 128 or 64; key/value caches (NB, bs, Hkv,
@@ -419,7 +454,12 @@ def paged_attention_gqa(query, key_cache, value_cache, plan, scale, out=None, fl
     D).  Returns (T, Hq, D) bf16.  With ``key_new`` / ``value_new`` (this
     step's new rows, (T, Hkv, D)) the kernel also writes them into the caches
     at the slots the block table assigns (the fused form of ``write_kv``).
+    ``kv_layout="nz"``: the caches hold the NZ layout of the reference's
+    graph mode (see ``write_kv_nz``); results are the same as for the same
+    values in the standard layout.
     """
+    _require(kv_layout in KV_LAYOUTS, f"kv_layout must be one of {sorted(KV_LAYOUTS)}")
+    flags |= KV_LAYOUTS[kv_layout]
     _check_device_tensor(query, "query", _BF16)
     _check_device_tensor(key_cache, "key_cache", _BF16)
     _check_device_tensor(value_cache, "value_cache", _BF16)

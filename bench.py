@@ -56,6 +56,9 @@ def parse():
     p.add_argument("--only", default=None,
                    help="run one other_configs entry and print it (for profiling): configs[1] "
                         ".. configs[4], pre_attention, mtp_compaction")
+    p.add_argument("--kv-layout", choices=("nd", "nz"), default="nd",
+                   help="cache layout of the GQA timings: nd (standard) or nz (the "
+                        "reference's graph-mode 16-wide fractal layout)")
     p.add_argument("--hbm-sweep", action="store_true",
                    help="only time plain device copies and row sums of 36 MB to 1.1 GB (the "
                         "practical HBM rate at the decode configs' sizes) and print them")
@@ -425,7 +428,15 @@ def _time_graph(fn, stream, reps, inner):
     return e0.elapsed_time(e1) * 1e3 / (reps * inner)
 
 
-def other_configs(stream, only=None):
+def nz_image(cache):
+    """The NZ memory image of a (NB, bs, Hkv, D) cache of standard-layout
+    values (each block viewed (Hkv D / 16, bs, 16)), same shape."""
+    nb, bs, h, d = cache.shape
+    return (cache.reshape(nb, bs, h * d // 16, 16).permute(0, 2, 1, 3).contiguous()
+            .reshape(nb, bs, h, d))
+
+
+def other_configs(stream, only=None, kv_layout="nd"):
     """Attention (+ merge) time of BASELINE configs 2-5 at full size, each
     with enough rotating caches to exceed the Infinity Cache, and the fused
     kernels either side of the path.  `only` selects one entry (its key:
@@ -442,6 +453,8 @@ def other_configs(stream, only=None):
         return only is None or only == key
 
     def gqa(name, step, pools, write=False):
+        if kv_layout == "nz":
+            step.k_cache, step.v_cache = nz_image(step.k_cache), nz_image(step.v_cache)
         kcs = [step.k_cache] + [torch.empty_like(step.k_cache).copy_(step.k_cache)
                                 for _ in range(pools - 1)]
         vcs = [step.v_cache] + [torch.empty_like(step.v_cache).copy_(step.v_cache)
@@ -455,7 +468,8 @@ def other_configs(stream, only=None):
         vn = step.v_new if write else None
         us = _time_graph(lambda i: ops.paged_attention_gqa(step.q, kcs[i % pools],
                                                            vcs[i % pools], plan, step.scale,
-                                                           out=out, key_new=kn, value_new=vn),
+                                                           out=out, key_new=kn, value_new=vn,
+                                                           kv_layout=kv_layout),
                          stream, 5, 2 * pools)
         by = step.kv_bytes_read() + 2 * out.numel() * 2
         if write:      # new rows read once, written once per cache
@@ -708,7 +722,7 @@ def main():
     if args.only:
         stream = torch.cuda.Stream()
         with torch.cuda.stream(stream):
-            print(json.dumps(other_configs(stream, args.only)), flush=True)
+            print(json.dumps(other_configs(stream, args.only, args.kv_layout)), flush=True)
         torch.cuda.synchronize()
         return
     dev = torch.device("cuda:0")
@@ -724,6 +738,9 @@ def main():
     bt = step.block_table.to(dev)
     gen = torch.Generator(device=dev).manual_seed(args.seed + 7)
     kcs, vcs = [step.k_cache.to(dev)], [step.v_cache.to(dev)]
+    lay = args.kv_layout
+    if lay == "nz":
+        kcs, vcs = [nz_image(kcs[0])], [nz_image(vcs[0])]
     for _ in range(L - 1):
         kcs.append((torch.randn(step.k_cache.shape, generator=gen, device=dev)
                     / 128 ** 0.5).to(torch.bfloat16))
@@ -747,7 +764,7 @@ def main():
             if layer == 0:
                 plan.replan()
             ops.paged_attention_gqa(q, kcs[layer], vcs[layer], plan, step.scale, out=out,
-                                    key_new=k_new, value_new=v_new)
+                                    key_new=k_new, value_new=v_new, kv_layout=lay)
 
     stream = torch.cuda.Stream(device=dev)
 
@@ -788,7 +805,7 @@ def main():
     with torch.cuda.stream(stream):
         a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         g2 = capture(lambda: [ops.paged_attention_gqa(q, kcs[i], vcs[i], plan, step.scale,
-                                                      out=out) for i in range(L)])
+                                                      out=out, kv_layout=lay) for i in range(L)])
         g2.replay()
         torch.cuda.synchronize()
         a0.record(stream)
@@ -855,7 +872,7 @@ def main():
     # profile summary; null if that measurement is absent.
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "gqa_decode_config1_traffic.json")
-    if os.path.exists(tpath):
+    if os.path.exists(tpath) and lay == "nd":
         with open(tpath) as f:
             traffic = int(round(json.load(f)["traffic_bytes"]))
 
@@ -878,7 +895,7 @@ def main():
             "workload": "configs[0]: GQA paged decode, Qwen3-0.6B heads Hq16/Hkv8/D128, "
                         "batch 16, Lq 1, Lk~U[128,2048], block 128, 512-block pool/layer",
             "batch": B, "kv_tokens": int(sum(step.seqlens_kv)),
-            "layers_rotated": L, "timing": "HIP graph replay, HIP events",
+            "layers_rotated": L, "kv_layout": lay, "timing": "HIP graph replay, HIP events",
             "step": "one attention layer: KV write of the 16 new rows fused into split-K "
                     "attention + merge, and the planner once per L layer-steps; value = 16 "
                     "tokens / layer-step time (tok/s per attention layer)",
@@ -905,7 +922,7 @@ def main():
     if not args.no_other_configs:
         torch.cuda.synchronize()
         with torch.cuda.stream(stream):
-            result["other_configs"] = other_configs(stream)
+            result["other_configs"] = other_configs(stream, kv_layout=lay)
         torch.cuda.synchronize()
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(step, args.cpu_seconds)

@@ -50,6 +50,21 @@ int aia_kv_write(const void* key, int64_t key_token_stride,
                  int32_t key_row_elems, int32_t value_row_elems,
                  int64_t num_slots, void* stream);
 
+/* KV slot write into caches in the NZ layout.  Replaces
+ * torch_npu.npu_scatter_pa_kv_cache of the reference's graph-mode backend
+ * (auto_infer/layers/attention/gqa.py:202-211), which scatters by
+ * slot_mapping into each cache viewed (num_blocks, Hkv * D / 16,
+ * block_size, 16): value d of head h of the token at slot s = blk *
+ * block_size + off sits at [blk][(h * D + d) / 16][off][d % 16].
+ * key / value: (num_tokens, row_elems) rows (row_elems = Hkv * D, a
+ * multiple of 16), 16-byte aligned, token strides a multiple of 8 values;
+ * value may be NULL (with value_cache NULL).  caches: num_slots = num_blocks
+ * * block_size token slots.  Slots < 0 or >= num_slots are skipped. */
+int aia_kv_write_nz(const void* key, int64_t key_token_stride, const void* value,
+                    int64_t value_token_stride, void* key_cache, void* value_cache,
+                    const int32_t* slot_mapping, int32_t num_tokens, int32_t row_elems,
+                    int32_t block_size, int64_t num_slots, void* stream);
+
 /* Bytes of workspace the attention planner/kernels need for a step of at
  * most `batch` requests and `num_tokens` query rows, planned with
  * `num_waves` key ranges (0 = the default, as in aia_attn_plan).  No
@@ -121,10 +136,15 @@ int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
  * Rows whose keys were split over several work-groups are merged by
  * log-sum-exp in a second kernel, from fp16 partials y = O / c scaled per
  * row (c = the row's largest |O|) with fp32 (max + log2 c, sum / c).
+ * flags: AIA_ATTN_KV_NZ -- the caches are in the NZ layout of the
+ * reference's graph mode (gqa.py:163,202-226; see aia_kv_write_nz); the
+ * fused KV write then writes that layout too.  Results are the same as with
+ * the same values in the standard layout.
  * If the plan overflowed (query lengths that do not add up to num_tokens:
  * the planner plans nothing and sets status -1 in the workspace header), the
  * output is filled with NaN.
- * flags must be 0. */
+ * Other flag bits must be 0. */
+#define AIA_ATTN_KV_NZ 1
 int aia_paged_attention_gqa(const void* query, int64_t q_token_stride,
                             int64_t q_head_stride,
                             const void* key_cache, const void* value_cache,

@@ -33,6 +33,43 @@ def kv_write(key, value, key_cache, value_cache, slot_mapping):
         value_cache.view(-1, vh, vd)[slots] = value.to(value_cache.dtype)
 
 
+# ---- NZ layout of the reference's graph-mode caches (gqa.py:163,195-226):
+# a (NB, bs, Hkv, D) cache tensor whose memory is viewed (NB, Hkv*D/16, bs,
+# 16) by npu_scatter_pa_kv_cache and FIA-v2.
+
+NZ = 16   # gqa.py:163
+
+
+def nz_from_nd(cache):
+    """The NZ memory image of standard-layout values: the returned (NB, bs,
+    Hkv, D) tensor, viewed (NB, Hkv*D/16, bs, 16), holds value d of head h of
+    block offset t at [blk, (h*D + d) // 16, t, d % 16]."""
+    nb, bs, h, d = cache.shape
+    return (cache.reshape(nb, bs, h * d // NZ, NZ).permute(0, 2, 1, 3).contiguous()
+            .reshape(nb, bs, h, d))
+
+
+def nd_from_nz(cache):
+    """Standard-layout values of a cache whose memory holds the NZ image."""
+    nb, bs, h, d = cache.shape
+    return cache.reshape(nb, h * d // NZ, bs, NZ).permute(0, 2, 1, 3).reshape(nb, bs, h, d)
+
+
+def kv_write_nz(key, value, key_cache, value_cache, slot_mapping):
+    """npu_scatter_pa_kv_cache(k, v, kc.view(NB, Hkv*D/16, bs, 16), ...,
+    slot_mapping) (gqa.py:202-211), in place: token t's row, split into
+    16-wide chunks, goes to [slot // bs, chunk, slot % bs, :]."""
+    for src, cache in ((key, key_cache), (value, value_cache)):
+        if src is None:
+            continue
+        nb, bs, h, d = cache.shape
+        view = cache.view(nb, h * d // NZ, bs, NZ)
+        rows = src.reshape(src.shape[0], h * d // NZ, NZ)
+        for t, s in enumerate(torch.as_tensor(slot_mapping).tolist()):
+            if 0 <= s < nb * bs:
+                view[s // bs, :, s % bs, :] = rows[t]
+
+
 def _segments(cu_seqlens_q):
     start = 0
     for end in cu_seqlens_q:

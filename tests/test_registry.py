@@ -76,6 +76,23 @@ def test_gqa_builder_and_cache_layout():
         registry.build_attention_backend(_gqa_model(), "dense", 2, 16)
 
 
+def test_gqa_nz_family_allocates_graph_mode_caches():
+    """gqa_hip_nz allocates what GraphGqaBackend.alloc_kv_caches does
+    (gqa.py:192-201): per layer two (num_blocks, block_size, n_kv, head_dim)
+    tensors."""
+    model = _gqa_model()
+    model.ATTENTION_FAMILY = "gqa_hip_nz"
+    backend, caches = registry.build_attention_backend(model, "graph", 10, 32)
+    assert isinstance(backend, GqaHipBackend) and backend.kv_layout == "nz"
+    assert len(caches) == 3
+    for kc, vc in caches:
+        assert kc.shape == vc.shape == (10, 32, 8, 128) and kc is not vc
+    backend, caches = registry.build_mtp_attention_backend(model, "graph", "model.mtp.", 5, 16)
+    assert backend.kv_layout == "nz" and caches[0][0].shape == (5, 16, 8, 128)
+    with pytest.raises(ValueError, match="kv_layout"):
+        GqaHipBackend(16, 8, 128, 0.1, 1, torch.device("cpu"), torch.bfloat16, kv_layout="nhd")
+
+
 def test_gqa_mtp_builds_one_layer_with_prefix():
     backend, caches = registry.build_mtp_attention_backend(_gqa_model(), "paged",
                                                            "model.mtp_layers.0.", 5, 16)
@@ -105,4 +122,5 @@ def test_register_into_another_registry():
         seen[name] = builder
 
     registry.register_into(reg, lambda n, b: seen_mtp.__setitem__(n, b))
-    assert set(seen) == {"gqa_hip", "mla_hip"} and set(seen_mtp) == {"gqa_hip"}
+    assert set(seen) == {"gqa_hip", "mla_hip", "gqa_hip_nz"}
+    assert set(seen_mtp) == {"gqa_hip", "gqa_hip_nz"}

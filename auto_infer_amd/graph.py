@@ -47,11 +47,16 @@ class DecodeGraph(_GearGraph):
     ``caches``: per-layer (key_cache, value_cache).  ``q``, ``k_new``,
     ``v_new``: fixed-address per-layer input buffers (T, H, D) the caller
     fills before each replay (the projections' outputs); ``out`` receives
-    each layer's attention output.
+    each layer's attention output.  ``kv_layout="nz"``: the caches are in the
+    NZ layout of the reference's graph mode (``GraphGqaBackend``,
+    gqa.py:192-226), as ``GqaHipBackend(kv_layout="nz")`` allocates them.
     """
 
     def __init__(self, stager, caches, *, num_q_heads, num_kv_heads, head_dim=128, scale=None,
-                 stream=None):
+                 stream=None, kv_layout="nd"):
+        if kv_layout not in ops.KV_LAYOUTS:
+            raise ValueError(f"kv_layout must be one of {sorted(ops.KV_LAYOUTS)}")
+        self.kv_layout = kv_layout
         self.stager = stager
         self.caches = caches
         dev = stager.block_table.device
@@ -74,7 +79,7 @@ class DecodeGraph(_GearGraph):
         for layer, (kc, vc) in enumerate(self.caches):
             ops.paged_attention_gqa(self.q[layer], kc, vc, self.plan, self.scale,
                                     out=self.out[layer], key_new=self.k_new[layer],
-                                    value_new=self.v_new[layer])
+                                    value_new=self.v_new[layer], kv_layout=self.kv_layout)
 
 
 class LatentDecodeGraph(_GearGraph):

@@ -9,13 +9,14 @@ from auto_infer_amd import packing
 from auto_infer_amd.execution import BatchPlan, RequestView, ScheduledRequest
 from auto_infer_amd.graph import DecodeGraph
 from oracle import pack
-from oracle.paged_attn import kv_write, paged_attention
+from oracle.paged_attn import kv_write, nd_from_nz, nz_from_nd, paged_attention
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-def test_decode_graph_replays_across_steps():
+@pytest.mark.parametrize("kv_layout", ["nd", "nz"])
+def test_decode_graph_replays_across_steps(kv_layout):
     rng = np.random.default_rng(0)
     gear, maxb, bs, nb, hq, hkv, d, L = 8, 16, 16, 200, 16, 8, 128, 2
     stager = packing.DecodeInputStager(
@@ -29,7 +30,10 @@ def test_decode_graph_replays_across_steps():
                torch.randn(nb, bs, hkv, d, generator=g, device=DEV, dtype=torch.bfloat16))
               for _ in range(L)]
     ref = [(k.cpu(), v.cpu()) for k, v in caches]
-    dg = DecodeGraph(stager, caches, num_q_heads=hq, num_kv_heads=hkv)
+    if kv_layout == "nz":      # the same values, in the graph mode's NZ memory layout
+        caches = [(nz_from_nd(k).to(DEV), nz_from_nd(v).to(DEV)) for k, v in ref]
+    view = nd_from_nz if kv_layout == "nz" else (lambda c: c)
+    dg = DecodeGraph(stager, caches, num_q_heads=hq, num_kv_heads=hkv, kv_layout=kv_layout)
     free = list(range(nb - gear))
     rng.shuffle(free)
     reqs = {}
@@ -62,8 +66,8 @@ def test_decode_graph_replays_across_steps():
             err = (dg.out[layer].float().cpu() - o).abs().max().item()
             print(f"step {step} layer {layer}: max-abs err {err:.3e}", flush=True)
             assert err <= 2e-2
-            assert torch.equal(caches[layer][0].cpu(), ref[layer][0])
-            assert torch.equal(caches[layer][1].cpu(), ref[layer][1])
+            assert torch.equal(view(caches[layer][0].cpu()), ref[layer][0])
+            assert torch.equal(view(caches[layer][1].cpu()), ref[layer][1])
         for r in reqs.values():
             r["pos"] += 1
 

@@ -282,3 +282,33 @@ def test_pinned_prefill_cases(case):
         err = (out.float().cpu() - exp).abs().max().item()
         print(f"max-abs err {err:.3e}", flush=True)
         assert err <= TOL
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_steps_nz_layout_equal_the_standard_layout(seed):
+    """The same random steps (head_dim 128 or 64) over caches in the NZ
+    layout of the reference's graph mode: outputs bit-identical to the
+    standard layout over the same values, and after a fused write the NZ
+    caches are the NZ image of the standard ones."""
+    from oracle.paged_attn import nz_from_nd
+    c = draw(6000 + seed)
+    d = 64 if seed % 3 == 2 else 128
+    if d == 64:
+        c["hq"], c["hkv"] = random.Random(seed).choice(HEADS_64)
+    print(f"case {seed}: d={d} {c}", flush=True)
+    step = workloads.make_gqa_step(lqs=c["lqs"], lks=c["lks"], num_q_heads=c["hq"],
+                                   num_kv_heads=c["hkv"], head_dim=d, block_size=c["bs"],
+                                   seed=seed, extra_blocks=3)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, c["hq"], c["hkv"], d, c["bs"],
+                                        num_waves=c["waves"])
+    kw = {}
+    if c["fused"]:
+        kw = dict(key_new=step.k_new.to(DEV), value_new=step.v_new.to(DEV))
+    kc, vc = step.k_cache.to(DEV), step.v_cache.to(DEV)
+    nd = ops.paged_attention_gqa(step.q.to(DEV), kc, vc, plan, step.scale, **kw)
+    kz, vz = nz_from_nd(step.k_cache).to(DEV), nz_from_nd(step.v_cache).to(DEV)
+    nz = ops.paged_attention_gqa(step.q.to(DEV), kz, vz, plan, step.scale, kv_layout="nz", **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(nz.view(torch.int16), nd.view(torch.int16))
+    assert torch.equal(kz.cpu(), nz_from_nd(kc.cpu())) and torch.equal(vz.cpu(), nz_from_nd(vc.cpu()))

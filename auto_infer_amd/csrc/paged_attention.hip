@@ -1509,11 +1509,19 @@ constexpr int kSgMfma = 0x008, kSgDsRead = 0x100;    // sched_group_barrier mask
 // 46.0).  Completion is explicit instead: every step waits vmcnt(0) before its
 // barrier.  Loads the compiler does not see can only make its own vmcnt waits
 // stricter, never too weak (the counter retires in order).
+// m0 (the LDS address of the load) is named as clobbered, which clang warns
+// about for a register it reserves: the warning is silenced here because the
+// clobber is what tells the compiler that m0 changed, and the compiler keeps
+// no value of its own in m0 in these kernels (their device assembly sets m0
+// only in front of these loads).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_load16(const uint16_t* src, uint16_t* lds) {
   const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                :: "s"(la), "v"(src) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 constexpr float kLazyLog2 = AIA_PF_LAZY;              // max growth (log2) before a rescale
 
 // Prefill attention: one work-group per (prefill item, kv head).  An item is

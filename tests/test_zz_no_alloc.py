@@ -19,14 +19,14 @@ DEV = torch.device("cuda:0")
 
 
 def _noalloc(q, kc, vc, bt, cu, kv, batch, T, hq, hkv, d, bs, nb, scale, out, kn, vn,
-             num_waves=0):
+             num_waves=0, flags=0):
     _native.call("aia_paged_attention_gqa_noalloc", q.data_ptr(), q.stride(0), q.stride(1),
                  kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), bt.stride(0), cu.data_ptr(),
                  kv.data_ptr(), batch, T, hq, hkv, d, bs, nb, float(scale), out.data_ptr(),
                  out.stride(0), out.stride(1), kn.data_ptr() if kn is not None else None,
                  vn.data_ptr() if vn is not None else None,
                  kn.stride(0) if kn is not None else 0, vn.stride(0) if vn is not None else 0,
-                 num_waves, 0, torch.cuda.current_stream(DEV).cuda_stream)
+                 num_waves, flags, torch.cuda.current_stream(DEV).cuda_stream)
 
 
 def _run_both(step, fused):
@@ -65,6 +65,31 @@ def test_noalloc_matches_workspace_entry_on_two_calls():
                                     num_kv_heads=4, block_size=128, seed=5)
     _run_both(mixed, fused=False)
     _run_both(big, fused=False)
+
+
+def test_noalloc_nz_layout_matches_workspace_entry():
+    """AIA_ATTN_KV_NZ through the allocation-free entry point: caches in the
+    reference's graph-mode NZ layout, fused write included, bit-identical to
+    the workspace entry point over the same caches."""
+    from oracle.paged_attn import nz_from_nd
+    step = workloads.make_gqa_step(lqs=[1, 2, 150, 1], lks=[700, 33, 400, 2000], num_q_heads=28,
+                                   num_kv_heads=4, block_size=16, seed=6, extra_blocks=2)
+    hq, hkv, d, bs, nb = 28, 4, 128, 16, step.k_cache.shape[0]
+    T, B = step.num_tokens, len(step.seqlens_kv)
+    q, bt = step.q.to(DEV), step.block_table.to(DEV)
+    kn, vn = step.k_new.to(DEV), step.v_new.to(DEV)
+    k1, v1 = nz_from_nd(step.k_cache).to(DEV), nz_from_nd(step.v_cache).to(DEV)
+    k2, v2 = k1.clone(), v1.clone()
+    plan = ops.AttentionPlan.from_lists(bt, step.cu_seqlens_q, step.seqlens_kv, hq, hkv, d, bs)
+    want = ops.paged_attention_gqa(q, k1, v1, plan, step.scale, key_new=kn, value_new=vn,
+                                   kv_layout="nz")
+    got = torch.empty_like(want)
+    print("no-alloc: NZ caches, mixed step with the fused write", flush=True)
+    _noalloc(q, k2, v2, bt, plan.cu_seqlens_q, plan.seqlens_kv, B, T, hq, hkv, d, bs, nb,
+             step.scale, got, kn, vn, flags=ops.KV_LAYOUTS["nz"])
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
 
 
 def test_noalloc_rejects_steps_past_its_scratch():

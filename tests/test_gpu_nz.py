@@ -147,3 +147,30 @@ def test_backend_nz_matches_nd_over_prefill_decode_and_a_foreign_slot_step():
         assert torch.equal(out_z.view(torch.int16), out_d.view(torch.int16))
         assert torch.equal(cz[0][0].cpu(), nz_from_nd(cd[0][0].cpu()))
         assert torch.equal(cz[0][1].cpu(), nz_from_nd(cd[0][1].cpu()))
+
+
+@pytest.mark.parametrize("name", ["configs[1]", "configs[3]"])
+def test_full_size_configs_nz_equal_nd(name):
+    """BASELINE configs[1] (mixed prefill chunks + 512 decode rows, one mixed
+    launch) and configs[3] (MTP verify with the fused write of both tokens)
+    at full size over NZ caches: outputs and written caches bit-identical to
+    the standard layout (which the config tests check against the oracle)."""
+    dev = torch.device(DEV)
+    if name == "configs[1]":
+        step, fused = workloads.config2_mixed(seed=0, device=dev), False
+    else:
+        step, fused = workloads.config4_mtp(seed=0, device=dev), True
+    print(f"{name}: NZ against ND at full size, fused={fused}", flush=True)
+    hq, hkv, d, bs = step.q.shape[1], step.k_cache.shape[2], step.q.shape[2], step.k_cache.shape[1]
+    plan = ops.AttentionPlan.from_lists(step.block_table, step.cu_seqlens_q, step.seqlens_kv,
+                                        hq, hkv, d, bs)
+    kw = dict(key_new=step.k_new, value_new=step.v_new) if fused else {}
+    kz, vz = nz_from_nd(step.k_cache), nz_from_nd(step.v_cache)
+    nz = ops.paged_attention_gqa(step.q, kz, vz, plan, step.scale, kv_layout="nz", **kw)
+    nd = ops.paged_attention_gqa(step.q, step.k_cache, step.v_cache, plan, step.scale, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(nz.view(torch.int16), nd.view(torch.int16))
+    if fused:
+        assert torch.equal(kz, nz_from_nd(step.k_cache)) and torch.equal(vz, nz_from_nd(step.v_cache))
+    del step, kz, vz
+    torch.cuda.empty_cache()

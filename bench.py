@@ -440,7 +440,7 @@ def other_configs(stream, only=None, kv_layout="nd"):
     """Attention (+ merge) time of BASELINE configs 2-5 at full size, each
     with enough rotating caches to exceed the Infinity Cache, and the fused
     kernels either side of the path.  `only` selects one entry (its key:
-    configs[1] .. configs[4], configs[1]_prefill, configs[1]_decode,
+    configs[0]_layouts, configs[1] .. configs[4], configs[1]_prefill, configs[1]_decode,
     prefill_long, pre_attention, mla_pre_attention, mla_v_up, mtp_compaction)."""
     import time as _time
     import numpy as np
@@ -452,8 +452,9 @@ def other_configs(stream, only=None, kv_layout="nd"):
     def want(key):
         return only is None or only == key
 
-    def gqa(name, step, pools, write=False):
-        if kv_layout == "nz":
+    def gqa(name, step, pools, write=False, layout=None):
+        layout = layout or kv_layout
+        if layout == "nz":
             step.k_cache, step.v_cache = nz_image(step.k_cache), nz_image(step.v_cache)
         kcs = [step.k_cache] + [torch.empty_like(step.k_cache).copy_(step.k_cache)
                                 for _ in range(pools - 1)]
@@ -469,7 +470,7 @@ def other_configs(stream, only=None, kv_layout="nd"):
         us = _time_graph(lambda i: ops.paged_attention_gqa(step.q, kcs[i % pools],
                                                            vcs[i % pools], plan, step.scale,
                                                            out=out, key_new=kn, value_new=vn,
-                                                           kv_layout=kv_layout),
+                                                           kv_layout=layout),
                          stream, 5, 2 * pools)
         by = step.kv_bytes_read() + 2 * out.numel() * 2
         if write:      # new rows read once, written once per cache
@@ -495,6 +496,13 @@ def other_configs(stream, only=None, kv_layout="nd"):
     def note(msg):
         print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
+    if want("configs[0]_layouts") and kv_layout == "nd":
+        # the headline workload over caches in the reference's graph-mode NZ
+        # layout beside the standard one, timed the same way (attention +
+        # merge, 8 rotating caches)
+        note("configs[0] over standard and NZ caches")
+        gqa("configs[0]_nd_layout", on_device(workloads.config1_decode(seed=0)), 8, layout="nd")
+        gqa("configs[0]_nz_layout", on_device(workloads.config1_decode(seed=0)), 8, layout="nz")
     if want("configs[1]"):
         note("configs[1] mixed prefill + decode")
         gqa("configs[1]_mixed_prefill_decode", workloads.config2_mixed(seed=0, device=dev), 1)

@@ -196,3 +196,19 @@ def test_mla_twenty_heads(waves):
     step = workloads.make_mla_step(lqs=[1, 1, 2], lks=[3000, 200, 900], num_heads=20,
                                    block_size=64, seed=20 + waves)
     check(step, waves)
+
+
+# MLA prefill-sized steps (two row blocks per segment from 2048 query rows,
+# tokens x heads, with more tokens than requests): long chunks, forced
+# splits, ragged batches with a decode row, 20 heads.
+@pytest.mark.parametrize("lqs,lks,heads,bs,waves", [
+    ([100, 60], [100 + 700, 60 + 33], 16, 64, 0),
+    ([512], [1536], 16, 128, 0),
+    ([512], [1536], 16, 128, 37),
+    ([300, 1, 200, 37], [800, 900, 200, 1037], 16, 64, 0),
+    ([420], [420 + 77], 20, 16, 0),
+])
+def test_mla_prefill_row_blocks(lqs, lks, heads, bs, waves):
+    print(f"mla prefill lqs={lqs} lks={lks} heads={heads} bs={bs} waves={waves}", flush=True)
+    step = workloads.make_mla_step(lqs=lqs, lks=lks, num_heads=heads, block_size=bs, seed=31)
+    check(step, waves)

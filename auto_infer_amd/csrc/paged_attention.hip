@@ -99,6 +99,10 @@ int32_t device_cus() {
 #ifndef AIA_PREFILL
 #define AIA_PREFILL 1
 #endif
+// AIA_MLA_PREFILL=0 keeps absorbed-MLA prefill steps on the split-K kernel.
+#ifndef AIA_MLA_PREFILL
+#define AIA_MLA_PREFILL 1
+#endif
 #ifndef AIA_PF_WAVES
 #define AIA_PF_WAVES 4
 #endif
@@ -124,6 +128,10 @@ constexpr int kPfKeys = AIA_PF_KEYS;         // keys per staged K/V tile (32 or 
 #define AIA_PF_TARGET 448
 #endif
 constexpr int kPfTargetWgs = AIA_PF_TARGET;
+#ifndef AIA_MLA_LPT
+#define AIA_MLA_LPT 1
+#endif
+
 constexpr int kPfMinChunk = 8;
 
 constexpr int64_t kMlaRb2Rows = 2048;
@@ -147,8 +155,12 @@ Geometry geometry(int32_t hq, int32_t hkv, int32_t batch, int32_t tokens, int32_
   // rows: with at least one query token per request, none holds more than
   // tokens - batch + 1.  (The planner routes nothing when this says no, so a
   // batch that breaks the assumption still runs, on split-K.)
-  g.pf = (AIA_PREFILL && (dv == kHeadDim || dv == 64) && batch > 0 &&
-          ((int64_t)tokens - batch + 1) * g.group >= kPfRows) ? 1 : 0;
+  // (absorbed MLA, whose 16 heads fill an item with 8 tokens, also needs an
+  // average of 4 tokens per request, so verify steps of 2 or 3 make no
+  // prefill launch that would find nothing routed)
+  g.pf = (AIA_PREFILL && (dv == kHeadDim || dv == 64 || (dv == 512 && AIA_MLA_PREFILL)) &&
+          batch > 0 && ((int64_t)tokens - batch + 1) * g.group >= kPfRows &&
+          (dv != 512 || tokens >= 4LL * batch)) ? 1 : 0;
   // with prefill routing, requests with many query rows leave the split-K
   // kernel, whose segments are then decode / short-verify sized
   // (MLA, dv 512: a token's heads fill a block.  Two blocks halve the
@@ -370,6 +382,12 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   // Every loop below runs over the flat item list (request-major, each
   // request's items last rows first), one item per thread.
   int units = 0, pmerges = 0, dealt = 0;
+  // Fill target.  Absorbed-MLA units (158 KB of LDS) run one per CU: few
+  // items are cut into one round of units (8 x 64 tokens at 4096 keys: 172
+  // us against 205 at 448), many into about 1.75 rounds so the causal
+  // items even out (1 x 2048 tokens: 218 against 280 at one round).
+  const int pf_target = dv != 512 || g.ncu <= 0 || g.ncu >= kPfTargetWgs ? kPfTargetWgs
+                        : (int64_t)pcarry * g.hkv <= g.ncu / 2 ? g.ncu : kPfTargetWgs;
   if (pcarry > 0) {
     __syncthreads();   // item offsets
     const int* cu_p = req_lds ? cuv : cu_q;
@@ -390,7 +408,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       return (kend + kPfKeys - 1) / kPfKeys;
     };
     int chunk = 0x7fffffff;
-    if ((int64_t)pcarry * g.hkv < kPfTargetWgs) {
+    if ((int64_t)pcarry * g.hkv < pf_target) {
       int mine = 0;
       for (int f = tid; f < pcarry; f += kPlanThreads) {
         int b, r0;
@@ -400,14 +418,14 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       block_exclusive_scan(mine, wave_sums, &wtot);
       // sum_i ceil(nt_i / c) <= W / c + P, so c = W Hkv / (target - P Hkv)
       // keeps units x kv heads within the target: one round of work-groups
-      const int64_t room = kPfTargetWgs - (int64_t)pcarry * g.hkv;
+      const int64_t room = pf_target - (int64_t)pcarry * g.hkv;
       chunk = max(kPfMinChunk, (int)(((int64_t)wtot * g.hkv + room - 1) / room));
       // That bound is loose.  In a step with no split-K segments the least
       // chunk whose units still fit evens the work-groups out (the slowest
       // one sets the kernel time), found by a binary search, one block
       // reduction per probe.  Beside split-K ranges the loose bound stays:
       // its fewer work-groups leave slots for the HBM-bound ranges.
-      const int ucap = kPfTargetWgs / g.hkv;
+      const int ucap = pf_target / g.hkv;
       int lo = carry > 0 ? chunk : max(kPfMinChunk, (wtot + ucap - 1) / ucap);
       while (lo < chunk) {
         const int mid = (lo + chunk) >> 1;
@@ -473,7 +491,12 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     // each XCD gets a contiguous run of pairs, kv-head major, so the items
     // that re-read one request's keys for one kv head share an XCD's L2.
     const int jobs = units * g.hkv;
-    if (jobs <= kPfTargetWgs && !(carry == 0 && jobs > g.ncu && jobs <= 2 * g.ncu)) {
+    // Absorbed-MLA units run one per CU: in more than one round the next
+    // work-group goes to whichever CU frees first, so they are dealt largest
+    // first (the longest-processing-time order).
+    const bool lpt = dv == 512 && AIA_MLA_LPT;
+    const bool pair_deal = !lpt && carry == 0 && jobs > g.ncu && jobs <= 2 * g.ncu;
+    if (jobs <= pf_target && !pair_deal && !lpt) {
       __syncthreads();   // publishes pf_units to the whole group
       const int q = jobs / kXcdsPlan, r = jobs - q * kXcdsPlan;
       for (int id = tid; id < jobs; id += kPlanThreads) {
@@ -486,7 +509,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       }
       dealt = jobs;
     }
-    if (carry == 0 && jobs > g.ncu && jobs <= 2 * g.ncu && jobs <= kPfTargetWgs) {
+    if ((pair_deal || lpt) && jobs <= pf_target) {
       if (tid < 64) pf_hist[tid] = 0;
       __syncthreads();   // also publishes pf_units to the whole group
       for (int p = tid; p < jobs; p += kPlanThreads) {
@@ -505,7 +528,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
         const int4 e = pf_units[2 * u];
         const int r = atomicAdd(&pf_hist[63 - min(e.w - e.z, 63)], 1);
         const int i = r - lone;
-        const int id = r < lone ? n2 + r : i < n2 ? i : g.ncu + (jobs - 1 - r);
+        const int id = lpt ? r : r < lone ? n2 + r : i < n2 ? i : g.ncu + (jobs - 1 - r);
         pf_wg[3 * id] = e;
         pf_wg[3 * id + 1] = pf_units[2 * u + 1];
         pf_wg[3 * id + 2] = make_int4(u, kvh, 0, 0);
@@ -2556,6 +2579,324 @@ void mla_attn_kernel(MlaArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- absorbed-MLA prefill units
+//
+// Prefill items of the absorbed-MLA path (one latent head of 576 values, V =
+// its first 512, Hq query heads), planned as the GQA units are (128-row items
+// of one request's (token, head) rows, cut into key chunks when they are
+// few, chunk partials folded by the merge kernel).  A work-group of 4 waves,
+// one per SIMD, takes its unit's rows in two passes of 64, 16 rows per wave:
+//   Q (16 rows x 576) as MFMA operands in registers (72 VGPRs) and O (16 x
+//   512 fp32, 128 registers); 32 rows per wave would need about 400;
+//   keys go through LDS in 32-key sub-tiles, a ring of four buffers filled by
+//   direct loads three sub-tiles ahead (at one wave per SIMD no other wave
+//   covers a load's latency), one barrier per sub-tile;
+//   per sub-tile: QK^T over 576 dims (four accumulation chains per 16 keys),
+//   softmax, PV over the first 512 dims (V^T through transposing reads).
+// The cache slots of a sub-tile's keys are computed by wave 0 four
+// sub-tiles ahead from the unit's block ids, which it stages in LDS (2048
+// at a time) so that no load the compiler tracks sits behind the direct
+// loads in the loop (its wait would drain them).
+// LDS sub-tile: the 512 latent values of key r (1 KB, one direct load) at
+// row r of stride 1040 bytes -- the 16-byte pad puts the 16 keys of a K
+// fragment read, and the keys of a V^T read group, on different banks --
+// then the 64 rope values of every key, 128 bytes per key, its eight 16-byte
+// chunks swizzled (chunk c at c ^ (r mod 8)) since eight keys' rope share
+// one direct load.
+constexpr int kMlaSub = 32;                                       // keys per sub-tile
+constexpr int kMlaRing = 4;                                       // sub-tile buffers
+constexpr int kMlaAhead = kMlaRing - 1;                           // loads ahead
+constexpr int kMlaPfRow = 520;                                    // latent row stride (elements)
+constexpr int kMlaPfRope = kMlaSub * kMlaPfRow;                   // rope region offset
+constexpr int kMlaPfBuf = kMlaPfRope + kMlaSub * (kMlaK - kMlaV);   // elements per buffer
+constexpr int kMlaLoads = kMlaSub / kPfWaves + 1;                 // direct loads per wave
+constexpr int kMlaBtl = 2048;                                     // staged block ids
+constexpr int kMlaKJ = kMlaK / 32;                                // 18 QK k-steps
+constexpr int kMlaDT = kMlaV / 16;                                // 32 output tiles
+constexpr int kMlaPassRows = kPfWaves * kRows;                    // 64 rows per pass
+constexpr float kMlaPfSpan = 64.f;   // log2 growth allowed over a row's reference max
+// s_waitcnt immediate: vmcnt(n) only (vmcnt bits 3:0 and 15:14)
+constexpr int wait_vmcnt(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+static_assert(wait_vmcnt(0) == kWaitVmcnt0, "s_waitcnt encoding");
+static_assert(kPfWaves == 4 && kPfKeys == 2 * kMlaSub && kPfRows % kMlaPassRows == 0 &&
+              kMlaV == 512 && kMlaK - kMlaV == 64 && kMlaSub == 8 * kPfWaves,
+              "MLA prefill unit shape");
+
+__global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void mla_prefill_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t ring[kMlaRing * kMlaPfBuf];
+  __shared__ int slots[kMlaRing][kMlaSub];
+  __shared__ int btl[kMlaBtl];
+  __shared__ int rerun_flag;
+  const int wg = blockIdx.x;
+  // this work-group's unit, as the GQA units take theirs (one kv head)
+  int4 w0 = make_int4(0, 0, 0, 0), w1 = w0, w2 = w0;
+  if (wg < kPfTargetWgs) {
+    w0 = a.dealt[3 * wg];
+    w1 = a.dealt[3 * wg + 1];
+    w2 = a.dealt[3 * wg + 2];
+  }
+  const int count = a.hdr[6];
+  if (wg >= count) return;
+  int unit;
+  int4 it, iq;
+  if (a.hdr[9] == count) {
+    it = w0;
+    iq = w1;
+    unit = w2.x;
+    if (unit < 0 || unit >= count) return;
+  } else {
+    unit = xcd_range(wg, count);
+    it = a.units[2 * unit];
+    iq = a.units[2 * unit + 1];
+  }
+  const int b = it.x, row0 = it.y, t0 = it.z, t1 = it.w;
+  if (b < 0 || b >= a.batch) return;
+  const int q_begin = iq.x, lq = iq.y, lk = iq.z;
+  const int G = a.group;
+  const int nrows = lq * G;
+  if (row0 < 0 || row0 >= nrows || q_begin < 0 || q_begin + lq > a.tokens) return;
+  const int ctx0 = lk - lq;
+  const int row_end = min(nrows, row0 + kPfRows);
+  const int kend = max(0, min(lk, ctx0 + (row_end - 1) / G + 1));   // the item's keys
+  const int ntiles = (kend + kPfKeys - 1) / kPfKeys;
+  if (t0 < 0 || t1 < t0 || t1 > ntiles) return;
+  const bool whole = t0 == 0 && t1 == ntiles;
+  if (!whole && unit >= a.part_units) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
+  const int bs = a.bs;
+
+  // Wave 0: stage block ids [wb, wb + kMlaBtl) of the row (those below nbk)
+  int wb = -1;
+  auto stage_ids = [&](int first, int nbk) __attribute__((always_inline)) {
+    wb = first;
+    for (int e = lane; e < kMlaBtl && first + e < nbk; e += 64)
+      btl[e] = min(max(btrow[first + e], 0), a.nb - 1);
+  };
+  // Wave 0, lanes 0..31: cache slots of sub-tile v's keys (keys past the
+  // pass's last visible one re-read it)
+  auto make_slots = [&](int v, int kendp, int nbk) __attribute__((always_inline)) {
+    const int p = min(v * kMlaSub + lane, kendp - 1);
+    const int bi = p / bs;
+    if (__builtin_amdgcn_readfirstlane((v * kMlaSub) / bs) < wb ||
+        __builtin_amdgcn_readfirstlane(min(v * kMlaSub + kMlaSub, kendp) - 1) / bs >= wb + kMlaBtl)
+      stage_ids((v * kMlaSub) / bs, nbk);       // rare: a unit spanning more than kMlaBtl blocks
+    if (lane < kMlaSub) slots[v % kMlaRing][lane] = btl[bi - wb] * bs + (p - bi * bs);
+  };
+  // Direct loads of sub-tile v into its ring buffer: wave w loads the latent
+  // of keys 8 w .. 8 w + 7 (one key per load, lane l its chunk l) and their
+  // rope (lane l chunk (l % 8) ^ (key % 8) of key 8 w + l / 8).
+  auto issue = [&](int v) __attribute__((always_inline)) {
+    uint16_t* dst = ring + (v % kMlaRing) * kMlaPfBuf;
+    const int* sl = slots[v % kMlaRing];
+#pragma unroll
+    for (int i = 0; i < kMlaSub / kPfWaves; ++i) {
+      const int r = wid * (kMlaSub / kPfWaves) + i;
+      const int slot = __builtin_amdgcn_readfirstlane(sl[r]);
+      lds_load16(a.kc + (int64_t)slot * kMlaK + 8 * lane, dst + r * kMlaPfRow);
+    }
+    const int r = wid * (kMlaSub / kPfWaves) + (lane >> 3);
+    lds_load16(a.kc + (int64_t)sl[r] * kMlaK + kMlaV + 8 * ((lane & 7) ^ (r & 7)),
+               dst + kMlaPfRope + wid * (kMlaSub / kPfWaves) * 64);
+  };
+
+  for (int pass = 0; pass < kPfRows / kMlaPassRows; ++pass) {
+    const int prow0 = row0 + pass * kMlaPassRows;
+    if (prow0 >= row_end) break;                      // uniform over the work-group
+    const int prow_end = min(row_end, prow0 + kMlaPassRows);
+    // keys this pass's last row sees, and its share of the unit's sub-tiles
+    const int kendp = max(0, min(lk, ctx0 + (prow_end - 1) / G + 1));
+    const int u0 = 2 * t0;
+    const int u1 = min(2 * t1, (kendp + kMlaSub - 1) / kMlaSub);
+    const int nbk = (kendp + bs - 1) / bs;            // blocks the pass may touch
+
+    const int row = prow0 + wid * kRows + n;
+    const bool rv = row < prow_end;
+    const int tokr = row / G, headr = row - tokr * G;
+    const int lim = rv ? min(ctx0 + tokr, lk - 1) : -1;
+    int wlim_lo = rv ? lim : 0x7fffffff, wlim_hi = lim;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      wlim_lo = min(wlim_lo, __shfl_xor(wlim_lo, d));
+      wlim_hi = max(wlim_hi, __shfl_xor(wlim_hi, d));
+    }
+    uint4 qf[kMlaKJ];
+    if (rv) {
+      const uint4* qp = reinterpret_cast<const uint4*>(
+          a.q + (int64_t)(q_begin + tokr) * a.q_ts + (int64_t)headr * a.q_hs);
+#pragma unroll
+      for (int j = 0; j < kMlaKJ; ++j) qf[j] = qp[4 * j + g];
+    } else {
+#pragma unroll
+      for (int j = 0; j < kMlaKJ; ++j) qf[j] = make_uint4(0, 0, 0, 0);
+    }
+    // Softmax without rescaling O: a row's reference m is its max over its
+    // first visible sub-tile, and later scores may exceed it by up to
+    // 2^kMlaPfSpan (P then stays a finite bf16, O and l finite fp32), so the
+    // loop holds no rescale branch (one would keep O's 128 registers moving
+    // between register files every sub-tile).  A row whose scores climb
+    // further sets `ovf`, and the work-group then runs its sub-tiles again
+    // with every row's exact max as m (rmax, tracked on the way).
+    float4_t o[kMlaDT];
+    float m = -INFINITY, lsum = 0.f, rmax = -INFINITY;
+    bool ovf = false;
+
+#pragma clang loop unroll(disable)
+    for (int attempt = 0; attempt < 2; ++attempt) {
+      // O lives in the accumulation registers throughout (the empty asm
+      // pins it there; left to itself the compiler copied all 128 values
+      // between register files every sub-tile)
+#pragma unroll
+      for (int dt = 0; dt < kMlaDT; ++dt) {
+        o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+        asm volatile("" : "+a"(o[dt]));
+      }
+      lsum = 0.f;
+      if (attempt > 0) { m = rmax; ovf = false; }   // every row's exact max
+      if (u1 > u0) {
+        // prologue: Q has arrived; slots of the first four sub-tiles, then
+        // the loads of the first three
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();                              // the ring is free
+        if (wid == 0) {
+          wb = -1;
+          stage_ids((u0 * kMlaSub) / bs, nbk);
+          __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+          for (int v = u0; v < min(u1, u0 + kMlaRing); ++v) make_slots(v, kendp, nbk);
+        }
+        __syncthreads();
+        for (int v = u0; v < min(u1, u0 + kMlaAhead); ++v) issue(v);
+#pragma clang loop unroll(disable)
+        for (int u = u0; u < u1; ++u) {
+          // sub-tile u's loads are the oldest of up to three in flight
+          const int younger = min(kMlaAhead - 1, u1 - 1 - u);
+          if (younger >= 2) __builtin_amdgcn_s_waitcnt(wait_vmcnt(2 * kMlaLoads));
+          else if (younger == 1) __builtin_amdgcn_s_waitcnt(wait_vmcnt(kMlaLoads));
+          else __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+          __syncthreads();
+          const uint16_t* kt = ring + (u % kMlaRing) * kMlaPfBuf;
+          const int kb = u * kMlaSub;
+          if (kb <= wlim_hi) {                        // some row of this wave sees the keys
+            float4_t acc[2];
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+              const int r = 16 * s2 + n;
+              const uint16_t* kl = kt + r * kMlaPfRow + 8 * g;
+              float4_t part[4];
+#pragma unroll
+              for (int c4 = 0; c4 < 4; ++c4) part[c4] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int j = 0; j < kMlaKJ - 2; ++j)
+                part[j & 3] = qk_step(*reinterpret_cast<const uint4*>(kl + 32 * j), qf[j], part[j & 3]);
+#pragma unroll
+              for (int j = kMlaKJ - 2; j < kMlaKJ; ++j) {
+                const int c = (4 * (j - (kMlaKJ - 2)) + g) ^ (r & 7);
+                part[j & 3] = qk_step(*reinterpret_cast<const uint4*>(kt + kMlaPfRope + r * 64 + 8 * c),
+                                      qf[j], part[j & 3]);
+              }
+              acc[s2] = (part[0] + part[1]) + (part[2] + part[3]);
+            }
+            if (u + kMlaAhead < u1) issue(u + kMlaAhead);
+            const bool mask = kb + kMlaSub - 1 > wlim_lo;
+            float sv[2][4];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                sv[s2][v] = (mask && kb + 16 * s2 + 4 * g + v > lim) ? -INFINITY : acc[s2][v];
+                tmax = fmaxf(tmax, sv[s2][v]);
+              }
+            tmax = aia::group4_max(tmax);
+            const float tm = tmax * a.scale_log2;
+            rmax = fmaxf(rmax, tm);
+            if (m == -INFINITY) m = tm;               // O and l are still zero
+            ovf = ovf || tm > m + kMlaPfSpan;
+            const float msub = m == -INFINITY ? 0.f : m;
+            float p[2][4];
+            float psum = 0.f;
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                p[s2][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[s2][v], a.scale_log2, -msub));
+                psum += p[s2][v];
+              }
+            lsum += psum;
+            uint4 pb;
+            pb.x = aia::pack_bf16x2(p[0][0], p[0][1]);
+            pb.y = aia::pack_bf16x2(p[0][2], p[0][3]);
+            pb.z = aia::pack_bf16x2(p[1][0], p[1][1]);
+            pb.w = aia::pack_bf16x2(p[1][2], p[1][3]);
+            // PV: lane (n, g) addresses key 4 g + n / 4 (and + 16), dims
+            // 16 dt + 4 (n % 4)
+            const uint16_t* v0p = kt + (4 * g + (n >> 2)) * kMlaPfRow + 4 * (n & 3);
+            const uint16_t* v1p = v0p + 16 * kMlaPfRow;
+#pragma unroll
+            for (int dt = 0; dt < kMlaDT; ++dt) {
+              const short4_t x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(v0p + 16 * dt));
+              const short4_t x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(v1p + 16 * dt));
+              const bf16x8_t va = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+              o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, as_b8(pb), o[dt], 0, 0, 0);
+            }
+#pragma unroll
+            for (int dt = 0; dt < kMlaDT; ++dt) asm volatile("" : "+a"(o[dt]));
+          } else if (u + kMlaAhead < u1) {
+            issue(u + kMlaAhead);
+          }
+          // slots of sub-tile u + 4 into the ring slot sub-tile u's loads used
+          if (wid == 0 && u + kMlaRing < u1) make_slots(u + kMlaRing, kendp, nbk);
+        }
+      }
+      // a row past its reference span: the work-group runs its sub-tiles again
+      if (tid == 0) rerun_flag = 0;
+      __syncthreads();
+      if (__any(ovf) && lane == 0) rerun_flag = 1;
+      __syncthreads();
+      const int rerun = rerun_flag;
+      __syncthreads();
+      if (!rerun) break;
+    }
+
+    lsum = aia::group4_sum(lsum);
+    float cmax = 0.f;
+    if (!whole) {
+#pragma unroll
+      for (int dt = 0; dt < kMlaDT; ++dt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) cmax = fmaxf(cmax, fabsf(o[dt][v]));
+      cmax = aia::group4_max(cmax);
+    }
+    if (!rv) continue;
+    if (!whole) {      // partial: y = O / c in fp16, (m + log2 c, l / c)
+      const float c = cmax > 0.f ? cmax : 1.f, ic = 1.f / c;
+      const int64_t prow = (int64_t)unit * kPfRows + (row - row0);
+      uint16_t* pp = a.part_o + prow * kMlaV;
+#pragma unroll
+      for (int dt = 0; dt < kMlaDT; ++dt) {
+        uint2 hv;
+        hv.x = pack_f16x2(o[dt][0] * ic, o[dt][1] * ic);
+        hv.y = pack_f16x2(o[dt][2] * ic, o[dt][3] * ic);
+        *reinterpret_cast<uint2*>(pp + 16 * dt + 4 * g) = hv;
+      }
+      if (g == 0) a.part_ml[prow] = make_float2(m + __log2f(c), lsum * ic);
+      continue;
+    }
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    uint16_t* op = a.out + (int64_t)(q_begin + tokr) * a.o_ts + (int64_t)headr * a.o_hs;
+#pragma unroll
+    for (int dt = 0; dt < kMlaDT; ++dt) {
+      uint2 wv;
+      wv.x = aia::pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
+      wv.y = aia::pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
+      *reinterpret_cast<uint2*>(op + 16 * dt + 4 * g) = wv;
+    }
+  }
+}
+
 int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32_t dv, int32_t batch,
                  int32_t tokens, int32_t waves,
                  const uint16_t* part_o,
@@ -2827,7 +3168,6 @@ extern "C" int aia_paged_attention_mla(
     void* out, int64_t out_token_stride, int64_t out_head_stride, int32_t num_waves, int32_t flags,
     void* workspace, int64_t workspace_bytes, void* stream) {
   using namespace aia;
-  (void)cu_seqlens_q; (void)seqlens_kv;
   if (flags != 0) return fail(AIA_ERR_INVALID, "aia_paged_attention_mla: flags must be 0");
   if (kv_lora_rank != kMlaV || rope_dim != kMlaK - kMlaV)
     return fail(AIA_ERR_UNSUPPORTED, "aia_paged_attention_mla: latent %d + rope %d (only 512 + 64)",
@@ -2872,6 +3212,25 @@ extern "C" int aia_paged_attention_mla(
   if (g.rb == 2) mla_attn_kernel<2><<<waves, 256, 0, s>>>(a);
   else mla_attn_kernel<1><<<waves, 256, 0, s>>>(a);
   if (int rc = check_hip(hipGetLastError(), "mla_attn_kernel launch")) return rc;
+  if (L.pf_cap > 0) {     // prefill items (requests of 128+ rows)
+    PrefillArgs pa = {};
+    pa.q = a.q; pa.q_ts = a.q_ts; pa.q_hs = a.q_hs;
+    pa.kc = const_cast<uint16_t*>(a.cache);
+    pa.bt = block_table; pa.bt_stride = block_table_stride;
+    pa.cu_q = cu_seqlens_q; pa.kvlen = seqlens_kv;
+    pa.hkv = 1; pa.group = g.group; pa.bs = block_size; pa.nb = num_blocks;
+    pa.batch = batch; pa.tokens = num_tokens;
+    pa.scale_log2 = a.scale_log2;
+    pa.out = a.out; pa.o_ts = a.o_ts; pa.o_hs = a.o_hs;
+    pa.units = reinterpret_cast<const int4*>(ws + L.pf);
+    pa.dealt = reinterpret_cast<const int4*>(ws + L.pfw);
+    pa.hdr = a.hdr;
+    pa.part_o = reinterpret_cast<uint16_t*>(ws + L.pf_o);
+    pa.part_ml = reinterpret_cast<float2*>(ws + L.pf_ml);
+    pa.part_units = (int32_t)L.pf_slots;
+    mla_prefill_kernel<<<(unsigned)L.pf_unit_cap, kPfWaves * 64, 0, s>>>(pa);
+    if (int rc = check_hip(hipGetLastError(), "mla_prefill_kernel launch")) return rc;
+  }
   return launch_merge(ws, L, g, 1, kMlaV, batch, num_tokens, waves, a.part_o, a.part_ml, a.seg, a.out, a.o_ts, a.o_hs,
                       s);
 }

@@ -441,7 +441,7 @@ def other_configs(stream, only=None, kv_layout="nd"):
     with enough rotating caches to exceed the Infinity Cache, and the fused
     kernels either side of the path.  `only` selects one entry (its key:
     configs[0]_layouts, configs[1] .. configs[4], configs[1]_prefill, configs[1]_decode,
-    prefill_long, pre_attention, mla_pre_attention, mla_v_up, mtp_compaction)."""
+    prefill_long, mla_prefill, pre_attention, mla_pre_attention, mla_v_up, mtp_compaction)."""
     import time as _time
     import numpy as np
     from auto_infer_amd import ops, packing, workloads
@@ -546,6 +546,27 @@ def other_configs(stream, only=None, kv_layout="nd"):
                                           "frac_of_peak": round(by / us / 1e3 / HBM_PEAK_GBS, 4)}
         del caches, mla
 
+    if want("mla_prefill"):
+        # not a BASELINE config: absorbed-MLA prefill steps (configs[2]'s head
+        # shape), which the MLA prefill units take
+        note("absorbed-MLA prefill steps")
+        for lqs, lks, key in (([2048], [2048], "mla_prefill_1x2048_at_2048"),
+                              ([64] * 8, [4096] * 8, "mla_prefill_8x64_at_4096")):
+            st = workloads.make_mla_step(lqs=lqs, lks=lks, num_heads=16, block_size=128, seed=3,
+                                         device=dev)
+            plan = ops.AttentionPlan.from_lists(st.block_table, st.cu_seqlens_q, st.seqlens_kv,
+                                                16, 1, 512, 128)
+            out = torch.empty(st.num_tokens, 16, 512, dtype=torch.bfloat16, device=dev)
+            torch.cuda.synchronize()
+            us = _time_graph(lambda i: ops.paged_attention_mla(st.q_latent, st.cache, plan,
+                                                               st.scale, out=out), stream, 5, 4)
+            starts = [0] + list(st.cu_seqlens_q[:-1])
+            vis = sum(lq * (lk - lq) + lq * (lq + 1) // 2 for lq, lk in
+                      ((e - b, k) for b, e, k in zip(starts, st.cu_seqlens_q, st.seqlens_kv)))
+            fl = 16.0 * vis * (576 + 512) * 2
+            res[key] = {"attn_us": round(us, 2), "TFLOPs": round(fl / us / 1e6, 1),
+                        "frac_of_bf16_mfma_peak": round(fl / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}
+            del st, out
     if want("pre_attention"):
         note("pre-attention: fused QK-norm + RoPE at the configs[1] shape")
         from auto_infer_amd.attention.layers import rms_norm, rotate_half

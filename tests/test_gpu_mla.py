@@ -212,3 +212,30 @@ def test_mla_prefill_row_blocks(lqs, lks, heads, bs, waves):
     print(f"mla prefill lqs={lqs} lks={lks} heads={heads} bs={bs} waves={waves}", flush=True)
     step = workloads.make_mla_step(lqs=lqs, lks=lks, num_heads=heads, block_size=bs, seed=31)
     check(step, waves)
+
+
+# MLA prefill units (requests of 8+ tokens, 4+ tokens per request on
+# average): 128-row items in two 64-row passes, 32-key sub-tiles in a ring
+# of four LDS buffers.  Cases: units cut into key chunks (partials and the
+# chunk merge), one request against 16K keys, a block size of 4 with more
+# than 2048 blocks under one unit (the staged block ids are replaced
+# mid-unit), units beside split-K rows, and scores spread so wide that a
+# row exceeds its reference max by 2^64 (the unit runs its tiles again).
+@pytest.mark.parametrize("lqs,lks,bs,heads", [
+    ([64] * 8, [4096] * 8, 128, 16),
+    ([512], [16384], 128, 16),
+    ([64], [12000], 4, 16),
+    ([40, 1, 1, 9, 24], [2000, 300, 5000, 9, 24 + 700], 16, 16),
+    ([16] * 6, [((i * 777) % 3000) + 16 for i in range(6)], 64, 32),
+])
+def test_mla_prefill_units(lqs, lks, bs, heads):
+    print(f"mla prefill units lqs={lqs[:5]} lks={lks[:5]} bs={bs} heads={heads}", flush=True)
+    step = workloads.make_mla_step(lqs=lqs, lks=lks, num_heads=heads, block_size=bs, seed=41)
+    check(step)
+
+
+def test_mla_prefill_unit_reruns_with_exact_row_maxima():
+    step = workloads.make_mla_step(lqs=[96, 40], lks=[1500, 40 + 900], block_size=64, seed=43)
+    step.q_latent = (step.q_latent.float() * 40).to(torch.bfloat16)
+    print("mla prefill units with scores spread past 2^64", flush=True)
+    check(step)

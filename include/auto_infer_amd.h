@@ -205,6 +205,8 @@ int aia_noalloc_scratch_bytes(int64_t* bytes);
  * q_latent:     (num_tokens, num_heads, 576), token/head strides given.
  * latent_cache: contiguous (num_blocks, block_size, 1, 576).
  * out:          (num_tokens, num_heads, 512).
+ * Requests of 8+ tokens (in steps of 4+ tokens per request on average) run
+ * on prefill units, the rest on split-K ranges; the caller sees one call.
  * The plan must come from aia_attn_plan(num_q_heads = num_heads,
  * num_kv_heads = 1, head_dim_v = 512, same num_waves).  flags must be 0. */
 int aia_paged_attention_mla(const void* q_latent, int64_t q_token_stride,

@@ -119,7 +119,9 @@ int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens_kv,
  * causal), query head h reads KV head h / (Hq / Hkv), KV row j at
  * block_table[b, j / block_size], offset j % block_size.
  * query:  (num_tokens, Hq, head_dim) with the given token/head strides.
- * caches: contiguous (num_blocks, block_size, Hkv, head_dim).
+ * caches: contiguous (num_blocks, block_size, Hkv, head_dim), with
+ *         num_blocks * block_size < 2^31 (the int32 slot_mapping's range;
+ *         AIA_ERR_INVALID otherwise, here and in aia_paged_attention_mla).
  * out:    (num_tokens, Hq, head_dim) with the given strides.
  * head_dim must be 128 (Qwen2-7B, Qwen3) or 64 (Qwen2 / Qwen2.5 0.5B:
  * hidden 896 over 14 heads), AIA_ERR_UNSUPPORTED otherwise; scale must be

@@ -2103,18 +2103,28 @@ __global__ __launch_bounds__(64 * kMergeGroups) void merge_kernel(MergeArgs a) {
   const int pf_tpr = a.dv / 8, pf_rpp = kMergeThreads / pf_tpr;
   const int kSlices = kPfRows / pf_rpp;
   const int per_rec = a.hkv * kSlices;
-  // planner status, read now and used at the end (no extra round trip)
-  const int status = a.hdr[8];
-  int4 pr0 = make_int4(0, 0, 0, 0);
-  int npm = 0;
-  if (a.pf_mrg) {
-    if (blockIdx.x < a.pf_items_cap) pr0 = a.pf_mrg[blockIdx.x / per_rec];
-    npm = a.hdr[7];
-  }
-  for (int64_t item = blockIdx.x; item < a.mrg_cap; item += gridDim.x) {
-    const int4 m0 = *reinterpret_cast<const int4*>(a.mrg + item * kMrgInts);
-    const int4 m1 = *reinterpret_cast<const int4*>(a.mrg + item * kMrgInts + 4);
-    if (item >= a.hdr[5]) break;                           // uniform over the group
+  // The header words, this work-group's first merge record and its first
+  // prefill record are loaded in straight-line code before any branch, so
+  // they go out together (one round trip, then one for the partials);
+  // behind a branch the compiler issued them one after another.  An index
+  // past a list reads the header instead, and its value is not used.
+  const int64_t item0 = blockIdx.x;
+  const int4* mp = item0 < a.mrg_cap ? reinterpret_cast<const int4*>(a.mrg + item0 * kMrgInts)
+                                     : reinterpret_cast<const int4*>(a.hdr);
+  const int4* pp0 = a.pf_mrg && item0 < a.pf_items_cap ? a.pf_mrg + (int)blockIdx.x / per_rec
+                                                         : reinterpret_cast<const int4*>(a.hdr);
+  const int4 m0_first = mp[0], m1_first = mp[1];
+  const int4 pr0 = pp0[0];
+  const int nmrg = a.hdr[5], npm_hdr = a.hdr[7];
+  const int status = a.hdr[8];             // planner status, used at the end
+  const int npm = a.pf_mrg ? npm_hdr : 0;
+  // the first test reads the first record too (a record has at least two
+  // parts), which keeps its loads ahead of the first branch
+  const bool first_live = (item0 < a.mrg_cap) & (item0 < nmrg) & (m1_first.y >= 2);
+  for (int64_t item = item0; first_live && item < a.mrg_cap; item += gridDim.x) {
+    if (item >= nmrg) break;                               // uniform over the group
+    const int4 m0 = item == item0 ? m0_first : *reinterpret_cast<const int4*>(a.mrg + item * kMrgInts);
+    const int4 m1 = item == item0 ? m1_first : *reinterpret_cast<const int4*>(a.mrg + item * kMrgInts + 4);
     const int qtok0 = m0.x, nq = m0.y, kvh = m0.z, hbi = m0.w;
     const int row_base = m1.x, np = m1.y, sl = m1.z, rows = m1.w;
     // A slice of fewer than 64 elements (a decode segment's few rows) takes

@@ -191,10 +191,33 @@ int64_t merge_slices(const Geometry& g, int32_t dv) {
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
+// Fixed partial slots.  In a small step (the geometry the small planner
+// serves, whose partial buffer is sized for kFixParts slots per segment)
+// whose segments are each split over at most kFixParts ranges, segment s
+// writes its partials to slots [kFixParts s, kFixParts s + np): the merge
+// work-group of (segment, kv head) then knows where its partials are without
+// reading a merge record, and issues those loads together with the
+// header's, one round trip instead of two.  hdr[10] = 1 marks such a plan.
+// Both planners decide it the same way, from the slot capacity the host
+// passes (fix_cap, 0 outside the geometry) and the ranges.
+constexpr int kFixParts = 32;
+constexpr int kSmallPlanSegs = 64;
+
+// The geometry of small steps: GQA without prefill routing, at most 64
+// requests and segments.  Their plans may use fixed partial slots (see
+// kFixParts), whichever planner makes them.
+bool small_geometry(const Geometry& g, int32_t dv, int32_t batch, int64_t seg_cap) {
+  return dv != 512 && !g.pf && batch >= 1 && batch <= 64 && seg_cap <= kSmallPlanSegs;
+}
+
+
 Layout layout(int32_t batch, int32_t tokens, const Geometry& g, int32_t dv, int32_t waves) {
   Layout L;
   L.seg_cap = (int64_t)g.nkvg * g.nhb * (batch + (tokens + g.qs - 1) / g.qs);
   L.part_cap = L.seg_cap + waves;
+  // small steps: room for the fixed partial slots too
+  if (small_geometry(g, dv, batch, L.seg_cap) && L.part_cap < kFixParts * L.seg_cap)
+    L.part_cap = kFixParts * L.seg_cap;
   int64_t off = 0;
   L.hdr = off;      off = align256(off + 64 * 4);
   L.seg = off;      off = align256(off + (L.seg_cap + 1) * 8 * 4);
@@ -309,6 +332,7 @@ constexpr int kPlanRegChunks = 2;        // segments kept in registers: 2 x 512
 #endif
 constexpr int kPadBelow = AIA_PAD_BELOW;  // pad segments when ranges are shorter (tiles)
 
+
 // Padded MLA plans: a request's tiles are split over its ranges evenly
 // (sizes floor / ceil of nt / k, never crossing requests) and the ranges are
 // dealt to work-group slots by size in a snake order over the CUs' slots
@@ -326,7 +350,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     int32_t* __restrict__ req_scratch,
     int32_t* __restrict__ mrg, int4* __restrict__ pf_units, int4* __restrict__ pf_mrg,
     int4* __restrict__ pf_wg, int32_t pf_cap, int32_t pf_unit_cap, int32_t pf_mrg_cap,
-    int32_t seg_cap) {
+    int32_t seg_cap, int32_t fix_cap) {
   __shared__ __attribute__((aligned(16))) int lds[kPlanLds];
   __shared__ int wave_sums[kPlanThreads / 64];
   __shared__ int2 wave_sums2[kPlanThreads / 64];
@@ -687,6 +711,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   int4* srec = reinterpret_cast<int4*>(lds + srec0);
   carry = 0;
   int mcarry = 0;
+  bool fixed = false;
   for (int base = 0, c = 0; base < nseg; base += kPlanThreads, ++c) {
     const int s = base + tid;
     int np = 0;
@@ -723,17 +748,21 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
         mcnt = nwv * nsl;
       }
     }
+    // fixed partial slots (see kFixParts), decided as the small planner does
+    fixed = nseg <= kSmallPlanSegs && nseg * kFixParts <= fix_cap &&
+            !__syncthreads_or(np > kFixParts);
     int2 tot2;
     const int2 ex2 = block_exclusive_scan2(make_int2(np, mcnt), wave_sums2, &tot2);
     const int ex = ex2.x, tot = tot2.x, mex = ex2.y, mtot = tot2.y;
-    if (s < nseg) seg[(int64_t)s * 8 + 7] = carry + ex;
+    const int pbase = fixed ? kFixParts * s : carry + ex;   // the segment's first partial slot
+    if (s < nseg) seg[(int64_t)s * 8 + 7] = pbase;
     if (bal && s < nseg) lds[pb0 + s] = carry + ex;
     if (rec_lds && s < nseg) {
 #pragma unroll
       for (int i = 0; i < kPlanRegChunks; ++i)
         if (i == c) {
           srec[2 * s] = my_head[i];
-          srec[2 * s + 1] = make_int4(my_lim[i], my_tb[i], my_tb[i] + my_nt[i], carry + ex);
+          srec[2 * s + 1] = make_int4(my_lim[i], my_tb[i], my_tb[i] + my_nt[i], pbase);
         }
     }
     if (mcnt > 0) {
@@ -744,21 +773,22 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
           // {first query token, query tokens, kv head, head block; first
           // partial row, parts, slice, rows}, as two 16-byte stores
           m[0] = make_int4(r0[2], r0[3] & 0xff, (r0[1] & 0xffff) * g.nw + w, (r0[1] >> 16) & 0x3fff);
-          m[1] = make_int4(((carry + ex) * g.nw + w) * seg_rows, np, sl, rows);
+          m[1] = make_int4((pbase * g.nw + w) * seg_rows, np, sl, rows);
         }
     }
     mcarry += mtot;
     carry += tot;
   }
   if (tid == 0) {
-    hdr[0] = nseg; hdr[1] = total_tiles; hdr[2] = tpw; hdr[3] = carry; hdr[4] = waves;
-    hdr[5] = mcarry; hdr[6] = units; hdr[7] = pmerges;
+    hdr[0] = nseg; hdr[1] = total_tiles; hdr[2] = tpw; hdr[3] = fixed ? kFixParts * nseg : carry;
+    hdr[4] = waves; hdr[5] = mcarry; hdr[6] = units; hdr[7] = pmerges;
     hdr[8] = overflow ? -1 : 0;   // status: -1 = the metadata asked for more work than fits
     hdr[9] = overflow ? 0 : dealt;
+    hdr[10] = fixed ? 1 : 0;
     // sentinel record so readers may look one past the end
     int* r = seg + (int64_t)nseg * 8;
     r[0] = 0; r[1] = 0; r[2] = 0; r[3] = 0; r[4] = 0;
-    r[5] = total_tiles; r[6] = total_tiles; r[7] = carry;
+    r[5] = total_tiles; r[6] = total_tiles; r[7] = fixed ? kFixParts * nseg : carry;
   }
   __syncthreads();
 
@@ -890,7 +920,6 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
 // for the range records.  The plan is the one plan_kernel makes for the
 // same step, record for record (tests compare the two workspaces).
 constexpr int kSmallPlanThreads = 256;
-constexpr int kSmallPlanSegs = 64;
 
 __device__ __forceinline__ int wave_total(int x) {   // sum over the 64 lanes, in every lane
   return __builtin_amdgcn_readlane(wave_incl_scan(x), 63);
@@ -901,7 +930,7 @@ __global__ __launch_bounds__(kSmallPlanThreads) void plan_small_kernel(
     const int32_t* __restrict__ block_table, int64_t bt_stride, int32_t block_size,
     int32_t batch, Geometry g, int32_t waves, int32_t dv,
     int32_t* __restrict__ hdr, int32_t* __restrict__ seg, int32_t* __restrict__ wave_rec,
-    int32_t* __restrict__ mrg, int32_t seg_cap) {
+    int32_t* __restrict__ mrg, int32_t seg_cap, int32_t fix_cap) {
   __shared__ int4 srec[kSmallPlanSegs + 1][2];   // segment records (+ sentinel)
   __shared__ int sinfo[4];                        // nseg, total tiles, tpw
   const int tid = threadIdx.x, lane = tid & 63;
@@ -985,8 +1014,10 @@ __global__ __launch_bounds__(kSmallPlanThreads) void plan_small_kernel(
       }
     }
     const int pinc = wave_incl_scan(np), minc = wave_incl_scan(mcnt);
-    const int part_base = pinc - np, mbase = minc - mcnt;
-    const int nparts = __builtin_amdgcn_readlane(pinc, 63);
+    // fixed partial slots (see kFixParts)
+    const bool fixed = nseg * kFixParts <= fix_cap && !__any(np > kFixParts);
+    const int part_base = fixed ? kFixParts * s : pinc - np, mbase = minc - mcnt;
+    const int nparts = fixed ? kFixParts * nseg : __builtin_amdgcn_readlane(pinc, 63);
     const int nmrg = __builtin_amdgcn_readlane(minc, 63);
     if (s < nseg) {
       const int4 r0 = make_int4(rec0, rec1, rec2, rec3);
@@ -1007,6 +1038,7 @@ __global__ __launch_bounds__(kSmallPlanThreads) void plan_small_kernel(
       hdr[5] = nmrg; hdr[6] = 0; hdr[7] = 0;
       hdr[8] = overflow ? -1 : 0;
       hdr[9] = 0;
+      hdr[10] = fixed ? 1 : 0;
       int4* r = reinterpret_cast<int4*>(seg + (int64_t)nseg * 8);   // sentinel
       r[0] = make_int4(0, 0, 0, 0);
       r[1] = make_int4(0, total_tiles, total_tiles, nparts);
@@ -2065,6 +2097,11 @@ struct MergeArgs {
   const uint16_t* pf_o;
   const float2* pf_ml;
   int32_t tokens;           // output rows (query tokens); heads = group x hkv
+  // fixed-slot merges (kFixParts): 1 when the launch has one work-group per
+  // (segment, kv head) and the kernel a fixed-slot path, and the partial
+  // slots the buffer holds
+  int32_t fixed_slots;
+  int64_t part_cap;
 };
 
 // Merge of split partials.  The planner lists the merge work: one record per
@@ -2085,8 +2122,11 @@ struct MergeArgs {
 #ifndef AIA_MERGE_WIDE
 #define AIA_MERGE_WIDE 1
 #endif
-template <int kMergeGroups>
-
+// FIXL: partial loads per thread of the fixed-slot path (0: none; see
+// kFixParts), a compile-time count so that the loads are issued
+// unconditionally and the compiler's counter waits for the header words
+// leave them in flight.
+template <int kMergeGroups, int FIXL>
 __global__ __launch_bounds__(64 * kMergeGroups) void merge_kernel(MergeArgs a) {
   constexpr int kMergeThreads = 64 * kMergeGroups;
   __shared__ float4 sacc[kMergeGroups - 1][kMergeDims / 4][64];
@@ -2103,24 +2143,163 @@ __global__ __launch_bounds__(64 * kMergeGroups) void merge_kernel(MergeArgs a) {
   const int pf_tpr = a.dv / 8, pf_rpp = kMergeThreads / pf_tpr;
   const int kSlices = kPfRows / pf_rpp;
   const int per_rec = a.hkv * kSlices;
-  // The header words, this work-group's first merge record and its first
-  // prefill record are loaded in straight-line code before any branch, so
-  // they go out together (one round trip, then one for the partials);
-  // behind a branch the compiler issued them one after another.  An index
-  // past a list reads the header instead, and its value is not used.
+  // Every load the work-group's first step needs goes out before any of
+  // them is waited for: the header words, its first merge record, its first
+  // prefill record and, for fixed-slot plans (kFixParts), its segment record
+  // and partials.  They are vector loads (indexed by an opaque zero), so the
+  // in-order vector counter lets the header be waited for while the
+  // partials are still in flight; as scalar loads they would share the
+  // kernel arguments' counter, and the compiler's waits for those would
+  // drain them.  An index past a list reads the header instead, and its
+  // value is not used.
+  int vz;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(vz));
   const int64_t item0 = blockIdx.x;
-  const int4* mp = item0 < a.mrg_cap ? reinterpret_cast<const int4*>(a.mrg + item0 * kMrgInts)
-                                     : reinterpret_cast<const int4*>(a.hdr);
-  const int4* pp0 = a.pf_mrg && item0 < a.pf_items_cap ? a.pf_mrg + (int)blockIdx.x / per_rec
-                                                         : reinterpret_cast<const int4*>(a.hdr);
-  const int4 m0_first = mp[0], m1_first = mp[1];
-  const int4 pr0 = pp0[0];
-  const int nmrg = a.hdr[5], npm_hdr = a.hdr[7];
-  const int status = a.hdr[8];             // planner status, used at the end
+  const int4* mp = (item0 < a.mrg_cap ? reinterpret_cast<const int4*>(a.mrg + item0 * kMrgInts)
+                                      : reinterpret_cast<const int4*>(a.hdr)) + vz;
+  const int4* pp0 = (a.pf_mrg && item0 < a.pf_items_cap ? a.pf_mrg + (int)blockIdx.x / per_rec
+                                                          : reinterpret_cast<const int4*>(a.hdr)) + vz;
+  const int* hv = a.hdr + vz;
+  const int4 m0_v = mp[0], m1_v = mp[1];
+  const int4 pr_v = pp0[0];
+  const int h0 = hv[0], h2 = hv[2], h5 = hv[5], h7 = hv[7], h8 = hv[8], h10 = hv[10];
+  auto fold_into = [](float& mx, float& ls, float4 (&acc)[kMergeDims / 4], float2 ml,
+                      const float4 (&x)[kMergeDims / 4]) {
+    const float mn = fmaxf(mx, ml.x);
+    const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
+    ls = ls * sa + ml.y * sb;
+#pragma unroll
+    for (int i = 0; i < kMergeDims / 4; ++i) {
+      acc[i].x = acc[i].x * sa + x[i].x * sb; acc[i].y = acc[i].y * sa + x[i].y * sb;
+      acc[i].z = acc[i].z * sa + x[i].z * sb; acc[i].w = acc[i].w * sa + x[i].w * sb;
+    }
+    mx = mn;
+  };
+  auto unpack16 = [](uint4 h0, uint4 h1, float4 (&x)[kMergeDims / 4]) {
+    const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+    for (int i = 0; i < kMergeDims / 4; ++i) {
+      const half2_t a2 = __builtin_bit_cast(half2_t, hw[2 * i]);
+      const half2_t b2 = __builtin_bit_cast(half2_t, hw[2 * i + 1]);
+      x[i] = make_float4((float)a2[0], (float)a2[1], (float)b2[0], (float)b2[1]);
+    }
+  };
+  // Fixed partial slots (kFixParts): work-group b merges (segment b / nw,
+  // kv head b % nw), whose row span holds at most 16 elements (rows x dv /
+  // 16: a decode segment's few rows).  Thread (wave kg, lane) takes element
+  // lane % 16 and the slots q + 4 G r (q = 4 kg + lane / 16, G waves, r <
+  // FIXL); a wave's four slot groups fold with two shuffles, the waves
+  // through LDS.  Slots past a segment's parts hold stale values that are
+  // not used.
+  static_assert(FIXL == 0 || FIXL * 4 * kMergeGroups == kFixParts, "one load per slot");
+  const int fb = blockIdx.x;
+  const int fs = fb / a.nw, fw = fb - fs * a.nw;
+  const int q = 4 * kg + (lane >> 4);
+  int4 r0_v = make_int4(0, 0, 0, 0), r1_v = r0_v;
+  float2 fml[FIXL > 0 ? FIXL : 1];
+  uint4 fh0[FIXL > 0 ? FIXL : 1], fh1[FIXL > 0 ? FIXL : 1];
+  if (FIXL > 0) {
+    const int4* sr = reinterpret_cast<const int4*>(a.seg) + 2 * (int64_t)fs + vz;
+    r0_v = sr[0];
+    r1_v = sr[1];
+    const int e = lane & 15;
+    const int n = min(e / epr, seg_rows - 1);
+    const int c = (e - (e / epr) * epr) * kMergeDims;
+#pragma unroll
+    for (int r = 0; r < FIXL; ++r) {
+      const int64_t slot = (int64_t)kFixParts * fs + q + 4 * kMergeGroups * r;
+      const int64_t prow = slot < a.part_cap ? (slot * a.nw + fw) * seg_rows + n : 0;
+      fml[r] = a.part_ml[prow];
+      const uint4* src = reinterpret_cast<const uint4*>(a.part_o + prow * a.dv + c);
+      fh0[r] = src[0];
+      fh1[r] = src[1];
+    }
+  }
+  const int nmrg = __builtin_amdgcn_readfirstlane(h5);
+  const int npm_hdr = __builtin_amdgcn_readfirstlane(h7);
+  const int status = __builtin_amdgcn_readfirstlane(h8);   // planner status, used at the end
   const int npm = a.pf_mrg ? npm_hdr : 0;
+  const int fixed_plan = FIXL > 0 ? __builtin_amdgcn_readfirstlane(h10) : 0;
+  const int4 pr0 = make_int4(__builtin_amdgcn_readfirstlane(pr_v.x), __builtin_amdgcn_readfirstlane(pr_v.y),
+                             __builtin_amdgcn_readfirstlane(pr_v.z), __builtin_amdgcn_readfirstlane(pr_v.w));
+  const int4 m0_first = make_int4(__builtin_amdgcn_readfirstlane(m0_v.x), __builtin_amdgcn_readfirstlane(m0_v.y),
+                                  __builtin_amdgcn_readfirstlane(m0_v.z), __builtin_amdgcn_readfirstlane(m0_v.w));
+  const int4 m1_first = make_int4(__builtin_amdgcn_readfirstlane(m1_v.x), __builtin_amdgcn_readfirstlane(m1_v.y),
+                                  __builtin_amdgcn_readfirstlane(m1_v.z), __builtin_amdgcn_readfirstlane(m1_v.w));
+  if (FIXL > 0) {
+    const int4 r0 = make_int4(__builtin_amdgcn_readfirstlane(r0_v.x), __builtin_amdgcn_readfirstlane(r0_v.y),
+                              __builtin_amdgcn_readfirstlane(r0_v.z), __builtin_amdgcn_readfirstlane(r0_v.w));
+    const int4 r1 = make_int4(__builtin_amdgcn_readfirstlane(r1_v.x), __builtin_amdgcn_readfirstlane(r1_v.y),
+                              __builtin_amdgcn_readfirstlane(r1_v.z), __builtin_amdgcn_readfirstlane(r1_v.w));
+    const int nseg = __builtin_amdgcn_readfirstlane(h0);
+    const int tpw = max(1, __builtin_amdgcn_readfirstlane(h2));
+    const int np = (r1.z - 1) / tpw - r1.y / tpw + 1;
+    const int kvg = r0.y & 0xffff, hbi = (r0.y >> 16) & 0x3fff;
+    const int nq = r0.w & 0xff;
+    const int nblk = (nq + qb - 1) / qb;
+    const int rows = (nblk - 1) * kRows + min(kRows, (nq - (nblk - 1) * qb) * a.hb);
+    const bool use = fixed_plan == 1 && fs < nseg && np > 1 && fw < min(a.nw, a.hkv - kvg * a.nw);
+    const int e = lane & 15;
+    const int n = e / epr;
+    const int c = (e - n * epr) * kMergeDims;
+    const int rblk = n / kRows, t = (n - rblk * kRows) / a.hb;
+    const int hh = n - rblk * kRows - t * a.hb;
+    const bool live = use && e < rows * epr && t < qb && rblk * qb + t < nq &&
+                      hbi * a.hb + hh < a.group;
+    float4 acc[kMergeDims / 4];
+#pragma unroll
+    for (int i = 0; i < kMergeDims / 4; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    float mx = -1e30f, ls = 0.f;
+#pragma unroll
+    for (int r = 0; r < FIXL; ++r) {
+      if (live && q + 4 * kMergeGroups * r < np) {
+        float4 x[kMergeDims / 4];
+        unpack16(fh0[r], fh1[r], x);
+        fold_into(mx, ls, acc, fml[r], x);
+      }
+    }
+    // the wave's four slot groups of an element sit in lanes 16 apart
+    for (int d = 16; d < 64; d <<= 1) {
+      const float2 oml = make_float2(__shfl_xor(mx, d), __shfl_xor(ls, d));
+      float4 ox[kMergeDims / 4];
+#pragma unroll
+      for (int i = 0; i < kMergeDims / 4; ++i)
+        ox[i] = make_float4(__shfl_xor(acc[i].x, d), __shfl_xor(acc[i].y, d),
+                            __shfl_xor(acc[i].z, d), __shfl_xor(acc[i].w, d));
+      fold_into(mx, ls, acc, oml, ox);
+    }
+    // and the waves' results through LDS
+    if (kg > 0 && lane < 16) {
+#pragma unroll
+      for (int i = 0; i < kMergeDims / 4; ++i) sacc[kg - 1][i][lane] = acc[i];
+      sml[kg - 1][lane] = make_float2(mx, ls);
+    }
+    __syncthreads();
+    if (kg == 0 && lane < 16 && live) {
+#pragma unroll
+      for (int j = 0; j < kMergeGroups - 1; ++j) {
+        float4 x[kMergeDims / 4];
+#pragma unroll
+        for (int i = 0; i < kMergeDims / 4; ++i) x[i] = sacc[j][i][lane];
+        fold_into(mx, ls, acc, sml[j][lane], x);
+      }
+      const float inv = ls > 0.f ? 1.f / ls : 0.f;
+      const int qi = rblk * qb + t;
+      const int head = (kvg * a.nw + fw) * a.group + hbi * a.hb + hh;
+      uint16_t* op = a.out + (int64_t)(r0.z + qi) * a.o_ts + (int64_t)head * a.o_hs + c;
+#pragma unroll
+      for (int i = 0; i < kMergeDims / 4; ++i) {
+        uint2 wv;
+        wv.x = aia::pack_bf16x2(acc[i].x * inv, acc[i].y * inv);
+        wv.y = aia::pack_bf16x2(acc[i].z * inv, acc[i].w * inv);
+        *reinterpret_cast<uint2*>(op + 4 * i) = wv;
+      }
+    }
+  }
   // the first test reads the first record too (a record has at least two
   // parts), which keeps its loads ahead of the first branch
-  const bool first_live = (item0 < a.mrg_cap) & (item0 < nmrg) & (m1_first.y >= 2);
+  const bool first_live = (fixed_plan != 1) & (item0 < a.mrg_cap) & (item0 < nmrg) &
+                          (m1_first.y >= 2);
   for (int64_t item = item0; first_live && item < a.mrg_cap; item += gridDim.x) {
     if (item >= nmrg) break;                               // uniform over the group
     const int4 m0 = item == item0 ? m0_first : *reinterpret_cast<const int4*>(a.mrg + item * kMrgInts);
@@ -2937,8 +3116,32 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
   const int64_t items = L.mrg_cap > pitems ? L.mrg_cap : pitems;
   int64_t mgrid = items < 2048 ? items : 2048;
   if (mgrid < 1) mgrid = 1;
-  if (wide) merge_kernel<8><<<(unsigned)mgrid, threads, 0, s>>>(mg);
-  else merge_kernel<4><<<(unsigned)mgrid, threads, 0, s>>>(mg);
+  // Fixed-slot merges for small steps (kFixParts): one work-group per
+  // (segment, kv head) when a segment's row span holds at most 16 elements
+  // (rows x dv / 16, rows bounded by the query tokens a request can hold),
+  // each thread loading kFixParts / (4 waves) slots.  (configs[3]'s verify
+  // segments, 64-128 elements, keep the records: in passes of 16 elements
+  // the call went 40.6 -> 54 us, and with one wave per 16 elements and 8 slot
+  // loads per thread 40.6 -> 42 us, config 1 then 21.9 -> 22.75.)
+  mg.fixed_slots = 0;
+  mg.part_cap = L.part_cap;
+  if (small_geometry(g, dv, batch, L.seg_cap) && L.part_cap >= kFixParts * L.seg_cap) {
+    const int64_t nq_max = std::min<int64_t>(g.qs, (int64_t)tokens - batch + 1);
+    const int64_t rows_max = std::min<int64_t>(
+        (int64_t)kRows * g.rb, nq_max <= g.qb ? nq_max * g.hb : (int64_t)kRows * ((nq_max + g.qb - 1) / g.qb));
+    if (nq_max >= 1 && rows_max * (dv / kMergeDims) <= 16) {
+      mg.fixed_slots = 1;
+      mgrid = L.seg_cap * nw;
+    }
+  }
+  const int fl = mg.fixed_slots ? kFixParts / (4 * (threads / 64)) : 0;   // slot loads per thread
+  if (wide) {
+    if (fl == 1) merge_kernel<8, 1><<<(unsigned)mgrid, threads, 0, s>>>(mg);
+    else merge_kernel<8, 0><<<(unsigned)mgrid, threads, 0, s>>>(mg);
+  } else {
+    if (fl == 2) merge_kernel<4, 2><<<(unsigned)mgrid, threads, 0, s>>>(mg);
+    else merge_kernel<4, 0><<<(unsigned)mgrid, threads, 0, s>>>(mg);
+  }
   return aia::check_hip(hipGetLastError(), "merge_kernel launch");
 }
 
@@ -2950,8 +3153,7 @@ bool small_plan(const Geometry& g, int32_t dv, int32_t batch, const Layout& L) {
     const char* e = getenv("AIA_PLANNER");
     return e && strcmp(e, "large") == 0;
   }();
-  return !force_large && dv != 512 && !g.pf && batch >= 1 && batch <= 64 &&
-         L.seg_cap <= kSmallPlanSegs && L.pf_cap == 0;
+  return !force_large && small_geometry(g, dv, batch, L.seg_cap);
 }
 
 // The attention launches of one call, for one cache layout.
@@ -3067,7 +3269,7 @@ extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens
         cu_seqlens_q, seqlens_kv, block_table, block_table_stride, block_size, batch, g, waves,
         head_dim_v, reinterpret_cast<int32_t*>(ws + L.hdr),
         reinterpret_cast<int32_t*>(ws + L.seg), reinterpret_cast<int32_t*>(ws + L.wave),
-        reinterpret_cast<int32_t*>(ws + L.mrg), (int32_t)L.seg_cap);
+        reinterpret_cast<int32_t*>(ws + L.mrg), (int32_t)L.seg_cap, (int32_t)L.part_cap);
     return check_hip(hipGetLastError(), "aia_attn_plan launch");
   }
   plan_kernel<<<1, kPlanThreads, 0, (hipStream_t)stream>>>(
@@ -3078,7 +3280,8 @@ extern "C" int aia_attn_plan(const int32_t* cu_seqlens_q, const int32_t* seqlens
       reinterpret_cast<int32_t*>(ws + L.mrg), reinterpret_cast<int4*>(ws + L.pf),
       reinterpret_cast<int4*>(ws + L.pfm), reinterpret_cast<int4*>(ws + L.pfw),
       (int32_t)L.pf_cap, (int32_t)L.pf_unit_cap,
-      (int32_t)L.pf_mrg_cap, (int32_t)L.seg_cap);
+      (int32_t)L.pf_mrg_cap, (int32_t)L.seg_cap,
+      small_geometry(g, head_dim_v, batch, L.seg_cap) ? (int32_t)L.part_cap : 0);
   return check_hip(hipGetLastError(), "aia_attn_plan launch");
 }
 

@@ -59,7 +59,7 @@ def plans():
         ws = plan.workspace.cpu().view(torch.int32).numpy()
         hdr = ws[:16].copy()
         nseg, nmrg = int(hdr[0]), int(hdr[5])
-        out[name + ".hdr"] = hdr[:10]
+        out[name + ".hdr"] = hdr[:11]
         out[name + ".seg"] = ws[L["seg"] // 4: L["seg"] // 4 + (nseg + 1) * 8].copy()
         rec = ws[L["wave"] // 4: L["wave"] // 4 + L["waves"] * 32].copy().reshape(-1, 32)
         rec[rec[:, 0] < 0, 4:] = 0        # an unused slot's record is its first 4 ints
@@ -83,3 +83,36 @@ def test_small_planner_matches_the_work_group_planner(tmp_path):
         for part in ("hdr", "seg", "rec", "mrg"):
             a, b = small[f"{name}.{part}"], large[f"{name}.{part}"]
             assert a.shape == b.shape and np.array_equal(a, b), (name, part)
+
+
+@pytest.mark.parametrize("waves, fixed", [(0, 1), (7, 1), (2048, 0)])
+def test_fixed_partial_slots(waves, fixed):
+    """Small steps whose segments have at most 32 ranges each put segment s's
+    partials at slots 32 s .. 32 s + 31 (header word 10 = 1), so the merge
+    finds them without a record; more ranges per segment fall back to the
+    packed slots and the merge records.  The output matches the oracle either
+    way."""
+    from oracle.paged_attn import paged_attention
+    s = workloads.config1_decode(seed=5)
+    plan = ops.AttentionPlan.from_lists(s.block_table.to(DEV), s.cu_seqlens_q, s.seqlens_kv,
+                                        16, 8, 128, 128, num_waves=waves)
+    out = ops.paged_attention_gqa(s.q.to(DEV), s.k_cache.to(DEV), s.v_cache.to(DEV), plan, s.scale)
+    torch.cuda.synchronize()
+    L = ops.workspace_layout(len(s.seqlens_kv), s.num_tokens, 16, 8, 128, waves)
+    ws = plan.workspace.cpu().view(torch.int32).numpy()
+    hdr = ws[:16]
+    nseg, tpw = int(hdr[0]), int(hdr[2])
+    seg = ws[L["seg"] // 4: L["seg"] // 4 + nseg * 8].reshape(nseg, 8)
+    nparts = (seg[:, 6] - 1) // tpw - seg[:, 5] // tpw + 1
+    print(f"waves {waves}: header {hdr[:11].tolist()}, ranges per segment {nparts.tolist()}",
+          flush=True)
+    assert int(hdr[10]) == fixed
+    assert (int(nparts.max()) <= 32) == bool(fixed)
+    if fixed:
+        assert np.array_equal(seg[:, 7], 32 * np.arange(nseg))
+    else:
+        assert np.array_equal(seg[:, 7], np.concatenate([[0], np.cumsum(nparts)[:-1]]))
+    ref = paged_attention(s.q, s.k_cache, s.v_cache, s.block_table, s.cu_seqlens_q,
+                          s.seqlens_kv, s.scale)
+    err = (out.float().cpu() - ref).abs().max().item()
+    assert err <= 2e-2, err

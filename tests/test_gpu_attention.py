@@ -494,3 +494,28 @@ def test_gqa_plan_ranges_spread_over_the_xcds(seed):
     assert max(counts) - min(counts) <= 1
     for x, v in starts.items():
         assert v == list(range(v[0], v[0] + len(v)))
+
+
+@pytest.mark.parametrize("hq,hkv", [(24, 12), (9, 3), (40, 2), (64, 8)])
+@pytest.mark.parametrize("waves", [0, 64, 7])
+def test_fixed_slot_merge_decode_steps(hq, hkv, waves):
+    """Decode steps small enough for fixed partial slots (header word 10):
+    a last kv-head group with fewer waves than the first (12 = 8 + 4 kv
+    heads), groups of 3, 20 and 8 query heads, and range counts from 7 to
+    the default.  The output is pre-filled with a sentinel, so a row the
+    merge misses or a stray write shows."""
+    lks = [700, 90, 1500, 33, 1, 2048, 17]
+    step = workloads.make_gqa_step(lqs=[1] * len(lks), lks=lks, num_q_heads=hq,
+                                   num_kv_heads=hkv, block_size=16, seed=hq + hkv + waves)
+    s = step
+    plan = ops.AttentionPlan.from_lists(s.block_table.to(DEV), s.cu_seqlens_q, s.seqlens_kv,
+                                        hq, hkv, 128, 16, num_waves=waves)
+    out = torch.full(s.q.shape, 7.0, dtype=torch.bfloat16, device=DEV)
+    ops.paged_attention_gqa(s.q.to(DEV), s.k_cache.to(DEV), s.v_cache.to(DEV), plan, s.scale,
+                            out=out)
+    torch.cuda.synchronize()
+    hdr = plan.workspace[:64].cpu().view(torch.int32)
+    err = (out.float().cpu() - oracle(step)).abs().max().item()
+    print(f"hq {hq} hkv {hkv} waves {waves}: header {hdr[:11].tolist()}, max-abs err {err:.3e}",
+          flush=True)
+    assert err <= TOL, err

@@ -75,6 +75,50 @@ def test_random_steps_match_the_oracle(seed):
     assert err <= TOL
 
 
+def draw_small_decode(seed):
+    r = random.Random(seed)
+    hq, hkv = r.choice(HEADS + [(16, 8), (16, 8), (24, 12), (8, 4)])
+    bs = r.choice(BLOCKS)
+    B = r.randint(1, 24)
+    lqs = [1 if r.random() < 0.7 else r.randint(2, 3) for _ in range(B)]
+    lks = [lq + r.randint(0, 2500) for lq in lqs]
+    waves = r.choice([0, 0, 5, 32, 128, 256, 1000])
+    return dict(hq=hq, hkv=hkv, bs=bs, lqs=lqs, lks=lks, waves=waves, fused=r.random() < 0.5)
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_random_small_decode_steps_match_the_oracle(seed):
+    """Decode and short-verify steps of at most 24 requests: the small-step
+    planner, its fixed partial slots (header word 10) where every segment has
+    at most 32 ranges, and the fixed-slot or record-driven merge."""
+    c = draw_small_decode(5000 + seed)
+    step = workloads.make_gqa_step(lqs=c["lqs"], lks=c["lks"], num_q_heads=c["hq"],
+                                   num_kv_heads=c["hkv"], block_size=c["bs"], seed=seed,
+                                   extra_blocks=3)
+    kc, vc = step.k_cache.to(DEV), step.v_cache.to(DEV)
+    plan = ops.AttentionPlan.from_lists(step.block_table.to(DEV), step.cu_seqlens_q,
+                                        step.seqlens_kv, c["hq"], c["hkv"], 128, c["bs"],
+                                        num_waves=c["waves"])
+    ek, ev = step.k_cache, step.v_cache
+    if c["fused"]:
+        ek, ev = ek.clone(), ev.clone()
+        kv_write(step.k_new, step.v_new, ek, ev, step.slot_mapping)
+        out = ops.paged_attention_gqa(step.q.to(DEV), kc, vc, plan, step.scale,
+                                      key_new=step.k_new.to(DEV), value_new=step.v_new.to(DEV))
+    else:
+        out = ops.paged_attention_gqa(step.q.to(DEV), kc, vc, plan, step.scale)
+    torch.cuda.synchronize()
+    fixed = int(plan.workspace[:64].cpu().view(torch.int32)[10])
+    print(f"case {seed}: {c}, fixed slots {fixed}", flush=True)
+    if c["fused"]:
+        assert torch.equal(kc.cpu(), ek) and torch.equal(vc.cpu(), ev)
+    exp = paged_attention(step.q, ek, ev, step.block_table, step.cu_seqlens_q, step.seqlens_kv,
+                          step.scale)
+    err = (out.float().cpu() - exp).abs().max().item()
+    print(f"max-abs err {err:.3e}", flush=True)
+    assert err <= TOL
+
+
 def draw_mla(seed):
     r = random.Random(seed)
     bs = r.choice(BLOCKS)

@@ -342,6 +342,28 @@ constexpr int kPadBelow = AIA_PAD_BELOW;  // pad segments when ranges are shorte
 #define AIA_MLA_BALANCE 1
 #endif
 
+// Range placement over the segments' first tiles held in LDS (tb[0..nseg]):
+// the last segment with first tile <= t0, and from it (galloping, then a
+// bracket search) the last segment with first tile < t1.
+__device__ __forceinline__ int range_first_seg(const int* tb, int nseg, int t0) {
+  int lo = 0, hi = nseg - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (tb[mid] <= t0) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+__device__ __forceinline__ int range_last_seg(const int* tb, int nseg, int lo, int t1) {
+  int lo2 = lo, step = 1;
+  while (lo2 + step < nseg && tb[lo2 + step] < t1) { lo2 += step; step <<= 1; }
+  int hi2 = min(nseg - 1, lo2 + step - 1);
+  while (lo2 < hi2) {
+    const int mid = (lo2 + hi2 + 1) >> 1;
+    if (tb[mid] < t1) lo2 = mid; else hi2 = mid - 1;
+  }
+  return lo2;
+}
+
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ kvlen,
     const int32_t* __restrict__ block_table, int64_t bt_stride, int32_t block_size,
@@ -709,6 +731,37 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   const int srec0 = (pb0 + 3) & ~3;
   const bool rec_lds = tb_lds && !bal && srec0 + 8 * nseg <= kPlanLds;
   int4* srec = reinterpret_cast<int4*>(lds + srec0);
+  // GQA plans: each thread's first range is placed now, before phase 3, and
+  // its block ids are loaded, so that load is in flight during phase 3's
+  // scans and merge records instead of opening phase 4 (the partial base of
+  // the LDS segment records follows in phase 3).
+  const int nr_used_early = min(waves, (total_tiles + tpw - 1) / tpw);
+  const bool early = rec_lds && tid < nr_used_early;
+  int e_lo = 0, e_lo2 = 0, e_blk = 0;
+  int e_bv[kRecBlocks];
+  if (rec_lds) {
+#pragma unroll
+    for (int i = 0; i < kPlanRegChunks; ++i) {
+      const int s = i * kPlanThreads + tid;
+      if (s < nseg) {
+        srec[2 * s] = my_head[i];
+        srec[2 * s + 1] = make_int4(my_lim[i], my_tb[i], my_tb[i] + my_nt[i], 0);
+      }
+    }
+    __syncthreads();   // first tiles and segment records
+    if (early) {
+      const int t0 = tid * tpw;
+      const int t1 = min(total_tiles, t0 + tpw);
+      e_lo = range_first_seg(lds, nseg, t0);
+      e_lo2 = range_last_seg(lds, nseg, e_lo, t1);
+      const int4 r0 = srec[2 * e_lo], r1 = srec[2 * e_lo + 1];
+      const int nblk_vis = (max(0, r1.x + (r0.w & 0xff)) + block_size - 1) / block_size;
+      e_blk = ((t0 - r1.y) * kTile) / block_size;
+      const int32_t* btrow = block_table + (int64_t)r0.x * bt_stride;
+#pragma unroll
+      for (int i = 0; i < kRecBlocks; ++i) e_bv[i] = e_blk + i < nblk_vis ? btrow[e_blk + i] : 0;
+    }
+  }
   carry = 0;
   int mcarry = 0;
   bool fixed = false;
@@ -757,14 +810,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int pbase = fixed ? kFixParts * s : carry + ex;   // the segment's first partial slot
     if (s < nseg) seg[(int64_t)s * 8 + 7] = pbase;
     if (bal && s < nseg) lds[pb0 + s] = carry + ex;
-    if (rec_lds && s < nseg) {
-#pragma unroll
-      for (int i = 0; i < kPlanRegChunks; ++i)
-        if (i == c) {
-          srec[2 * s] = my_head[i];
-          srec[2 * s + 1] = make_int4(my_lim[i], my_tb[i], my_tb[i] + my_nt[i], pbase);
-        }
-    }
+    if (rec_lds && s < nseg) lds[srec0 + 8 * s + 7] = pbase;   // srec[2 s + 1].w
     if (mcnt > 0) {
       const int seg_rows = kRows * g.rb;
       int4* m = reinterpret_cast<int4*>(mrg + (int64_t)(mcarry + mex) * kMrgInts);
@@ -886,6 +932,17 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   for (int r = tid; r < nr_used; r += kPlanThreads) {
     const int t0 = r * tpw;
     const int t1 = min(total_tiles, t0 + tpw);
+    if (early && r == tid) {      // placed before phase 3, block ids loaded then
+      int4* o4 = reinterpret_cast<int4*>(wave_rec + (int64_t)slot_of(r) * kRecInts);
+      o4[0] = make_int4(e_lo, t0, t1, tpw);
+      o4[1] = srec[2 * e_lo];
+      o4[2] = srec[2 * e_lo + 1];
+      o4[3] = make_int4(e_blk, e_lo2, 0, 0);
+#pragma unroll
+      for (int i = 0; i < kRecBlocks / 4; ++i)
+        o4[4 + i] = make_int4(e_bv[4 * i], e_bv[4 * i + 1], e_bv[4 * i + 2], e_bv[4 * i + 3]);
+      continue;
+    }
     int lo = 0, hi = nseg - 1;  // last s with tile_begin <= t0
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;

@@ -63,6 +63,9 @@ class DeviceRequestTable:
         self._free = list(range(max_slots - 1, -1, -1))
         self._step = 0
         self._cap_blocks, self._cap_tokens = max_blocks, max_len
+        # (token row width, token pool address, block row width, block pool
+        # address) for the pack launch, refreshed when the pools grow
+        self.pool_args = None
         self.uploaded_block_rows = 0
         self.uploaded_block_elements = 0
 
@@ -84,6 +87,7 @@ class DeviceRequestTable:
         if s1 > s0:
             self._free = list(range(s1 - 1, s0 - 1, -1)) + self._free
         self._cap_blocks, self._cap_tokens = b1, t1
+        self.pool_args = None
 
     def release(self, rid):
         slot = self._slot.pop(rid, None)
@@ -315,14 +319,17 @@ def _launch(table, uploader, upd, *, block_size, bt_width, token_ids, positions,
         o = out_ptrs or (token_ids.data_ptr(), positions.data_ptr(), slot_mapping.data_ptr(),
                          block_table.data_ptr(), cu.data_ptr(), kv.data_ptr(),
                          last_rows.data_ptr())
-        tp, bp = table.token_pool, table.block_pool
-        tw, bw = tp.shape[1], bp.shape[1]
+        pa = table.pool_args
+        if pa is None:
+            tp, bp = table.token_pool, table.block_pool
+            pa = table.pool_args = (tp.shape[1], tp.data_ptr(), bp.shape[1], bp.data_ptr())
+        tw, tpa, bw, bpa = pa
         fn = uploader.inline_addr
         if not fn:
             fn = uploader.inline_addr = _native.address("aia_pack_rows_inline")
         rc = _hostpack.pack_inline(
             upd, fn, sp, tw, bw, _ROW_INTS,
-            tp.data_ptr(), tw, bp.data_ptr(), bw, block_size, bt_width, o[0], o[1], o[2], o[3],
+            tpa, tw, bpa, bw, block_size, bt_width, o[0], o[1], o[2], o[3],
             o[4], o[5], o[6], sample_rows.data_ptr() if sample_rows is not None else 0,
             sample_count, cap)
         if rc != _INLINE_TOO_LARGE:

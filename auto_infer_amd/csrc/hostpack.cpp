@@ -113,6 +113,10 @@ PyObject* build_rows(PyObject*, PyObject* args) {
 
   Ref cu(PyList_New(0)), kv(PyList_New(0)), sample(PyDict_New()), splice(PyList_New(0));
   if (!cu || !kv || !sample || !splice) return nullptr;
+  // get_request: the plan's lookup, or its request mapping itself (a plan
+  // whose get_request is a plain mapping lookup, as BatchPlan's is), which
+  // saves a Python call per request
+  const bool by_map = !PyCallable_Check(get_request);
   Ref seq(PySequence_Fast(scheduled, "scheduled must be a sequence"));
   if (!seq) return nullptr;
   const Py_ssize_t count = PySequence_Fast_GET_SIZE(seq.get());
@@ -125,7 +129,8 @@ PyObject* build_rows(PyObject*, PyObject* args) {
     PyObject* sr = items[r];
     Ref rid(PyObject_GetAttr(sr, s_rid));
     if (!rid) return nullptr;
-    Ref req(PyObject_CallOneArg(get_request, rid.get()));
+    Ref req(by_map ? PyObject_GetItem(get_request, rid.get())
+                   : PyObject_CallOneArg(get_request, rid.get()));
     if (!req) return nullptr;
     const long long n = attr_ll(sr, s_n, &err);
     const long long start = attr_ll(req.get(), s_ncomp, &err);

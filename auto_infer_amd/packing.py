@@ -21,9 +21,11 @@ contents changed since the last stage, times the row width); what this
 design actually uploads (new block ids only) is counted by the shared
 ``DeviceRequestTable.uploaded_block_rows`` / ``uploaded_block_elements``.
 """
+import types
 from dataclasses import dataclass
 
 import numpy as np
+
 import torch
 
 from auto_infer_amd import _native
@@ -40,6 +42,7 @@ _HIP_ERROR = -1000      # _hostpack.upload_pack: statuses at or below are HIP ru
 # the current stream's raw handle without building a Stream object (about 2 us
 # less per step than torch.cuda.current_stream); the public call where absent
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_PLAIN_MAPPINGS = (types.MappingProxyType, dict)
 
 
 class DeviceRequestTable:
@@ -450,8 +453,13 @@ class DeviceBatchPacker:
         upd = table.begin_step()
         scheduled = plan.scheduled
         if _hostpack is not None:     # builds the live set itself, only if a slot is needed
+            # a BatchPlan's get_request is a lookup in its request mapping
+            # (execution.py:54-55 in the reference): the native loop reads the
+            # mapping directly then
+            reqs = getattr(plan, "requests", None)
+            lookup = reqs if type(reqs) in _PLAIN_MAPPINGS else plan.get_request
             cu, kv, sample_idx, decode_splice, all_decode, qacc, width = _hostpack.build_rows(
-                table, scheduled, plan.get_request, plan.block_tables, bs, upd, None)
+                table, scheduled, lookup, plan.block_tables, bs, upd, None)
         else:
             cu, kv, sample_idx, decode_splice, all_decode, qacc, width = build_rows_py(
                 table, scheduled, plan.get_request, plan.block_tables, bs, upd,

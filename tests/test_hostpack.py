@@ -24,19 +24,22 @@ def upd_state(u):
     return (u.rows, u.tok_slot, u.tok_idx, u.tok_val, u.blk_slot, u.blk_idx, u.blk_val)
 
 
+@pytest.mark.parametrize("by_map", [False, True])
 @pytest.mark.parametrize("lazy_live", [False, True])
 @pytest.mark.parametrize("depth,seed,slots", [(0, 1, 64), (1, 2, 64), (3, 3, 4), (0, 4, 2)])
-def test_native_loop_matches_python(depth, seed, slots, lazy_live):
+def test_native_loop_matches_python(depth, seed, slots, lazy_live, by_map):
     # small tables force LRU slot recycling and pool growth; with lazy_live
     # the native loop builds the step's request-id set itself when a slot
-    # is needed
+    # is needed; with by_map it reads the plan's request mapping instead of
+    # calling get_request (what DeviceBatchPacker.build passes for a BatchPlan)
     tn = packing.DeviceRequestTable("cpu", max_slots=slots, max_blocks=2, max_len=8)
     tp = packing.DeviceRequestTable("cpu", max_slots=slots, max_blocks=2, max_len=8)
     steps = 0
     for plan in simulate(50, seed=seed, block_size=16, draft_depth=depth):
         live = {sr.request_id for sr in plan.scheduled}
         un, up = tn.begin_step(), tp.begin_step()
-        rn = packing._hostpack.build_rows(tn, plan.scheduled, plan.get_request,
+        lookup = plan.requests if by_map else plan.get_request
+        rn = packing._hostpack.build_rows(tn, plan.scheduled, lookup,
                                           plan.block_tables, 16, un, None if lazy_live else live)
         rp = packing.build_rows_py(tp, plan.scheduled, plan.get_request, plan.block_tables, 16,
                                    up, live)

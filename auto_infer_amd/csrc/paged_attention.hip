@@ -2384,17 +2384,7 @@ __global__ __launch_bounds__(64 * kMergeGroups) void merge_kernel(MergeArgs a) {
 #pragma unroll
     for (int i = 0; i < kMergeDims / 4; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     float mx = -1e30f, ls = 0.f;
-    auto fold = [&](float2 ml, const float4 (&x)[kMergeDims / 4]) {
-      const float mn = fmaxf(mx, ml.x);
-      const float sa = __builtin_amdgcn_exp2f(mx - mn), sb = __builtin_amdgcn_exp2f(ml.x - mn);
-      ls = ls * sa + ml.y * sb;
-#pragma unroll
-      for (int i = 0; i < kMergeDims / 4; ++i) {
-        acc[i].x = acc[i].x * sa + x[i].x * sb; acc[i].y = acc[i].y * sa + x[i].y * sb;
-        acc[i].z = acc[i].z * sa + x[i].z * sb; acc[i].w = acc[i].w * sa + x[i].w * sb;
-      }
-      mx = mn;
-    };
+    auto fold = [&](float2 ml, const float4 (&x)[kMergeDims / 4]) { fold_into(mx, ls, acc, ml, x); };
     if (live) {    // fp16 partials y = O / c, with (m + log2 c, l / c)
 #pragma unroll 2
       for (int k = kg * ng + pg; k < np; k += kMergeGroups * ng) {
@@ -2402,15 +2392,8 @@ __global__ __launch_bounds__(64 * kMergeGroups) void merge_kernel(MergeArgs a) {
         const float2 ml = a.part_ml[pr];
         const uint4* src = reinterpret_cast<const uint4*>(
             a.part_o + pr * a.dv + c);
-        const uint4 h0 = src[0], h1 = src[1];
-        const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
         float4 x[kMergeDims / 4];
-#pragma unroll
-        for (int i = 0; i < kMergeDims / 4; ++i) {
-          const half2_t a2 = __builtin_bit_cast(half2_t, hw[2 * i]);
-          const half2_t b2 = __builtin_bit_cast(half2_t, hw[2 * i + 1]);
-          x[i] = make_float4((float)a2[0], (float)a2[1], (float)b2[0], (float)b2[1]);
-        }
+        unpack16(src[0], src[1], x);
         fold(ml, x);
       }
     }

@@ -85,6 +85,10 @@ def test_argument_validation_of_the_fused_kernels_without_gpu():
                                      vp(16), 2048, 128, None, None, 0, 0, 0, 0, vp(16), 1 << 20,
                                      None)
     assert rc == _native.AIA_ERR_INVALID and "int32 slot range" in _native.last_error()
+    rc = lib.aia_paged_attention_mla(vp(16), 16 * 576, 576, vp(16), vp(16), 16, vp(16), vp(16),
+                                     1, 1, 16, 512, 64, 256, 1 << 23, ctypes.c_float(0.1),
+                                     vp(16), 16 * 512, 512, 0, 0, vp(256), 1 << 20, None)
+    assert rc == _native.AIA_ERR_INVALID and "int32 slot range" in _native.last_error()
     # the workspace must be 256-byte aligned
     rc = lib.aia_attn_plan(vp(256), vp(256), vp(256), 16, 16, 1, 1, 16, 8, 128, 0, vp(256 + 16),
                            1 << 30, None)

@@ -201,6 +201,10 @@ int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 // Both planners decide it the same way, from the slot capacity the host
 // passes (fix_cap, 0 outside the geometry) and the ranges.
 constexpr int kFixParts = 32;
+#ifndef AIA_FIX_WAVES
+#define AIA_FIX_WAVES 2
+#endif
+constexpr int kFixWaves = AIA_FIX_WAVES;   // waves of a fixed-slot merge work-group
 constexpr int kSmallPlanSegs = 64;
 
 // The geometry of small steps: GQA without prefill routing, at most 64
@@ -2186,8 +2190,9 @@ struct MergeArgs {
 template <int kMergeGroups, int FIXL>
 __global__ __launch_bounds__(64 * kMergeGroups) void merge_kernel(MergeArgs a) {
   constexpr int kMergeThreads = 64 * kMergeGroups;
-  __shared__ float4 sacc[kMergeGroups - 1][kMergeDims / 4][64];
-  __shared__ float2 sml[kMergeGroups - 1][64];
+  constexpr int kLdsGroups = kMergeGroups > 1 ? kMergeGroups - 1 : 1;
+  __shared__ float4 sacc[kLdsGroups][kMergeDims / 4][64];
+  __shared__ float2 sml[kLdsGroups][64];
   const int lane = threadIdx.x & 63, kg = threadIdx.x >> 6;
   const int epr = a.dv / kMergeDims;                      // elements per row
   const int seg_rows = kRows * a.rb;
@@ -3159,7 +3164,8 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
   // Fixed-slot merges for small steps (kFixParts): one work-group per
   // (segment, kv head) when a segment's row span holds at most 16 elements
   // (rows x dv / 16, rows bounded by the query tokens a request can hold),
-  // each thread loading kFixParts / (4 waves) slots.  (configs[3]'s verify
+  // each thread of its kFixWaves waves loading kFixParts / (4 kFixWaves)
+  // slots.  (configs[3]'s verify
   // segments, 64-128 elements, keep the records: in passes of 16 elements
   // the call went 40.6 -> 54 us, and with one wave per 16 elements and 8 slot
   // loads per thread 40.6 -> 42 us, config 1 then 21.9 -> 22.75.)
@@ -3174,14 +3180,14 @@ int launch_merge(char* ws, const Layout& L, const Geometry& g, int32_t nw, int32
       mgrid = L.seg_cap * nw;
     }
   }
-  const int fl = mg.fixed_slots ? kFixParts / (4 * (threads / 64)) : 0;   // slot loads per thread
-  if (wide) {
-    if (fl == 1) merge_kernel<8, 1><<<(unsigned)mgrid, threads, 0, s>>>(mg);
-    else merge_kernel<8, 0><<<(unsigned)mgrid, threads, 0, s>>>(mg);
-  } else {
-    if (fl == 2) merge_kernel<4, 2><<<(unsigned)mgrid, threads, 0, s>>>(mg);
-    else merge_kernel<4, 0><<<(unsigned)mgrid, threads, 0, s>>>(mg);
+  if (mg.fixed_slots && !wide) {
+    // kFixWaves waves of kFixParts / (4 kFixWaves) slot loads per thread (config 1,
+    // us per layer: 2 waves 21.62-21.66, 1 wave 21.87-21.91, 4 waves 21.86-21.89)
+    merge_kernel<kFixWaves, kFixParts / (4 * kFixWaves)><<<(unsigned)mgrid, 64 * kFixWaves, 0, s>>>(mg);
+    return aia::check_hip(hipGetLastError(), "merge_kernel launch");
   }
+  if (wide) merge_kernel<8, 0><<<(unsigned)mgrid, threads, 0, s>>>(mg);
+  else merge_kernel<4, 0><<<(unsigned)mgrid, threads, 0, s>>>(mg);
   return aia::check_hip(hipGetLastError(), "merge_kernel launch");
 }
 
